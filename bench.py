@@ -1,0 +1,228 @@
+"""Benchmark of the MI355X attention hot path.
+
+Headline (one JSON line): config 2 of the north star -- LLaMA-2-style GQA causal
+prefill, f32, B=4, Hq=32, Hkv=8, T=2048, d=128, Q/K/V ~ N(0,1) with a per-
+position scale U[0.5, 1.5] on Q and K (seeded, synthetic).  A step is one
+prefill forward over the whole batch with inputs resident in HBM; value is
+attention TFLOP/s (2 FLOP per multiply-add of QK^T and PV over the T(T+1)/2
+unmasked pairs per head).  The same line carries:
+  * roofline -- the prefill kernel's average launch time from HIP events on
+    the launch stream, against MI355X's fp32 matrix peak (157.3 TFLOP/s);
+  * decode   -- config 3: 64 single-token decode steps (append + attend) over
+    a ragged KV cache, B=32, Hq=32, Hkv=8, d=128, L0 ~ U[512, 4096], as KV-read
+    GB/s against HBM peak (8 TB/s);
+  * cpu_baseline -- the CPU restatement of the reference's GQA attention path
+    (oracle/oracle.c, a "port"), timed on this host's cores on a bounded sample
+    of the same workload.
+
+    python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-cpu] [--all]
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+
+PEAK_FP32_MATRIX_TFLOPS = 157.3
+PEAK_HBM_GBS = 8000.0
+
+
+def load_pkg():
+    sys.path.insert(0, os.path.join(ROOT, "tests"))
+    import nne_testlib
+    return nne_testlib.load_package()
+
+
+def causal_flops(b, hq, t, d):
+    return 4.0 * b * hq * d * t * (t + 1) / 2.0
+
+
+def full_flops(b, hq, tq, tk, d):
+    return 4.0 * b * hq * d * tq * tk
+
+
+def config2_inputs(torch, dev, b=4, hq=32, hkv=8, t=2048, d=128, seed=0x5EED0002):
+    g = torch.Generator(device=dev).manual_seed(seed)
+    s = torch.rand(t, generator=g, device=dev) + 0.5
+    q = torch.randn(b, hq, t, d, generator=g, device=dev) * s[None, None, :, None]
+    k = torch.randn(b, hkv, t, d, generator=g, device=dev) * s[None, None, :, None]
+    v = torch.randn(b, hkv, t, d, generator=g, device=dev)
+    return q, k, v
+
+
+def time_prefill(nne, torch, q, k, v, causal, steps, warmup, out, q_offset=0):
+    for _ in range(warmup):
+        nne.attention_forward(q, k, v, causal, q_offset=q_offset, out=out)
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    ev0 = torch.cuda.Event(enable_timing=True)
+    ev1 = torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    ev0.record(stream)
+    for _ in range(steps):
+        nne.attention_forward(q, k, v, causal, q_offset=q_offset, out=out)
+    ev1.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    kernel_ms = ev0.elapsed_time(ev1) / steps
+    return wall * 1e3 / steps, kernel_ms
+
+
+def bench_decode(nne, torch, dev, steps=64, warmup=4, seed=0x5EED0003):
+    """Config 3: B=32, Hq=32, Hkv=8, d=128, ragged lengths, 64 append+attend steps."""
+    import numpy as np
+    b, hq, hkv, d = 32, 32, 8, 128
+    rng = np.random.default_rng(seed)
+    lens0 = rng.integers(512, 4097, size=b).astype(np.int32)
+    cap = 4096 + steps + warmup
+    cache = nne.KVCache(1, b, hkv, cap, d, device=dev)
+    g = torch.Generator(device=dev).manual_seed(seed)
+    cache.k[0].normal_(generator=g)
+    cache.v[0].normal_(generator=g)
+    qs = torch.randn(steps, b, hq, 1, d, generator=g, device=dev)
+    kn = torch.randn(steps, b, hkv, 1, d, generator=g, device=dev)
+    vn = torch.randn(steps, b, hkv, 1, d, generator=g, device=dev)
+    out = torch.empty(b, hq, 1, d, device=dev)
+    cache.set_lengths(0, lens0)
+    for i in range(warmup):
+        cache.decode_step(0, qs[i], kn[i], vn[i], out=out)
+    cache.set_lengths(0, lens0)
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    ev0 = torch.cuda.Event(enable_timing=True)
+    ev1 = torch.cuda.Event(enable_timing=True)
+    ev0.record(stream)
+    for i in range(steps):
+        cache.decode_step(0, qs[i], kn[i], vn[i], out=out)
+    ev1.record(stream)
+    torch.cuda.synchronize()
+    ms = ev0.elapsed_time(ev1)
+    # K+V rows read once per KV head (GQA-shared) after each step's append,
+    # plus q/o and the appended rows.
+    total = 0.0
+    for i in range(steps):
+        total += float((lens0 + i + 1).sum()) * hkv * d * 4 * 2
+        total += 2 * b * hq * d * 4 + b * hkv * d * 4 * 2
+    gbs = total / (ms / 1e3) / 1e9
+    return {"metric": "decode KV-read GB/s", "value": round(gbs, 1), "unit": "GB/s",
+            "steps": steps, "ms_per_step": round(ms / steps, 4),
+            "bytes_per_step": round(total / steps),
+            "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS,
+                         "unit": "GB/s", "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": None},
+            "config": {"workload": "config3: decode B=32 Hq=32 Hkv=8 d=128 "
+                                   "L0~U[512,4096] ragged, 64 steps append+attend, f32"}}
+
+
+def cpu_baseline(target_seconds=15.0):
+    """Oracle (CPU restatement of llama.rs:253-296) on a bounded sample of config 2."""
+    import numpy as np
+    sys.path.insert(0, os.path.join(ROOT, "tests"))
+    import nne_testlib as T
+    threads = min(16, os.cpu_count() or 1)
+    t, d, hkv_s = 2048, 128, 1
+    rng = np.random.default_rng(0x5EED0002)
+    s = rng.uniform(0.5, 1.5, size=t).astype(np.float32)
+    # one batch element, growing numbers of query heads sharing one KV head
+    k = rng.standard_normal((1, hkv_s, t, d)).astype(np.float32) * s[None, None, :, None]
+    v = rng.standard_normal((1, hkv_s, t, d)).astype(np.float32)
+    heads = threads
+    while True:
+        q = rng.standard_normal((1, heads, t, d)).astype(np.float32) * s[None, None, :, None]
+        t0 = time.perf_counter()
+        T.ref_standard(q, k, v, masked=True, threads=threads)
+        el = time.perf_counter() - t0
+        if el >= target_seconds / 4 or heads >= 128:
+            break
+        heads *= 2
+    flops = causal_flops(1, heads, t, d)
+    return {"value": round(flops / el / 1e12, 6), "unit": "TFLOP/s", "cores": threads,
+            "kind": "port",
+            "sample": "config 2 GQA causal prefill restated from llama.rs:253-296 "
+                      "(repeat-KV, -1e4 mask, softmax, PV; f32), B=1, %d query heads on one "
+                      "KV head, T=2048, d=128; %.2f s wall; FLOPs counted like the GPU "
+                      "(unmasked pairs only)" % (heads, el)}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-decode", action="store_true")
+    ap.add_argument("--all", action="store_true", help="also print lines for configs 1, 4, 5")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print("bench.py measures one GPU only: this build has no multi-GPU path "
+              "(every box has one MI355X); run with --gpus 1", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    nne = load_pkg()
+    nne.lib()
+    dev = torch.device("cuda:0")
+
+    b, hq, hkv, t, d = 4, 32, 8, 2048, 128
+    q, k, v = config2_inputs(torch, dev)
+    out = torch.empty_like(q)
+    print("bench: config2 prefill steps=%d warmup=%d" % (args.steps, args.warmup),
+          file=sys.stderr, flush=True)
+    ms, kms = time_prefill(nne, torch, q, k, v, True, args.steps, args.warmup, out)
+    flops = causal_flops(b, hq, t, d)
+    value = flops / (ms / 1e3) / 1e12
+    achieved = flops / (kms / 1e3) / 1e12
+    line = {
+        "metric": "prefill attn TFLOP/s + decode KV-read GB/s on 1 MI355X, vs host-CPU Rayon",
+        "value": round(value, 3), "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(ms, 4), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "f32", "data": "synthetic",
+        "config": {"workload": "config2: GQA causal prefill B=4 Hq=32 Hkv=8 T=2048 d=128 f32, "
+                               "Q/K/V~N(0,1), per-position scale U[0.5,1.5] on Q,K",
+                   "global_batch": b, "seq_len": t, "parallelism": "none (1 GPU)"},
+        "roofline": {"bound": "mfma", "achieved": round(achieved, 3),
+                     "peak": PEAK_FP32_MATRIX_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(achieved / PEAK_FP32_MATRIX_TFLOPS, 4), "traffic": None,
+                     "kernel": "prefill_mfma_kernel<128,causal,vec>",
+                     "kernel_ms": round(kms, 4)},
+    }
+    del q, k, v, out
+    if not args.no_decode:
+        print("bench: config3 decode", file=sys.stderr, flush=True)
+        line["decode"] = bench_decode(nne, torch, dev)
+    if args.all:
+        extra = []
+        g = torch.Generator(device=dev).manual_seed(0x5EED0001)
+        for name, (bb, h, tt, dd, causal, std) in {
+            "config1": (1, 4, 256, 64, True, 1.0),
+            "config4": (1, 16, 16384, 64, True, 0.5),
+            "config5a": (8, 20, 1500, 64, False, 1.0),
+        }.items():
+            q = torch.randn(bb, h, tt, dd, generator=g, device=dev) * std
+            k = torch.randn(bb, h, tt, dd, generator=g, device=dev) * std
+            v = torch.randn(bb, h, tt, dd, generator=g, device=dev) * std
+            o = torch.empty_like(q)
+            ms_c, kms_c = time_prefill(nne, torch, q, k, v, causal, max(3, args.steps // 2), 2, o)
+            fl = causal_flops(bb, h, tt, dd) if causal else full_flops(bb, h, tt, tt, dd)
+            extra.append({"workload": name, "TFLOP/s": round(fl / (kms_c / 1e3) / 1e12, 3),
+                          "kernel_ms": round(kms_c, 4),
+                          "frac": round(fl / (kms_c / 1e3) / 1e12 / PEAK_FP32_MATRIX_TFLOPS, 4)})
+            if name == "config5a":
+                qx = torch.randn(8, 20, 8, 64, generator=g, device=dev)
+                ox = torch.empty_like(qx)
+                ms_x, kms_x = time_prefill(nne, torch, qx, k, v, False, 20, 3, ox)
+                by = (2 * 8 * 20 * 1500 * 64 + 2 * 8 * 20 * 8 * 64) * 4
+                extra.append({"workload": "config5b cross 8q->1500", "GB/s":
+                              round(by / (kms_x / 1e3) / 1e9, 1), "kernel_ms": round(kms_x, 4),
+                              "note": "K/V (123 MB) fits the 256 MB MALL: cache-warm figure"})
+            del q, k, v, o
+        line["other_configs"] = extra
+    if not args.no_cpu:
+        print("bench: cpu baseline", file=sys.stderr, flush=True)
+        line["cpu_baseline"] = cpu_baseline()
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

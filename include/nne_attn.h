@@ -1,0 +1,129 @@
+/*
+ * nne_attn.h -- C ABI of the MI355X (gfx950) attention hot path.
+ *
+ * Drop-in boundary for elvin-mark/neural-network-engine's attention forward:
+ * the Rust side keeps its Tensor / FlashAttention / KVCache API and calls these
+ * functions through a thin `extern "C"` crate.  Plain pointers and sizes only:
+ * every tensor argument is a DEVICE pointer to f32 data plus a 4-D shape and
+ * element strides ([batch, head, row, dim]); a NULL strides pointer means
+ * row-major contiguous.  `stream` is a hipStream_t (NULL = default stream).
+ * Calls enqueue work and return without synchronising.
+ *
+ * Return value: NNE_OK or an error code that maps onto the reference's
+ * EngineError (src/error.rs:6-58); nne_last_error() returns the message of the
+ * calling thread's last failure.  No call aborts the process.
+ */
+#ifndef NNE_ATTN_H
+#define NNE_ATTN_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum {
+    NNE_OK = 0,
+    NNE_EINVAL = 1,    /* EngineError::InvalidArgument   (src/error.rs:42) */
+    NNE_ESHAPE = 2,    /* EngineError::ShapeMismatch     (src/error.rs:12) */
+    NNE_ECAPACITY = 3, /* KV cache append past capacity -> EngineError::GpuError */
+    NNE_EHIP = 4       /* HIP runtime failure            -> EngineError::GpuError (src/error.rs:48) */
+};
+
+#define NNE_ABI_VERSION 1
+
+int nne_abi_version(void);
+
+/* Message for the calling thread's last non-OK return (empty if none). */
+const char *nne_last_error(void);
+
+/* ---- device memory owned by the caller (the Rust side) -------------------
+ * The reference keeps tensors in host Vec<f32> storage (src/tensor/storage.rs:84-163);
+ * on the GPU path the caller allocates and frees device buffers with these. */
+int nne_dev_alloc(void **ptr, uint64_t bytes);
+int nne_dev_free(void *ptr);
+int nne_memcpy_h2d(void *dst, const void *src, uint64_t bytes, void *stream);
+int nne_memcpy_d2h(void *dst, const void *src, uint64_t bytes, void *stream);
+int nne_memcpy_d2d(void *dst, const void *src, uint64_t bytes, void *stream);
+int nne_stream_sync(void *stream);
+
+/* ---- prefill -------------------------------------------------------------
+ * Replaces `flash_attention_forward(q, k, v, is_causal, scale, block_size_r,
+ * block_size_c) -> Result<RawTensor>` (src/nn/flash_attention.rs:19-199).
+ * Same checks and error classes as the reference: K and V must match Q in
+ * batch, heads and head dim and each other in length (:43-48, NNE_ESHAPE);
+ * has_scale = 0 means scale = 1/sqrt(d) (:50); block sizes are accepted and
+ * only validated (they change the reference's rounding order, not the result).
+ * Causal masking is top-left: key c is visible to query row r iff c <= r
+ * (:113).  Rows that see no key are zero (:186-194).  `o` has Q's shape. */
+int nne_flash_attention_forward(const float *q, const int64_t q_shape[4], const int64_t q_strides[4],
+                                const float *k, const int64_t k_shape[4], const int64_t k_strides[4],
+                                const float *v, const int64_t v_shape[4], const int64_t v_strides[4],
+                                float *o, const int64_t o_strides[4], int is_causal, int has_scale,
+                                float scale, int64_t block_size_r, int64_t block_size_c, void *stream);
+
+/* Grouped-query / offset generalisation of the same forward, for the
+ * reference's standard attention paths: GroupedQueryAttention::forward_gqa_cached
+ * (src/models/llama.rs:253-296), MultiHeadAttention::forward_attention_cached
+ * (src/nn/attention.rs:93-122) and forward_cross_attention_cached
+ * (src/nn/attention.rs:193-203).  k_shape[1] must divide q_shape[1]; query
+ * head hq reads KV head hq / (Hq / Hkv) (llama.rs:256-266).  With is_causal,
+ * key c is visible to row r iff c <= r + q_offset (llama.rs uses
+ * q_offset = start_pos, attention.rs uses Tk - Tq).  The reference's additive
+ * -1e4 mask and this exact exclusion give identical f32 results whenever
+ * |scores| < ~4e3.  Few-query problems (Hq/Hkv * Tq <= 16 rows per KV head
+ * with every key visible) run on the split-K kernel. */
+int nne_attention_forward(const float *q, const int64_t q_shape[4], const int64_t q_strides[4],
+                          const float *k, const int64_t k_shape[4], const int64_t k_strides[4],
+                          const float *v, const int64_t v_shape[4], const int64_t v_strides[4],
+                          float *o, const int64_t o_strides[4], int is_causal, int64_t q_offset,
+                          int has_scale, float scale, void *stream);
+
+/* ---- KV cache ------------------------------------------------------------
+ * Replaces KVCache (src/nn/kv_cache.rs:11-74) and the per-layer
+ * (Tensor, Tensor) slots models append to with Tensor::cat (llama.rs:239-251,
+ * attention.rs:79-91).  Storage per layer: K and V device buffers laid out
+ * [B][Hkv][capacity][d] (head-major, contiguous, d % 4 == 0), plus the
+ * sequence lengths kept twice: lens_dev (int32[B], device, read by kernels)
+ * and lens_host (int32[B], host, used for validation and launch sizing).
+ * Functions that append update both. */
+
+/* Appends k_new / v_new ([B, Hkv, t_new, d], any strides) at row lens[b] of
+ * every (b, kv head) in place -- the KVCache::update of kv_cache.rs:49-74
+ * without the O(L) copy.  NNE_ECAPACITY (nothing written) if some
+ * lens_host[b] + t_new > capacity. */
+int nne_kv_append(float *k_cache, float *v_cache, int32_t *lens_dev, int32_t *lens_host,
+                  const float *k_new, const int64_t k_new_strides[4], const float *v_new,
+                  const int64_t v_new_strides[4], int64_t B, int64_t Hkv, int64_t capacity,
+                  int64_t d, int64_t t_new, void *stream);
+
+/* Device workspace bytes needed by nne_decode_attention / nne_decode_step for
+ * sequences up to max_len keys (0 means none is needed). */
+uint64_t nne_decode_workspace_bytes(int64_t B, int64_t Hq, int64_t Hkv, int64_t d, int64_t max_len);
+
+/* Single-token decode attention over the cache: q [B, Hq, 1, d] attends to
+ * the first lens[b] rows of its sequence, no mask (llama.rs:239-296 with
+ * t = 1).  Ragged lengths are allowed.  workspace may be NULL (the library
+ * then allocates stream-ordered scratch) or a device buffer of at least
+ * nne_decode_workspace_bytes(B, Hq, Hkv, d, max(lens_host)) bytes. */
+int nne_decode_attention(const float *q, const int64_t q_strides[4], const float *k_cache,
+                         const float *v_cache, const int32_t *lens_dev, const int32_t *lens_host,
+                         float *o, const int64_t o_strides[4], int64_t B, int64_t Hq, int64_t Hkv,
+                         int64_t capacity, int64_t d, int has_scale, float scale, void *workspace,
+                         uint64_t workspace_bytes, void *stream);
+
+/* One decode step: nne_kv_append of one row, then nne_decode_attention --
+ * the append-then-attend order of llama.rs:239-296 and attention.rs:79-122. */
+int nne_decode_step(const float *q, const int64_t q_strides[4], float *k_cache, float *v_cache,
+                    int32_t *lens_dev, int32_t *lens_host, const float *k_new,
+                    const int64_t k_new_strides[4], const float *v_new,
+                    const int64_t v_new_strides[4], float *o, const int64_t o_strides[4],
+                    int64_t B, int64_t Hq, int64_t Hkv, int64_t capacity, int64_t d,
+                    int has_scale, float scale, void *workspace, uint64_t workspace_bytes,
+                    void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* NNE_ATTN_H */

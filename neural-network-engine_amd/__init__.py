@@ -1,0 +1,340 @@
+"""Python host mirror of the MI355X attention hot path.
+
+Binds the C ABI of lib/libnne_attn.so (declared in include/nne_attn.h) with
+ctypes and exposes it with the names and argument meanings of the reference
+engine's attention API (elvin-mark/neural-network-engine):
+
+* ``flash_attention_forward(q, k, v, is_causal, scale, block_size_r,
+  block_size_c)``  -- src/nn/flash_attention.rs:19-199
+* ``attention_forward(q, k, v, is_causal, q_offset, scale)`` -- the GQA /
+  offset generalisation behind GroupedQueryAttention (src/models/llama.rs:253-296)
+  and MultiHeadAttention (src/nn/attention.rs:51-210)
+* ``KVCache`` -- src/nn/kv_cache.rs:11-74, stored on the device head-major
+  and appended in place
+* ``FlashAttention`` layer -- src/nn/flash_attention.rs:202-292
+
+Tensors are torch tensors on the GPU (torch is used only for device memory and
+streams).  Errors raise the EngineError variant the reference would return.
+There is no CPU path: if the HIP library is missing, importing works but every
+call raises.
+"""
+import ctypes
+import math
+import os
+
+import numpy as np
+
+_PKG = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_PKG, "lib", "libnne_attn.so")
+
+NNE_OK, NNE_EINVAL, NNE_ESHAPE, NNE_ECAPACITY, NNE_EHIP = 0, 1, 2, 3, 4
+
+
+class EngineError(RuntimeError):
+    """Base of the reference's error enum (src/error.rs:9-52)."""
+
+
+class InvalidArgument(EngineError):
+    pass
+
+
+class ShapeMismatch(EngineError):
+    pass
+
+
+class GpuError(EngineError):
+    pass
+
+
+class CapacityError(GpuError):
+    pass
+
+
+_ERRORS = {NNE_EINVAL: InvalidArgument, NNE_ESHAPE: ShapeMismatch,
+           NNE_ECAPACITY: CapacityError, NNE_EHIP: GpuError}
+
+_lib = None
+
+_i64p = ctypes.POINTER(ctypes.c_int64)
+_i32p = ctypes.POINTER(ctypes.c_int32)
+_vp = ctypes.c_void_p
+
+# exported symbol -> (restype, argtypes); mirrors include/nne_attn.h
+SIGNATURES = {
+    "nne_abi_version": (ctypes.c_int, []),
+    "nne_last_error": (ctypes.c_char_p, []),
+    "nne_dev_alloc": (ctypes.c_int, [ctypes.POINTER(ctypes.c_void_p), ctypes.c_uint64]),
+    "nne_dev_free": (ctypes.c_int, [_vp]),
+    "nne_memcpy_h2d": (ctypes.c_int, [_vp, _vp, ctypes.c_uint64, _vp]),
+    "nne_memcpy_d2h": (ctypes.c_int, [_vp, _vp, ctypes.c_uint64, _vp]),
+    "nne_memcpy_d2d": (ctypes.c_int, [_vp, _vp, ctypes.c_uint64, _vp]),
+    "nne_stream_sync": (ctypes.c_int, [_vp]),
+    "nne_flash_attention_forward": (ctypes.c_int, [
+        _vp, _i64p, _i64p, _vp, _i64p, _i64p, _vp, _i64p, _i64p, _vp, _i64p,
+        ctypes.c_int, ctypes.c_int, ctypes.c_float, ctypes.c_int64, ctypes.c_int64, _vp]),
+    "nne_attention_forward": (ctypes.c_int, [
+        _vp, _i64p, _i64p, _vp, _i64p, _i64p, _vp, _i64p, _i64p, _vp, _i64p,
+        ctypes.c_int, ctypes.c_int64, ctypes.c_int, ctypes.c_float, _vp]),
+    "nne_kv_append": (ctypes.c_int, [
+        _vp, _vp, _vp, _i32p, _vp, _i64p, _vp, _i64p, ctypes.c_int64, ctypes.c_int64,
+        ctypes.c_int64, ctypes.c_int64, ctypes.c_int64, _vp]),
+    "nne_decode_workspace_bytes": (ctypes.c_uint64, [
+        ctypes.c_int64, ctypes.c_int64, ctypes.c_int64, ctypes.c_int64, ctypes.c_int64]),
+    "nne_decode_attention": (ctypes.c_int, [
+        _vp, _i64p, _vp, _vp, _vp, _i32p, _vp, _i64p, ctypes.c_int64, ctypes.c_int64,
+        ctypes.c_int64, ctypes.c_int64, ctypes.c_int64, ctypes.c_int, ctypes.c_float, _vp,
+        ctypes.c_uint64, _vp]),
+    "nne_decode_step": (ctypes.c_int, [
+        _vp, _i64p, _vp, _vp, _vp, _i32p, _vp, _i64p, _vp, _i64p, _vp, _i64p,
+        ctypes.c_int64, ctypes.c_int64, ctypes.c_int64, ctypes.c_int64, ctypes.c_int64,
+        ctypes.c_int, ctypes.c_float, _vp, ctypes.c_uint64, _vp]),
+}
+
+
+def lib():
+    """The loaded HIP library; raises if it has not been built."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise GpuError("HIP attention library not built: %s is missing "
+                           "(run neural-network-engine_amd/build.py)" % LIB_PATH)
+        l = ctypes.CDLL(LIB_PATH)
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(l, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = l
+    return _lib
+
+
+def check(rc):
+    if rc != NNE_OK:
+        msg = lib().nne_last_error().decode(errors="replace")
+        raise _ERRORS.get(rc, EngineError)(msg)
+
+
+def _i64(vals):
+    arr = (ctypes.c_int64 * 4)(*[int(x) for x in vals])
+    return arr
+
+
+def _stream(stream=None):
+    import torch
+    s = stream if stream is not None else torch.cuda.current_stream()
+    return ctypes.c_void_p(s.cuda_stream)
+
+
+def _require_f32_cuda(*ts):
+    import torch
+    for t in ts:
+        if not t.is_cuda or t.dtype != torch.float32:
+            raise InvalidArgument("Invalid configuration or argument: expected float32 GPU tensors")
+
+
+def _shape4(t, what):
+    if t.dim() != 4:
+        raise InvalidArgument(
+            "Invalid configuration or argument: FlashAttention expects 4D tensors "
+            "[Batch, Heads, SeqLen, Dim], got %s:%s" % (what, list(t.shape)))
+    return t.shape, t.stride()
+
+
+def flash_attention_forward(q, k, v, is_causal, scale=None, block_size_r=64, block_size_c=64,
+                            out=None, stream=None):
+    """flash_attention_forward (src/nn/flash_attention.rs:19-199) on the GPU.
+
+    q, k, v: float32 CUDA tensors [B, H, T, d] with any strides.  Returns a new
+    contiguous [B, H, Tq, d] tensor (or fills ``out``)."""
+    import torch
+    qs, qst = _shape4(q, "Q")
+    ks, kst = _shape4(k, "K")
+    vs, vst = _shape4(v, "V")
+    _require_f32_cuda(q, k, v)
+    if out is None:
+        out = torch.empty(tuple(qs), dtype=torch.float32, device=q.device)
+    check(lib().nne_flash_attention_forward(
+        q.data_ptr(), _i64(qs), _i64(qst), k.data_ptr(), _i64(ks), _i64(kst),
+        v.data_ptr(), _i64(vs), _i64(vst), out.data_ptr(), _i64(out.stride()),
+        int(bool(is_causal)), int(scale is not None), float(scale or 0.0),
+        int(block_size_r), int(block_size_c), _stream(stream)))
+    return out
+
+
+def attention_forward(q, k, v, is_causal, q_offset=0, scale=None, out=None, stream=None):
+    """GQA-capable attention: q [B, Hq, Tq, d], k/v [B, Hkv, Tk, d], Hkv | Hq.
+
+    Query head hq reads KV head hq // (Hq // Hkv) (src/models/llama.rs:256-266);
+    with is_causal, key c is visible to row r iff c <= r + q_offset."""
+    import torch
+    qs, qst = _shape4(q, "Q")
+    ks, kst = _shape4(k, "K")
+    vs, vst = _shape4(v, "V")
+    _require_f32_cuda(q, k, v)
+    if out is None:
+        out = torch.empty(tuple(qs), dtype=torch.float32, device=q.device)
+    check(lib().nne_attention_forward(
+        q.data_ptr(), _i64(qs), _i64(qst), k.data_ptr(), _i64(ks), _i64(kst),
+        v.data_ptr(), _i64(vs), _i64(vst), out.data_ptr(), _i64(out.stride()),
+        int(bool(is_causal)), int(q_offset), int(scale is not None), float(scale or 0.0),
+        _stream(stream)))
+    return out
+
+
+class KVCache:
+    """Device-resident KV cache (src/nn/kv_cache.rs:11-74).
+
+    Per layer: K and V buffers [B, Hkv, capacity, d] (head-major, rows appended
+    in place) and per-sequence lengths kept on the device (read by kernels) and
+    on the host (validation, launch sizing).  Sequences may be ragged."""
+
+    def __init__(self, num_layers, batch, num_kv_heads, capacity, head_dim, device="cuda"):
+        import torch
+        self.batch, self.num_kv_heads = int(batch), int(num_kv_heads)
+        self.capacity, self.head_dim = int(capacity), int(head_dim)
+        shape = (self.batch, self.num_kv_heads, self.capacity, self.head_dim)
+        self.k = [torch.zeros(shape, dtype=torch.float32, device=device) for _ in range(num_layers)]
+        self.v = [torch.zeros(shape, dtype=torch.float32, device=device) for _ in range(num_layers)]
+        self.lens_dev = [torch.zeros(self.batch, dtype=torch.int32, device=device)
+                         for _ in range(num_layers)]
+        self.lens_host = [np.zeros(self.batch, dtype=np.int32) for _ in range(num_layers)]
+        self._ws = None
+
+    # kv_cache.rs:25-29
+    def reset(self):
+        for i in range(self.num_layers()):
+            self.lens_dev[i].zero_()
+            self.lens_host[i][:] = 0
+
+    # kv_cache.rs:32-34
+    def num_layers(self):
+        return len(self.k)
+
+    # kv_cache.rs:37-44 (0 for an out-of-range layer; with ragged sequences the
+    # longest one)
+    def current_seq_len(self, layer_idx):
+        if layer_idx >= self.num_layers():
+            return 0
+        return int(self.lens_host[layer_idx].max()) if self.batch else 0
+
+    def set_lengths(self, layer_idx, lens):
+        """Declares that rows [0, lens[b]) of each sequence are filled."""
+        import torch
+        lens = np.asarray(lens, dtype=np.int32)
+        if lens.shape != (self.batch,) or (lens < 0).any() or (lens > self.capacity).any():
+            raise InvalidArgument("Invalid configuration or argument: bad lengths")
+        self.lens_host[layer_idx][:] = lens
+        self.lens_dev[layer_idx].copy_(torch.from_numpy(lens))
+
+    def _check_layer(self, layer_idx):
+        if layer_idx >= self.num_layers():
+            raise InvalidArgument(
+                "Invalid configuration or argument: KVCache layer index %d out of range "
+                "(total layers: %d)" % (layer_idx, self.num_layers()))
+
+    # kv_cache.rs:49-74: append along the sequence axis; returns views of all rows
+    def update(self, layer_idx, k_new, v_new, stream=None):
+        self._check_layer(layer_idx)
+        _require_f32_cuda(k_new, v_new)
+        b, h, t, d = k_new.shape
+        if (b, h, d) != (self.batch, self.num_kv_heads, self.head_dim) or v_new.shape != k_new.shape:
+            raise ShapeMismatch("Shape mismatch error: expected shape %s, got %s" % (
+                [self.batch, self.num_kv_heads, t, self.head_dim], list(k_new.shape)))
+        lh = self.lens_host[layer_idx]
+        check(lib().nne_kv_append(
+            self.k[layer_idx].data_ptr(), self.v[layer_idx].data_ptr(),
+            self.lens_dev[layer_idx].data_ptr(), lh.ctypes.data_as(_i32p),
+            k_new.data_ptr(), _i64(k_new.stride()), v_new.data_ptr(), _i64(v_new.stride()),
+            self.batch, self.num_kv_heads, self.capacity, self.head_dim, t, _stream(stream)))
+        L = int(lh.max()) if self.batch else 0
+        return self.k[layer_idx][:, :, :L], self.v[layer_idx][:, :, :L]
+
+    def workspace(self, num_heads):
+        import torch
+        need = lib().nne_decode_workspace_bytes(self.batch, num_heads, self.num_kv_heads,
+                                                self.head_dim, self.capacity)
+        if need and (self._ws is None or self._ws.numel() < need):
+            self._ws = torch.empty(int(need), dtype=torch.uint8, device=self.k[0].device)
+        return self._ws
+
+    def attend(self, layer_idx, q, out=None, scale=None, stream=None):
+        """Decode attention of q [B, Hq, 1, d] over the cached rows."""
+        import torch
+        self._check_layer(layer_idx)
+        _require_f32_cuda(q)
+        hq = q.shape[1]
+        if out is None:
+            out = torch.empty(q.shape, dtype=torch.float32, device=q.device)
+        ws = self.workspace(hq)
+        check(lib().nne_decode_attention(
+            q.data_ptr(), _i64(q.stride()), self.k[layer_idx].data_ptr(),
+            self.v[layer_idx].data_ptr(), self.lens_dev[layer_idx].data_ptr(),
+            self.lens_host[layer_idx].ctypes.data_as(_i32p), out.data_ptr(), _i64(out.stride()),
+            self.batch, hq, self.num_kv_heads, self.capacity, self.head_dim,
+            int(scale is not None), float(scale or 0.0),
+            ws.data_ptr() if ws is not None else None, ws.numel() if ws is not None else 0,
+            _stream(stream)))
+        return out
+
+    def decode_step(self, layer_idx, q, k_new, v_new, out=None, scale=None, stream=None):
+        """Append one row per sequence, then attend (llama.rs:239-296, t = 1)."""
+        import torch
+        self._check_layer(layer_idx)
+        _require_f32_cuda(q, k_new, v_new)
+        hq = q.shape[1]
+        if out is None:
+            out = torch.empty(q.shape, dtype=torch.float32, device=q.device)
+        ws = self.workspace(hq)
+        check(lib().nne_decode_step(
+            q.data_ptr(), _i64(q.stride()), self.k[layer_idx].data_ptr(),
+            self.v[layer_idx].data_ptr(), self.lens_dev[layer_idx].data_ptr(),
+            self.lens_host[layer_idx].ctypes.data_as(_i32p), k_new.data_ptr(),
+            _i64(k_new.stride()), v_new.data_ptr(), _i64(v_new.stride()), out.data_ptr(),
+            _i64(out.stride()), self.batch, hq, self.num_kv_heads, self.capacity, self.head_dim,
+            int(scale is not None), float(scale or 0.0),
+            ws.data_ptr() if ws is not None else None, ws.numel() if ws is not None else 0,
+            _stream(stream)))
+        return out
+
+
+class FlashAttention:
+    """FlashAttention layer (src/nn/flash_attention.rs:202-292), forward only.
+
+    The four d_model x d_model projections are plain GEMMs (torch); the
+    attention core runs on the HIP kernel and reads the projected [B, T, H, d]
+    activations through strides, so no transpose copies are made."""
+
+    def __init__(self, d_model, num_heads, is_causal, device="cuda", seed=0):
+        import torch
+        if d_model % num_heads != 0:
+            raise InvalidArgument("d_model (%d) must be divisible by num_heads (%d)"
+                                  % (d_model, num_heads))
+        self.d_model, self.num_heads = d_model, num_heads
+        self.head_dim = d_model // num_heads
+        self.is_causal = is_causal
+        self.block_size = 64
+        g = torch.Generator(device="cpu").manual_seed(seed)
+        bound = 1.0 / math.sqrt(d_model)
+
+        def lin():
+            w = (torch.rand(d_model, d_model, generator=g) * 2 - 1) * bound
+            b = (torch.rand(d_model, generator=g) * 2 - 1) * bound
+            return w.to(device), b.to(device)
+
+        self.q_proj, self.k_proj, self.v_proj, self.out_proj = lin(), lin(), lin(), lin()
+
+    def forward(self, x):
+        import torch
+        if x.dim() != 3:
+            raise EngineError("Incompatible shapes for operation FlashAttention forward "
+                              "(expected 3D input [B, T, C]): %s" % [list(x.shape)])
+        b, t, _ = x.shape
+        h, d = self.num_heads, self.head_dim
+        q = torch.nn.functional.linear(x, *self.q_proj).view(b, t, h, d).transpose(1, 2)
+        k = torch.nn.functional.linear(x, *self.k_proj).view(b, t, h, d).transpose(1, 2)
+        v = torch.nn.functional.linear(x, *self.v_proj).view(b, t, h, d).transpose(1, 2)
+        out = torch.empty((b, t, h, d), dtype=torch.float32, device=x.device)
+        flash_attention_forward(q, k, v, self.is_causal, None, self.block_size, self.block_size,
+                                out=out.transpose(1, 2))
+        return torch.nn.functional.linear(out.view(b, t, self.d_model), *self.out_proj)
+
+    __call__ = forward

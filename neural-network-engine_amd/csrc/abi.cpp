@@ -1,0 +1,405 @@
+// extern "C" boundary of the attention hot path (declared in include/nne_attn.h).
+//
+// This layer validates shapes the way the reference does, picks the kernel
+// and fills the launch-parameter structs; it never computes attention itself.
+// There is no CPU fallback: every compute entry point either launches a HIP
+// kernel or returns an error.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <string>
+
+#include "nne_attn.h"
+#include "nne_launch.hpp"
+
+namespace {
+
+thread_local std::string g_err;
+
+int fail(int code, const char* fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof(buf), fmt, ap);
+    va_end(ap);
+    g_err = buf;
+    return code;
+}
+
+int hip_fail(hipError_t e, const char* what) {
+    return fail(NNE_EHIP, "GPU compute error: %s: %s", what, hipGetErrorString(e));
+}
+
+inline hipStream_t as_stream(void* s) { return static_cast<hipStream_t>(s); }
+
+void contiguous_strides(const int64_t* shape, int64_t* st) {
+    st[3] = 1;
+    st[2] = shape[3];
+    st[1] = shape[2] * shape[3];
+    st[0] = shape[1] * st[1];
+}
+
+std::string shape_str(const int64_t* s) {
+    char buf[128];
+    snprintf(buf, sizeof(buf), "[%lld, %lld, %lld, %lld]", (long long)s[0], (long long)s[1],
+             (long long)s[2], (long long)s[3]);
+    return buf;
+}
+
+bool dims_ok(const int64_t* s) {
+    for (int i = 0; i < 4; ++i)
+        if (s[i] < 0 || s[i] > INT32_MAX) return false;
+    return true;
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+// 16-byte vector access is valid for this view: unit dim stride and every
+// other stride a multiple of 4 floats, 16-byte aligned base.
+bool vec_view(const void* p, const int64_t* st) {
+    return aligned16(p) && st[3] == 1 && st[0] % 4 == 0 && st[1] % 4 == 0 && st[2] % 4 == 0;
+}
+
+nne::View4 make_view(const float* p, const int64_t* st) {
+    nne::View4 v;
+    v.p = p;
+    v.sb = st[0]; v.sh = st[1]; v.st = st[2]; v.sd = st[3];
+    return v;
+}
+
+nne::OutView4 make_out(float* p, const int64_t* st) {
+    nne::OutView4 v;
+    v.p = p;
+    v.sb = st[0]; v.sh = st[1]; v.st = st[2]; v.sd = st[3];
+    return v;
+}
+
+float softmax_scale(int has_scale, float scale, int64_t d) {
+    // scale.unwrap_or(1.0 / (d as f32).sqrt())  (flash_attention.rs:50, llama.rs:273)
+    return has_scale ? scale : 1.0f / std::sqrt((float)d);
+}
+
+// Shared body of the two prefill entry points.  Shapes were validated.
+int run_attention(const float* q, const int64_t* qs_, const int64_t* qst, const float* k,
+                  const int64_t* ks_, const int64_t* kst, const float* v, const int64_t* vst,
+                  float* o, const int64_t* ost, bool causal, int64_t q_offset, float scale,
+                  hipStream_t stream) {
+    const int B = (int)qs_[0], Hq = (int)qs_[1], Tq = (int)qs_[2], d = (int)qs_[3];
+    const int Hkv = (int)ks_[1], Tk = (int)ks_[2];
+    if ((int64_t)B * Hq * Tq == 0 || d == 0) return NNE_OK;
+    if (nne::prefill_padded_dim(d) == 0)
+        return fail(NNE_EINVAL, "Invalid configuration or argument: head dim %d > 128 is not "
+                                "supported by the gfx950 attention kernels", d);
+    // Offsets beyond +-2^30 cannot change visibility for int32 lengths.
+    const int qoff = (int)std::max<int64_t>(-(1 << 30), std::min<int64_t>(q_offset, 1 << 30));
+    const bool vec = d % 4 == 0 && vec_view(q, qst) && vec_view(k, kst) && vec_view(v, vst) &&
+                     vec_view(o, ost);
+    const int G = Hq / Hkv;
+    const bool all_visible = !causal || (int64_t)qoff >= (int64_t)Tk - 1;
+    const int64_t rows = (int64_t)G * Tq;
+
+    if (vec && all_visible && rows <= nne::splitk_max_rows() && Tk > 0) {
+        nne::SplitKParams p{};
+        p.q = make_view(q, qst);
+        p.k = k; p.v = v;
+        p.ksb = kst[0]; p.ksh = kst[1]; p.kst = kst[2];
+        p.vsb = vst[0]; p.vsh = vst[1]; p.vst = vst[2];
+        p.lens = nullptr;
+        p.tk = Tk;
+        p.o = make_out(o, ost);
+        p.B = B; p.Hq = Hq; p.Hkv = Hkv; p.Tq = Tq; p.d = d;
+        p.qscale = scale * nne::kLog2e;
+        const int kps = nne::splitk_keys_per_split(Tk, B * Hkv);
+        void* ws = nullptr;
+        if (Tk > kps) {
+            const uint64_t bytes = nne::splitk_workspace_bytes(B, Hkv, (int)rows, d, Tk, kps);
+            hipError_t e = hipMallocAsync(&ws, bytes, stream);
+            if (e != hipSuccess) return hip_fail(e, "hipMallocAsync(split-K workspace)");
+        }
+        hipError_t e = nne::launch_splitk(p, Tk, kps, ws, stream);
+        if (ws) {
+            hipError_t e2 = hipFreeAsync(ws, stream);
+            if (e == hipSuccess) e = e2;
+        }
+        if (e != hipSuccess) return hip_fail(e, "split-K attention launch");
+        return NNE_OK;
+    }
+
+    nne::PrefillParams p{};
+    p.q = make_view(q, qst);
+    p.k = make_view(k, kst);
+    p.v = make_view(v, vst);
+    p.o = make_out(o, ost);
+    p.B = B; p.Hq = Hq; p.Hkv = Hkv; p.Tq = Tq; p.Tk = Tk; p.d = d;
+    p.q_offset = qoff;
+    p.qscale = scale * nne::kLog2e;
+    hipError_t e = nne::launch_prefill(p, causal, vec, stream);
+    if (e != hipSuccess) return hip_fail(e, "prefill attention launch");
+    return NNE_OK;
+}
+
+struct Resolved {
+    int64_t q[4], k[4], v[4], o[4];
+};
+
+void resolve_strides(Resolved& r, const int64_t* qs_, const int64_t* qst, const int64_t* ks_,
+                     const int64_t* kst, const int64_t* vs_, const int64_t* vst, const int64_t* ost) {
+    int64_t c[4];
+    contiguous_strides(qs_, c);
+    for (int i = 0; i < 4; ++i) r.q[i] = qst ? qst[i] : c[i];
+    for (int i = 0; i < 4; ++i) r.o[i] = ost ? ost[i] : c[i];
+    contiguous_strides(ks_, c);
+    for (int i = 0; i < 4; ++i) r.k[i] = kst ? kst[i] : c[i];
+    contiguous_strides(vs_, c);
+    for (int i = 0; i < 4; ++i) r.v[i] = vst ? vst[i] : c[i];
+}
+
+int check_kv_cache_args(int64_t B, int64_t Hq, int64_t Hkv, int64_t capacity, int64_t d) {
+    if (B < 0 || Hq < 0 || Hkv <= 0 || capacity < 0 || d <= 0 || B > INT32_MAX ||
+        Hq > INT32_MAX || Hkv > INT32_MAX || capacity > INT32_MAX || d > INT32_MAX)
+        return fail(NNE_EINVAL, "Invalid configuration or argument: bad KV cache geometry "
+                                "B=%lld Hq=%lld Hkv=%lld capacity=%lld d=%lld",
+                    (long long)B, (long long)Hq, (long long)Hkv, (long long)capacity, (long long)d);
+    if (Hq % Hkv != 0)
+        return fail(NNE_EINVAL, "Invalid configuration or argument: num_heads (%lld) must be "
+                                "divisible by num_kv_heads (%lld) for GQA",
+                    (long long)Hq, (long long)Hkv);
+    if (d % 4 != 0 || nne::splitk_padded_dim((int)d) == 0)
+        return fail(NNE_EINVAL, "Invalid configuration or argument: KV cache head dim %lld must be "
+                                "a multiple of 4 and at most 128", (long long)d);
+    return NNE_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int nne_abi_version(void) { return NNE_ABI_VERSION; }
+
+const char* nne_last_error(void) { return g_err.c_str(); }
+
+int nne_dev_alloc(void** ptr, uint64_t bytes) {
+    if (!ptr) return fail(NNE_EINVAL, "Invalid configuration or argument: null output pointer");
+    *ptr = nullptr;
+    if (bytes == 0) return NNE_OK;
+    hipError_t e = hipMalloc(ptr, bytes);
+    if (e != hipSuccess) return hip_fail(e, "hipMalloc");
+    return NNE_OK;
+}
+
+int nne_dev_free(void* ptr) {
+    if (!ptr) return NNE_OK;
+    hipError_t e = hipFree(ptr);
+    if (e != hipSuccess) return hip_fail(e, "hipFree");
+    return NNE_OK;
+}
+
+int nne_memcpy_h2d(void* dst, const void* src, uint64_t bytes, void* stream) {
+    hipError_t e = hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, as_stream(stream));
+    if (e == hipSuccess) e = hipStreamSynchronize(as_stream(stream));
+    return e == hipSuccess ? NNE_OK : hip_fail(e, "hipMemcpy H2D");
+}
+
+int nne_memcpy_d2h(void* dst, const void* src, uint64_t bytes, void* stream) {
+    hipError_t e = hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, as_stream(stream));
+    if (e == hipSuccess) e = hipStreamSynchronize(as_stream(stream));
+    return e == hipSuccess ? NNE_OK : hip_fail(e, "hipMemcpy D2H");
+}
+
+int nne_memcpy_d2d(void* dst, const void* src, uint64_t bytes, void* stream) {
+    hipError_t e = hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, as_stream(stream));
+    return e == hipSuccess ? NNE_OK : hip_fail(e, "hipMemcpy D2D");
+}
+
+int nne_stream_sync(void* stream) {
+    hipError_t e = hipStreamSynchronize(as_stream(stream));
+    return e == hipSuccess ? NNE_OK : hip_fail(e, "hipStreamSynchronize");
+}
+
+int nne_flash_attention_forward(const float* q, const int64_t q_shape[4], const int64_t q_strides[4],
+                                const float* k, const int64_t k_shape[4], const int64_t k_strides[4],
+                                const float* v, const int64_t v_shape[4], const int64_t v_strides[4],
+                                float* o, const int64_t o_strides[4], int is_causal, int has_scale,
+                                float scale, int64_t block_size_r, int64_t block_size_c,
+                                void* stream) {
+    if (!q_shape || !k_shape || !v_shape)
+        return fail(NNE_EINVAL, "Invalid configuration or argument: FlashAttention expects 4D "
+                                "tensors [Batch, Heads, SeqLen, Dim]");
+    if (!dims_ok(q_shape) || !dims_ok(k_shape) || !dims_ok(v_shape))
+        return fail(NNE_EINVAL, "Invalid configuration or argument: FlashAttention dims out of "
+                                "range, got Q:%s, K:%s, V:%s", shape_str(q_shape).c_str(),
+                    shape_str(k_shape).c_str(), shape_str(v_shape).c_str());
+    // flash_attention.rs:39-48
+    const int64_t b = q_shape[0], h = q_shape[1], d = q_shape[3];
+    const int64_t kb = k_shape[0], kh = k_shape[1], tk = k_shape[2], kd = k_shape[3];
+    const int64_t vb = v_shape[0], vh = v_shape[1], vt = v_shape[2], vd = v_shape[3];
+    if (b != kb || b != vb || h != kh || h != vh || d != kd || d != vd || tk != vt) {
+        const int64_t expected[4] = {b, h, tk, d};
+        const int64_t actual[4] = {kb, kh, tk, kd};
+        return fail(NNE_ESHAPE, "Shape mismatch error: expected shape %s, got %s",
+                    shape_str(expected).c_str(), shape_str(actual).c_str());
+    }
+    (void)block_size_r;   // br, bc = max(arg, 16) (:51-52) only order the reference's loops
+    (void)block_size_c;
+    if (b * h * q_shape[2] > 0 && (!q || !k || !v || !o) && tk > 0)
+        return fail(NNE_EINVAL, "Invalid configuration or argument: null tensor pointer");
+    Resolved r;
+    resolve_strides(r, q_shape, q_strides, k_shape, k_strides, v_shape, v_strides, o_strides);
+    return run_attention(q, q_shape, r.q, k, k_shape, r.k, v, r.v, o, r.o, is_causal != 0, 0,
+                         softmax_scale(has_scale, scale, d), as_stream(stream));
+}
+
+int nne_attention_forward(const float* q, const int64_t q_shape[4], const int64_t q_strides[4],
+                          const float* k, const int64_t k_shape[4], const int64_t k_strides[4],
+                          const float* v, const int64_t v_shape[4], const int64_t v_strides[4],
+                          float* o, const int64_t o_strides[4], int is_causal, int64_t q_offset,
+                          int has_scale, float scale, void* stream) {
+    if (!q_shape || !k_shape || !v_shape)
+        return fail(NNE_EINVAL, "Invalid configuration or argument: attention expects 4D "
+                                "tensors [Batch, Heads, SeqLen, Dim]");
+    if (!dims_ok(q_shape) || !dims_ok(k_shape) || !dims_ok(v_shape))
+        return fail(NNE_EINVAL, "Invalid configuration or argument: attention dims out of range, "
+                                "got Q:%s, K:%s, V:%s", shape_str(q_shape).c_str(),
+                    shape_str(k_shape).c_str(), shape_str(v_shape).c_str());
+    const int64_t b = q_shape[0], hq = q_shape[1], d = q_shape[3];
+    const int64_t kb = k_shape[0], hkv = k_shape[1], tk = k_shape[2], kd = k_shape[3];
+    if (b != kb || b != v_shape[0] || hkv != v_shape[1] || d != kd || d != v_shape[3] ||
+        tk != v_shape[2] || hkv == 0 || hq % hkv != 0) {
+        const int64_t expected[4] = {b, hkv > 0 && hq % hkv == 0 ? hkv : hq, tk, d};
+        const int64_t actual[4] = {kb, hkv, tk, kd};
+        return fail(NNE_ESHAPE, "Shape mismatch error: expected shape %s, got %s",
+                    shape_str(expected).c_str(), shape_str(actual).c_str());
+    }
+    if (b * hq * q_shape[2] > 0 && (!q || !k || !v || !o) && tk > 0)
+        return fail(NNE_EINVAL, "Invalid configuration or argument: null tensor pointer");
+    Resolved r;
+    resolve_strides(r, q_shape, q_strides, k_shape, k_strides, v_shape, v_strides, o_strides);
+    return run_attention(q, q_shape, r.q, k, k_shape, r.k, v, r.v, o, r.o, is_causal != 0,
+                         q_offset, softmax_scale(has_scale, scale, d), as_stream(stream));
+}
+
+int nne_kv_append(float* k_cache, float* v_cache, int32_t* lens_dev, int32_t* lens_host,
+                  const float* k_new, const int64_t k_new_strides[4], const float* v_new,
+                  const int64_t v_new_strides[4], int64_t B, int64_t Hkv, int64_t capacity,
+                  int64_t d, int64_t t_new, void* stream) {
+    int rc = check_kv_cache_args(B, Hkv, Hkv, capacity, d);
+    if (rc) return rc;
+    if (t_new < 0 || t_new > INT32_MAX)
+        return fail(NNE_EINVAL, "Invalid configuration or argument: t_new = %lld", (long long)t_new);
+    if (B > 0 && !lens_host)
+        return fail(NNE_EINVAL, "Invalid configuration or argument: lens_host is null");
+    for (int64_t b = 0; b < B; ++b) {
+        if (lens_host[b] < 0 || (int64_t)lens_host[b] + t_new > capacity)
+            return fail(NNE_ECAPACITY, "GPU compute error: KV cache append of %lld rows to "
+                                       "sequence %lld of length %d exceeds capacity %lld",
+                        (long long)t_new, (long long)b, lens_host[b], (long long)capacity);
+    }
+    if (B == 0 || t_new == 0) return NNE_OK;
+    const int64_t shape[4] = {B, Hkv, t_new, d};
+    int64_t c[4];
+    contiguous_strides(shape, c);
+    nne::View4 kn = make_view(k_new, k_new_strides ? k_new_strides : c);
+    nne::View4 vn = make_view(v_new, v_new_strides ? v_new_strides : c);
+    hipError_t e = nne::launch_kv_append(k_cache, v_cache, lens_dev, kn, vn, (int)B, (int)Hkv,
+                                         (int)capacity, (int)d, (int)t_new, as_stream(stream));
+    if (e != hipSuccess) return hip_fail(e, "KV append launch");
+    for (int64_t b = 0; b < B; ++b) lens_host[b] += (int32_t)t_new;
+    return NNE_OK;
+}
+
+uint64_t nne_decode_workspace_bytes(int64_t B, int64_t Hq, int64_t Hkv, int64_t d, int64_t max_len) {
+    if (B <= 0 || Hkv <= 0 || Hq <= 0 || Hq % Hkv != 0 || d <= 0 || max_len <= 0) return 0;
+    const int kps = nne::splitk_keys_per_split((int)max_len, (int)(B * Hkv));
+    if (max_len <= kps) return 0;
+    return nne::splitk_workspace_bytes((int)B, (int)Hkv, (int)(Hq / Hkv), (int)d, (int)max_len, kps);
+}
+
+int nne_decode_attention(const float* q, const int64_t q_strides[4], const float* k_cache,
+                         const float* v_cache, const int32_t* lens_dev, const int32_t* lens_host,
+                         float* o, const int64_t o_strides[4], int64_t B, int64_t Hq, int64_t Hkv,
+                         int64_t capacity, int64_t d, int has_scale, float scale, void* workspace,
+                         uint64_t workspace_bytes, void* stream) {
+    int rc = check_kv_cache_args(B, Hq, Hkv, capacity, d);
+    if (rc) return rc;
+    if (Hq / Hkv > nne::splitk_max_rows())
+        return fail(NNE_EINVAL, "Invalid configuration or argument: %lld query heads per KV head "
+                                "exceeds the decode kernel's %d", (long long)(Hq / Hkv),
+                    nne::splitk_max_rows());
+    if (B == 0 || Hq == 0) return NNE_OK;
+    if (!lens_host)
+        return fail(NNE_EINVAL, "Invalid configuration or argument: lens_host is null");
+    int max_len = 0;
+    for (int64_t b = 0; b < B; ++b) {
+        if (lens_host[b] < 0 || lens_host[b] > capacity)
+            return fail(NNE_EINVAL, "Invalid configuration or argument: sequence %lld length %d "
+                                    "outside [0, %lld]", (long long)b, lens_host[b],
+                        (long long)capacity);
+        max_len = std::max(max_len, (int)lens_host[b]);
+    }
+    const int64_t qshape[4] = {B, Hq, 1, d};
+    int64_t c[4];
+    contiguous_strides(qshape, c);
+    const int64_t* qst = q_strides ? q_strides : c;
+    const int64_t* ost = o_strides ? o_strides : c;
+    if (qst[3] != 1 || ost[3] != 1)
+        return fail(NNE_EINVAL, "Invalid configuration or argument: decode q/o need unit dim stride");
+    if (!aligned16(k_cache) || !aligned16(v_cache))
+        return fail(NNE_EINVAL, "Invalid configuration or argument: KV cache must be 16-byte aligned");
+
+    nne::SplitKParams p{};
+    p.q = make_view(q, qst);
+    p.k = k_cache; p.v = v_cache;
+    p.ksb = Hkv * capacity * d; p.ksh = capacity * d; p.kst = d;
+    p.vsb = p.ksb; p.vsh = p.ksh; p.vst = p.kst;
+    p.lens = lens_dev;
+    p.tk = 0;
+    p.o = make_out(o, ost);
+    p.B = (int)B; p.Hq = (int)Hq; p.Hkv = (int)Hkv; p.Tq = 1; p.d = (int)d;
+    p.qscale = softmax_scale(has_scale, scale, d) * nne::kLog2e;
+    const int ml = std::max(max_len, 1);
+    const int kps = nne::splitk_keys_per_split(ml, (int)(B * Hkv));
+    const uint64_t need = ml > kps ? nne::splitk_workspace_bytes((int)B, (int)Hkv, (int)(Hq / Hkv),
+                                                                 (int)d, ml, kps)
+                                   : 0;
+    hipStream_t s = as_stream(stream);
+    void* ws = workspace;
+    bool owned = false;
+    if (need > 0 && !ws) {
+        hipError_t e = hipMallocAsync(&ws, need, s);
+        if (e != hipSuccess) return hip_fail(e, "hipMallocAsync(decode workspace)");
+        owned = true;
+    } else if (need > workspace_bytes) {
+        return fail(NNE_EINVAL, "Invalid configuration or argument: decode workspace of %llu bytes "
+                                "is smaller than the %llu required",
+                    (unsigned long long)workspace_bytes, (unsigned long long)need);
+    }
+    hipError_t e = nne::launch_splitk(p, ml, kps, ws, s);
+    if (owned) {
+        hipError_t e2 = hipFreeAsync(ws, s);
+        if (e == hipSuccess) e = e2;
+    }
+    if (e != hipSuccess) return hip_fail(e, "decode attention launch");
+    return NNE_OK;
+}
+
+int nne_decode_step(const float* q, const int64_t q_strides[4], float* k_cache, float* v_cache,
+                    int32_t* lens_dev, int32_t* lens_host, const float* k_new,
+                    const int64_t k_new_strides[4], const float* v_new,
+                    const int64_t v_new_strides[4], float* o, const int64_t o_strides[4],
+                    int64_t B, int64_t Hq, int64_t Hkv, int64_t capacity, int64_t d,
+                    int has_scale, float scale, void* workspace, uint64_t workspace_bytes,
+                    void* stream) {
+    int rc = check_kv_cache_args(B, Hq, Hkv, capacity, d);
+    if (rc) return rc;
+    rc = nne_kv_append(k_cache, v_cache, lens_dev, lens_host, k_new, k_new_strides, v_new,
+                       v_new_strides, B, Hkv, capacity, d, 1, stream);
+    if (rc) return rc;
+    return nne_decode_attention(q, q_strides, k_cache, v_cache, lens_dev, lens_host, o, o_strides,
+                                B, Hq, Hkv, capacity, d, has_scale, scale, workspace,
+                                workspace_bytes, stream);
+}
+
+}  // extern "C"

@@ -1,0 +1,86 @@
+// Shared device helpers and launch-parameter structs for the attention kernels.
+//
+// Layout conventions (all f32):
+//   Q/O  [B, Hq,  T_q, d]  and  K/V [B, Hkv, T_k, d], each a strided view
+//   (element strides for batch, head, row, dim).  Query head hq reads KV head
+//   hq / G with G = Hq / Hkv, the repeat-KV mapping of the reference's
+//   GroupedQueryAttention (src/models/llama.rs:256-266).
+//   A key c is visible to query row r iff c <= r + q_offset (causal) -- the
+//   reference's flash path uses q_offset = 0 (src/nn/flash_attention.rs:113),
+//   its cached GQA/MHA paths use q_offset = start_pos (llama.rs:280-283,
+//   attention.rs:104-108).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace nne {
+
+typedef float floatx16 __attribute__((ext_vector_type(16)));
+
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kNegInf = -__builtin_huge_valf();
+
+struct View4 {
+    const float* p;
+    int64_t sb, sh, st, sd;
+};
+
+struct OutView4 {
+    float* p;
+    int64_t sb, sh, st, sd;
+};
+
+// Prefill (MFMA) kernel parameters.  One workgroup = 4 waves; each wave owns
+// one "unit" = 32 query rows of one query head.  Units of one KV head are
+// numbered u = row_block * G + g, and workgroup w of that KV head takes units
+// 4w .. 4w+3, so the G query heads of a group share every K/V tile the
+// workgroup stages in LDS.
+struct PrefillParams {
+    View4 q, k, v;
+    OutView4 o;
+    int B, Hq, Hkv, G, Tq, Tk, d;
+    int q_offset;
+    float qscale;   // softmax scale * log2(e), folded into Q
+    int n_rb;       // ceil(Tq / 32)
+    int n_units;    // G * n_rb
+    int n_wg;       // ceil(n_units / 4) workgroups per KV head
+    int total;      // B * Hkv * n_wg
+};
+
+// Split-K few-query kernel parameters (decode and cross-attention).  Each KV
+// head serves R = G * Tq query rows; row rr maps to query head kvh*G + rr/Tq
+// and query position rr % Tq.  Every row sees every key of its sequence.
+struct SplitKParams {
+    View4 q;
+    const float* k;
+    const float* v;
+    int64_t ksb, ksh, kst;   // K strides (dim stride 1)
+    int64_t vsb, vsh, vst;   // V strides (dim stride 1)
+    const int32_t* lens;     // per-sequence key counts (device), or null
+    int tk;                  // key count when lens == null
+    OutView4 o;
+    int B, Hq, Hkv, G, Tq, d, R;
+    float qscale;            // softmax scale * log2(e)
+    int n_chunks;            // chunk slots per (b, kv head) in the workspace
+    float* ws_o;             // [B*Hkv][n_chunks][R][D] unnormalised partial O
+    float* ws_ml;            // [B*Hkv][n_chunks][R][2] partial (max, sum)
+};
+
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// Swaps lanes 32..63 of `a` with lanes 0..31 of `b` (gfx950 v_permlane32_swap).
+// Called with a == b == x, element 0 of the result holds x from lanes 0..31 in
+// both halves and element 1 holds x from lanes 32..63 in both halves, so
+// combining the two elements reduces over the lane pair (l, l ^ 32).
+__device__ __forceinline__ float pair_max(float x) {
+    auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+
+__device__ __forceinline__ float pair_sum(float x) {
+    auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+}  // namespace nne

@@ -1,0 +1,306 @@
+// FlashAttention forward for gfx950 on full-fp32 MFMA (v_mfma_f32_32x32x2_f32).
+//
+// Algorithm: the tiled online softmax of the reference's
+// flash_attention_forward (src/nn/flash_attention.rs:91-195) -- per query row a
+// running max m and sum l, P = exp(S - m), O = alpha*O + P V, O /= l at the end
+// with rows that saw no key left at zero (:186-194), fully masked key tiles
+// skipped (:101-104) -- generalised to grouped-query heads (KV head hq / G) and
+// a causal offset.
+//
+// MI355X mapping.  One wave owns 32 query rows and computes the score tile
+// transposed, S^T = K Q^T, on 32x32x2 MFMAs:
+//   A = K tile  (lane l supplies key l%32, reduction index l/32)
+//   B = Q^T     (lane l supplies query row l%32; held in registers, pre-scaled
+//                by scale*log2(e) so the softmax is a bare exp2)
+// The reduction (head-dim) order is permuted so that lane half h covers dims
+// [h*D/2, h*D/2 + D/2): each lane then reads its K operands as contiguous
+// 16-byte LDS vectors.  The accumulator layout of S^T puts query row l%32 in
+// lane l and keys 8*(r/4) + 4*(l/32) + r%4 in register r, so
+//   * the row max / row sum are 16 in-lane ops plus one lane-pair exchange
+//     (v_permlane32_swap),
+//   * P^T register r is already the B operand of step r of O^T = V^T P^T
+//     (the key order of that reduction is chosen to match), so P never
+//     leaves registers,
+//   * every O^T accumulator of a lane belongs to that lane's query row, so the
+//     online-softmax rescale is a lane-local multiply.
+// K and V tiles (32 keys) are staged through LDS, double buffered, with the
+// next tile's global loads in flight while the current tile is computed.  The
+// G query heads that share a KV head run as waves of one workgroup and read
+// the same staged tiles.  Workgroups are numbered so that each XCD works on a
+// contiguous range of KV heads (its own L2) and, within a head, the longest
+// causal row blocks start first.
+#include "nne_common.hpp"
+#include "nne_launch.hpp"
+
+namespace nne {
+
+namespace {
+
+template <int D, bool VEC>
+struct TileLoader {
+    // K/V tile of 32 keys x D dims = 8*D float4; 256 threads -> D/32 each.
+    static constexpr int NV = D / 32;
+    static constexpr int C4 = D / 4;    // float4 columns per row
+    float4 kr[NV], vr[NV];
+
+    __device__ __forceinline__ void load(const PrefillParams& p, const float* kb, const float* vb,
+                                         int key0, int tid) {
+#pragma unroll
+        for (int i = 0; i < NV; ++i) {
+            const int idx = tid + 256 * i;
+            const int row = idx / C4, c = (idx % C4) * 4;
+            const int key = key0 + row;
+            if (VEC) {
+                const bool ok = key < p.Tk && c < p.d;
+                kr[i] = ok ? *reinterpret_cast<const float4*>(kb + key * p.k.st + c)
+                           : make_float4(0.f, 0.f, 0.f, 0.f);
+                vr[i] = ok ? *reinterpret_cast<const float4*>(vb + key * p.v.st + c)
+                           : make_float4(0.f, 0.f, 0.f, 0.f);
+            } else {
+                float kx[4], vx[4];
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const bool ok = key < p.Tk && c + j < p.d;
+                    kx[j] = ok ? kb[key * p.k.st + (c + j) * p.k.sd] : 0.f;
+                    vx[j] = ok ? vb[key * p.v.st + (c + j) * p.v.sd] : 0.f;
+                }
+                kr[i] = make_float4(kx[0], kx[1], kx[2], kx[3]);
+                vr[i] = make_float4(vx[0], vx[1], vx[2], vx[3]);
+            }
+        }
+    }
+
+    __device__ __forceinline__ void store(float* ks, float* vs, int tid) const {
+        constexpr int KS = D + 4, VS = D + 8;
+#pragma unroll
+        for (int i = 0; i < NV; ++i) {
+            const int idx = tid + 256 * i;
+            const int row = idx / C4, c = (idx % C4) * 4;
+            *reinterpret_cast<float4*>(ks + row * KS + c) = kr[i];
+            *reinterpret_cast<float4*>(vs + row * VS + c) = vr[i];
+        }
+    }
+};
+
+// Last key index visible to any row of row block rb (or -1).
+__device__ __forceinline__ int last_visible_key(const PrefillParams& p, int rb, bool causal) {
+    if (!causal) return p.Tk - 1;
+    int last_row = rb * 32 + 31;
+    if (last_row > p.Tq - 1) last_row = p.Tq - 1;
+    int lk = last_row + p.q_offset;
+    return lk < p.Tk - 1 ? lk : p.Tk - 1;
+}
+
+template <int D, bool CAUSAL, bool VEC>
+__global__ __launch_bounds__(256, 2) void prefill_mfma_kernel(const PrefillParams p) {
+    constexpr int KS = D + 4;          // K row stride in LDS (16-byte reads conflict-free)
+    constexpr int VS = D + 8;          // V row stride in LDS (lane halves on disjoint banks)
+    constexpr int STAGE = 32 * KS + 32 * VS;
+    constexpr int NB = D / 32;         // 32-wide output column blocks
+    __shared__ __attribute__((aligned(16))) float lds[2 * STAGE];
+
+    // ---- workgroup -> (KV head, workgroup-in-head) --------------------------
+    // Hardware dispatches consecutive workgroup ids round-robin over the 8
+    // XCDs; remap so XCD c gets the contiguous logical range [c*per, (c+1)*per).
+    const int per = gridDim.x >> 3;
+    const int logical = (blockIdx.x & 7) * per + (blockIdx.x >> 3);
+    if (logical >= p.total) return;
+    const int head = logical / p.n_wg;
+    const int wgi = p.n_wg - 1 - (logical % p.n_wg);   // longest causal work first
+    const int bi = head / p.Hkv, kvh = head % p.Hkv;
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int l32 = lane & 31, half = lane >> 5;
+
+    const int unit = wgi * 4 + wave;
+    const bool active = unit < p.n_units;
+    const int rb = active ? unit / p.G : 0;
+    const int g = active ? unit % p.G : 0;
+    const int hq = kvh * p.G + g;
+    const int row0 = rb * 32;
+    const int qrow = row0 + l32;
+
+    // ---- key-tile range ------------------------------------------------------
+    const int n_kt = (p.Tk + 31) >> 5;
+    int last_unit = wgi * 4 + 3;
+    if (last_unit > p.n_units - 1) last_unit = p.n_units - 1;
+    const int wg_last_key = last_visible_key(p, last_unit / p.G, CAUSAL);
+    int n_tiles = wg_last_key < 0 ? 0 : (wg_last_key >> 5) + 1;
+    if (n_tiles > n_kt) n_tiles = n_kt;
+    const int wave_last_key = last_visible_key(p, rb, CAUSAL);
+    const int wave_tiles = active ? (wave_last_key < 0 ? 0 : (wave_last_key >> 5) + 1) : 0;
+
+    // ---- Q^T fragment: qf[s] = Q[qrow][half*D/2 + s] * scale*log2(e) ----------
+    float qf[D / 2];
+    {
+        const float* qp = p.q.p + bi * p.q.sb + hq * p.q.sh + (int64_t)qrow * p.q.st;
+        const bool rok = active && qrow < p.Tq;
+#pragma unroll
+        for (int s4 = 0; s4 < D / 8; ++s4) {
+            const int c = half * (D / 2) + 4 * s4;
+            float x[4];
+            if (VEC) {
+                float4 t = (rok && c < p.d) ? *reinterpret_cast<const float4*>(qp + c)
+                                            : make_float4(0.f, 0.f, 0.f, 0.f);
+                x[0] = t.x; x[1] = t.y; x[2] = t.z; x[3] = t.w;
+            } else {
+#pragma unroll
+                for (int j = 0; j < 4; ++j) x[j] = (rok && c + j < p.d) ? qp[(c + j) * p.q.sd] : 0.f;
+            }
+#pragma unroll
+            for (int j = 0; j < 4; ++j) qf[4 * s4 + j] = x[j] * p.qscale;
+        }
+    }
+
+    const float* kb = p.k.p + bi * p.k.sb + kvh * p.k.sh;
+    const float* vb = p.v.p + bi * p.v.sb + kvh * p.v.sh;
+
+    floatx16 o[NB];
+#pragma unroll
+    for (int b = 0; b < NB; ++b)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) o[b][r] = 0.f;
+    float m_run = kNegInf, l_run = 0.f;
+
+    TileLoader<D, VEC> ld;
+    if (n_tiles > 0) {
+        ld.load(p, kb, vb, 0, tid);
+        ld.store(lds, lds + 32 * KS, tid);
+    }
+    __syncthreads();
+
+    for (int kt = 0; kt < n_tiles; ++kt) {
+        const bool has_next = kt + 1 < n_tiles;
+        if (has_next) ld.load(p, kb, vb, (kt + 1) * 32, tid);
+
+        if (kt < wave_tiles) {
+            const float* Ks = lds + (kt & 1) * STAGE;
+            const float* Vs = Ks + 32 * KS;
+
+            // S^T = K Q^T  (32 keys x 32 rows), log2 domain.
+            floatx16 s;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) s[r] = 0.f;
+            const float* krow = Ks + l32 * KS + half * (D / 2);
+#pragma unroll
+            for (int t = 0; t < D / 8; ++t) {
+                const float4 kq = *reinterpret_cast<const float4*>(krow + 4 * t);
+                s = __builtin_amdgcn_mfma_f32_32x32x2f32(kq.x, qf[4 * t + 0], s, 0, 0, 0);
+                s = __builtin_amdgcn_mfma_f32_32x32x2f32(kq.y, qf[4 * t + 1], s, 0, 0, 0);
+                s = __builtin_amdgcn_mfma_f32_32x32x2f32(kq.z, qf[4 * t + 2], s, 0, 0, 0);
+                s = __builtin_amdgcn_mfma_f32_32x32x2f32(kq.w, qf[4 * t + 3], s, 0, 0, 0);
+            }
+
+            // Mask keys past T_k and (causal) keys after row + q_offset.
+            const int key0 = kt * 32;
+            const bool need_mask = (key0 + 32 > p.Tk) || (CAUSAL && key0 + 31 > row0 + p.q_offset);
+            if (need_mask) {
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const int key = key0 + 8 * (r >> 2) + 4 * half + (r & 3);
+                    const bool vis = key < p.Tk && (!CAUSAL || key <= qrow + p.q_offset);
+                    s[r] = vis ? s[r] : kNegInf;
+                }
+            }
+
+            // Online softmax for this lane's row (keys split over the lane pair).
+            float mt = s[0];
+#pragma unroll
+            for (int r = 1; r < 16; ++r) mt = fmaxf(mt, s[r]);
+            mt = pair_max(mt);
+            const float m_new = fmaxf(m_run, mt);
+            const float m_use = (m_new == kNegInf) ? 0.f : m_new;
+            const float alpha = fast_exp2(m_run - m_use);
+            float ls = 0.f;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                s[r] = fast_exp2(s[r] - m_use);
+                ls += s[r];
+            }
+            l_run = alpha * l_run + ls;
+            m_run = m_new;
+#pragma unroll
+            for (int b = 0; b < NB; ++b)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) o[b][r] *= alpha;
+
+            // O^T += V^T P^T ; reduction step r pairs key 8*(r/4)+4*half+r%4.
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const float* vrow = Vs + (8 * (r >> 2) + 4 * half + (r & 3)) * VS + l32;
+#pragma unroll
+                for (int b = 0; b < NB; ++b)
+                    o[b] = __builtin_amdgcn_mfma_f32_32x32x2f32(vrow[32 * b], s[r], o[b], 0, 0, 0);
+            }
+        }
+
+        if (has_next) {
+            float* ks = lds + ((kt + 1) & 1) * STAGE;
+            ld.store(ks, ks + 32 * KS, tid);
+        }
+        __syncthreads();
+    }
+
+    // ---- normalise and write O[qrow][dim], dim = 32b + 8(r/4) + 4*half + r%4 --
+    const float l_tot = pair_sum(l_run);
+    const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
+    if (active && qrow < p.Tq) {
+        float* op = p.o.p + bi * p.o.sb + hq * p.o.sh + (int64_t)qrow * p.o.st;
+#pragma unroll
+        for (int b = 0; b < NB; ++b) {
+#pragma unroll
+            for (int qq = 0; qq < 4; ++qq) {
+                const int c = 32 * b + 8 * qq + 4 * half;
+                if (VEC) {
+                    if (c < p.d)
+                        *reinterpret_cast<float4*>(op + c) =
+                            make_float4(o[b][4 * qq] * inv, o[b][4 * qq + 1] * inv,
+                                        o[b][4 * qq + 2] * inv, o[b][4 * qq + 3] * inv);
+                } else {
+#pragma unroll
+                    for (int j = 0; j < 4; ++j)
+                        if (c + j < p.d) op[(c + j) * p.o.sd] = o[b][4 * qq + j] * inv;
+                }
+            }
+        }
+    }
+}
+
+template <int D, bool CAUSAL, bool VEC>
+hipError_t launch_t(const PrefillParams& p, hipStream_t stream) {
+    const int grid = ((p.total + 7) / 8) * 8;
+    hipLaunchKernelGGL((prefill_mfma_kernel<D, CAUSAL, VEC>), dim3(grid), dim3(256), 0, stream, p);
+    return hipGetLastError();
+}
+
+template <int D>
+hipError_t launch_d(const PrefillParams& p, bool causal, bool vec, hipStream_t stream) {
+    if (causal) return vec ? launch_t<D, true, true>(p, stream) : launch_t<D, true, false>(p, stream);
+    return vec ? launch_t<D, false, true>(p, stream) : launch_t<D, false, false>(p, stream);
+}
+
+}  // namespace
+
+int prefill_padded_dim(int d) {
+    if (d <= 32) return 32;
+    if (d <= 64) return 64;
+    if (d <= 128) return 128;
+    return 0;
+}
+
+hipError_t launch_prefill(PrefillParams p, bool causal, bool vec, hipStream_t stream) {
+    p.G = p.Hq / p.Hkv;
+    p.n_rb = (p.Tq + 31) / 32;
+    p.n_units = p.G * p.n_rb;
+    p.n_wg = (p.n_units + 3) / 4;
+    p.total = p.B * p.Hkv * p.n_wg;
+    if (p.total == 0) return hipSuccess;
+    switch (prefill_padded_dim(p.d)) {
+        case 32: return launch_d<32>(p, causal, vec, stream);
+        case 64: return launch_d<64>(p, causal, vec, stream);
+        case 128: return launch_d<128>(p, causal, vec, stream);
+        default: return hipErrorInvalidValue;
+    }
+}
+
+}  // namespace nne

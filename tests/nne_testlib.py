@@ -1,0 +1,181 @@
+"""Test-side helpers: load the product package and the CPU oracle.
+
+The oracle (oracle/liboracle.so) is the checker only; the product library never
+loads it.  Tolerances follow the north-star parity bar: per element
+|gpu - ref| <= 1e-4 + 1e-3 * |ref|.
+"""
+import ctypes
+import importlib.util
+import os
+import subprocess
+import sys
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+PKG_DIR = os.path.join(ROOT, "neural-network-engine_amd")
+HEADER = os.path.join(ROOT, "include", "nne_attn.h")
+ORACLE_DIR = os.path.join(ROOT, "oracle")
+ORACLE_LIB = os.path.join(ORACLE_DIR, "liboracle.so")
+GOLDEN_DIR = os.path.join(ROOT, "tests", "golden")
+
+ATOL = 1e-4
+RTOL = 1e-3
+
+
+def load_package():
+    name = "nne_amd"
+    if name in sys.modules:
+        return sys.modules[name]
+    spec = importlib.util.spec_from_file_location(
+        name, os.path.join(PKG_DIR, "__init__.py"), submodule_search_locations=[PKG_DIR])
+    mod = importlib.util.module_from_spec(spec)
+    sys.modules[name] = mod
+    spec.loader.exec_module(mod)
+    return mod
+
+
+_oracle = None
+_f = ctypes.POINTER(ctypes.c_float)
+_i32 = ctypes.POINTER(ctypes.c_int32)
+_I = ctypes.c_int64
+
+
+def oracle():
+    global _oracle
+    if _oracle is None:
+        if not os.path.exists(ORACLE_LIB):
+            subprocess.run(["make", "-s", "-C", ORACLE_DIR], check=True)
+        o = ctypes.CDLL(ORACLE_LIB)
+        o.oracle_flash_forward.argtypes = [_f, _f, _f, _f, _I, _I, _I, _I, _I, ctypes.c_int,
+                                           ctypes.c_int, ctypes.c_float, _I, _I, ctypes.c_int]
+        o.oracle_flash_forward.restype = None
+        o.oracle_standard_attention.argtypes = [_f, _f, _f, _f, _I, _I, _I, _I, _I, _I,
+                                                ctypes.c_int, _I, ctypes.c_int, ctypes.c_float,
+                                                ctypes.c_int]
+        o.oracle_standard_attention.restype = None
+        o.oracle_kv_append.argtypes = [_f, _f, _i32, _f, _f, _I, _I, _I, _I, _I]
+        o.oracle_kv_append.restype = ctypes.c_int
+        o.oracle_decode_step.argtypes = [_f, _f, _f, _i32, _f, _f, _f, _I, _I, _I, _I, _I,
+                                         ctypes.c_int, ctypes.c_float, ctypes.c_int]
+        o.oracle_decode_step.restype = ctypes.c_int
+        o.oracle_decode_attend.argtypes = [_f, _f, _f, _i32, _f, _I, _I, _I, _I, _I,
+                                           ctypes.c_int, ctypes.c_float, ctypes.c_int]
+        o.oracle_decode_attend.restype = None
+        _oracle = o
+    return _oracle
+
+
+def _p(a):
+    assert a.flags.c_contiguous
+    return a.ctypes.data_as(_f)
+
+
+def _threads():
+    return min(8, os.cpu_count() or 1)
+
+
+def ref_flash(q, k, v, causal, scale=None, br=64, bc=64, threads=None):
+    q, k, v = (np.ascontiguousarray(x, dtype=np.float32) for x in (q, k, v))
+    b, h, tq, d = q.shape
+    tk = k.shape[2]
+    out = np.zeros((b, h, tq, d), np.float32)
+    oracle().oracle_flash_forward(_p(q), _p(k), _p(v), _p(out), b, h, tq, tk, d, int(causal),
+                                  int(scale is not None), float(scale or 0.0), br, bc,
+                                  threads or _threads())
+    return out
+
+
+def ref_standard(q, k, v, masked, start_pos=0, scale=None, threads=None):
+    q, k, v = (np.ascontiguousarray(x, dtype=np.float32) for x in (q, k, v))
+    b, hq, tq, d = q.shape
+    hkv, tk = k.shape[1], k.shape[2]
+    out = np.zeros((b, hq, tq, d), np.float32)
+    oracle().oracle_standard_attention(_p(q), _p(k), _p(v), _p(out), b, hq, hkv, tq, tk, d,
+                                       int(masked), start_pos, int(scale is not None),
+                                       float(scale or 0.0), threads or _threads())
+    return out
+
+
+def ref_decode_attend(q, kc, vc, lens, scale=None, threads=None):
+    q, kc, vc = (np.ascontiguousarray(x, dtype=np.float32) for x in (q, kc, vc))
+    lens = np.ascontiguousarray(lens, dtype=np.int32)
+    b, hq, _, d = q.shape
+    hkv, cap = kc.shape[1], kc.shape[2]
+    out = np.zeros((b, hq, 1, d), np.float32)
+    oracle().oracle_decode_attend(_p(q), _p(kc), _p(vc), lens.ctypes.data_as(_i32), _p(out), b,
+                                  hq, hkv, cap, d, int(scale is not None), float(scale or 0.0),
+                                  threads or _threads())
+    return out
+
+
+def ref_decode_step(q, kc, vc, lens, kn, vn, scale=None, threads=None):
+    """Returns (out, kc', vc', lens') -- inputs are not modified."""
+    q, kn, vn = (np.ascontiguousarray(x, dtype=np.float32) for x in (q, kn, vn))
+    kc, vc = kc.astype(np.float32, copy=True), vc.astype(np.float32, copy=True)
+    lens = np.array(lens, dtype=np.int32, copy=True)
+    b, hq, _, d = q.shape
+    hkv, cap = kc.shape[1], kc.shape[2]
+    out = np.zeros((b, hq, 1, d), np.float32)
+    rc = oracle().oracle_decode_step(_p(q), _p(kc), _p(vc), lens.ctypes.data_as(_i32), _p(kn),
+                                     _p(vn), _p(out), b, hq, hkv, cap, d, int(scale is not None),
+                                     float(scale or 0.0), threads or _threads())
+    assert rc == 0
+    return out, kc, vc, lens
+
+
+def ref_kv_append(kc, vc, lens, kn, vn):
+    kc, vc = kc.astype(np.float32, copy=True), vc.astype(np.float32, copy=True)
+    lens = np.array(lens, dtype=np.int32, copy=True)
+    kn, vn = (np.ascontiguousarray(x, dtype=np.float32) for x in (kn, vn))
+    b, hkv, cap, d = kc.shape
+    rc = oracle().oracle_kv_append(_p(kc), _p(vc), lens.ctypes.data_as(_i32), _p(kn), _p(vn), b,
+                                   hkv, cap, d, kn.shape[2])
+    return rc, kc, vc, lens
+
+
+def assert_close(got, ref, atol=ATOL, rtol=RTOL, what=""):
+    got = np.asarray(got, dtype=np.float64)
+    ref = np.asarray(ref, dtype=np.float64)
+    assert got.shape == ref.shape, (what, got.shape, ref.shape)
+    assert np.isfinite(got).all(), what + ": non-finite output"
+    err = np.abs(got - ref)
+    bound = atol + rtol * np.abs(ref)
+    bad = err > bound
+    if bad.any():
+        i = np.unravel_index(np.argmax(err - bound), err.shape)
+        raise AssertionError("%s: %d/%d elements out of tolerance; worst at %s: got %r ref %r "
+                             "(max abs err %.3g)" % (what, bad.sum(), bad.size, i, got[i], ref[i],
+                                                     err.max()))
+
+
+def error_stats(got, ref):
+    got = np.asarray(got, dtype=np.float64)
+    ref = np.asarray(ref, dtype=np.float64)
+    err = np.abs(got - ref)
+    big = np.abs(ref) >= 1e-3
+    return {"max_abs": float(err.max()) if err.size else 0.0,
+            "max_rel": float((err[big] / np.abs(ref[big])).max()) if big.any() else 0.0}
+
+
+def load_golden(name):
+    with np.load(os.path.join(GOLDEN_DIR, name + ".npz"), allow_pickle=False) as z:
+        return {k: z[k] for k in z.files}
+
+
+def golden_names(kind=None):
+    out = []
+    for f in sorted(os.listdir(GOLDEN_DIR)):
+        if f.endswith(".npz"):
+            n = f[:-4]
+            if kind is None or str(load_golden(n)["kind"]) == kind:
+                out.append(n)
+    return out
+
+
+def header_symbols():
+    """Function names declared in include/nne_attn.h."""
+    import re
+    txt = open(HEADER).read()
+    txt = re.sub(r"/\*.*?\*/", "", txt, flags=re.S)
+    return sorted(set(re.findall(r"\b(nne_[a-z0-9_]+)\s*\(", txt)))

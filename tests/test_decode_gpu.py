@@ -1,0 +1,174 @@
+"""GPU parity of the KV cache (in-place append) and single-token decode.
+
+Reference semantics: llama.rs:239-296 with t = 1 -- append the new K/V row,
+then attend to all L rows of the sequence with no mask; ragged batches are
+separate B = 1 problems in the reference.  Bar: |gpu - ref| <= 1e-4 +
+1e-3 |ref|; cache contents bit-exact.
+"""
+import numpy as np
+import pytest
+
+import nne_testlib as T
+
+pytestmark = pytest.mark.gpu
+
+
+def rnd(rng, *shape):
+    return rng.standard_normal(shape).astype(np.float32)
+
+
+def dev(x, cuda):
+    import torch
+    return torch.from_numpy(np.ascontiguousarray(x)).to(cuda)
+
+
+def host(t):
+    import torch
+    torch.cuda.synchronize()
+    return t.cpu().numpy()
+
+
+def make_cache(nne, cuda, b, hkv, cap, d, lens, rng):
+    cache = nne.KVCache(1, b, hkv, cap, d, device=cuda)
+    kc = np.zeros((b, hkv, cap, d), np.float32)
+    vc = np.zeros((b, hkv, cap, d), np.float32)
+    for i, L in enumerate(lens):
+        kc[i, :, :L] = rnd(rng, hkv, L, d)
+        vc[i, :, :L] = rnd(rng, hkv, L, d)
+    cache.k[0].copy_(dev(kc, cuda))
+    cache.v[0].copy_(dev(vc, cuda))
+    cache.set_lengths(0, lens)
+    return cache, kc, vc
+
+
+def test_decode_golden(nne, cuda):
+    g = T.load_golden("decode_ragged_b5g2d16")
+    b, hkv, cap, d = g["k_cache"].shape
+    cache = nne.KVCache(1, b, hkv, cap, d, device=cuda)
+    cache.k[0].copy_(dev(g["k_cache"], cuda))
+    cache.v[0].copy_(dev(g["v_cache"], cuda))
+    cache.set_lengths(0, g["lens"])
+    out = cache.decode_step(0, dev(g["q"], cuda), dev(g["k_new"], cuda), dev(g["v_new"], cuda))
+    T.assert_close(host(out), g["out"], what="decode golden")
+    assert list(cache.lens_host[0]) == list(g["lens"] + 1)
+    assert list(host(cache.lens_dev[0])) == list(g["lens"] + 1)
+
+
+def test_append_is_bit_exact_and_capacity_checked(nne, cuda):
+    rng = np.random.default_rng(1)
+    b, hkv, cap, d = 3, 2, 12, 16
+    lens = np.array([0, 5, 9], np.int32)
+    cache, kc, vc = make_cache(nne, cuda, b, hkv, cap, d, lens, rng)
+    kn, vn = rnd(rng, b, hkv, 3, d), rnd(rng, b, hkv, 3, d)
+    k_all, v_all = cache.update(0, dev(kn, cuda), dev(vn, cuda))
+    rc, kc2, vc2, lens2 = T.ref_kv_append(kc, vc, lens, kn, vn)
+    assert rc == 0
+    assert np.array_equal(host(cache.k[0]), kc2) and np.array_equal(host(cache.v[0]), vc2)
+    assert list(host(cache.lens_dev[0])) == list(lens2)
+    assert tuple(k_all.shape) == (b, hkv, 12, d)
+    with pytest.raises(nne.CapacityError):
+        cache.update(0, dev(kn[:, :, :1], cuda), dev(vn[:, :, :1], cuda))   # 12 + 1 > 12
+    assert list(cache.lens_host[0]) == list(lens2)
+    # strided new rows ([B, T, H, d] projection layout)
+    cache2, kc, vc = make_cache(nne, cuda, b, hkv, cap, d, np.array([1, 2, 3], np.int32), rng)
+    kt, vt = rnd(rng, b, 2, hkv, d), rnd(rng, b, 2, hkv, d)
+    cache2.update(0, dev(kt, cuda).transpose(1, 2), dev(vt, cuda).transpose(1, 2))
+    _, kc3, vc3, _ = T.ref_kv_append(kc, vc, np.array([1, 2, 3], np.int32),
+                                     kt.transpose(0, 2, 1, 3), vt.transpose(0, 2, 1, 3))
+    assert np.array_equal(host(cache2.k[0]), kc3) and np.array_equal(host(cache2.v[0]), vc3)
+
+
+@pytest.mark.parametrize("g,d", [(4, 128), (1, 64), (8, 64), (16, 32), (2, 16)])
+def test_decode_ragged_group_sizes(nne, cuda, g, d):
+    print("case g=%d d=%d" % (g, d), flush=True)
+    rng = np.random.default_rng(100 + g + d)
+    b, hkv, cap = 6, 2, 1200
+    lens = np.array([1, 63, 64, 65, 700, 1100], np.int32)
+    cache, kc, vc = make_cache(nne, cuda, b, hkv, cap, d, lens, rng)
+    q = rnd(rng, b, hkv * g, 1, d)
+    out = host(cache.attend(0, dev(q, cuda)))
+    T.assert_close(out, T.ref_decode_attend(q, kc, vc, lens), what="decode g=%d d=%d" % (g, d))
+
+
+def test_decode_zero_length_sequence_gives_zero(nne, cuda):
+    rng = np.random.default_rng(7)
+    lens = np.array([0, 3000], np.int32)
+    cache, kc, vc = make_cache(nne, cuda, 2, 1, 4096, 64, lens, rng)
+    q = rnd(rng, 2, 4, 1, 64)
+    out = host(cache.attend(0, dev(q, cuda)))
+    assert not out[0].any()
+    T.assert_close(out[1:], T.ref_decode_attend(q, kc, vc, lens)[1:], what="len 3000")
+
+
+def test_config3_multi_step_decode(nne, cuda):
+    """Config 3 geometry (Hq=32, Hkv=8, d=128, ragged L in [512, 4096]) at
+    B=4 over 6 steps; every step checked against the oracle's append+attend."""
+    rng = np.random.default_rng(0x5EED0003)
+    b, hq, hkv, d, steps = 4, 32, 8, 128, 6
+    lens = rng.integers(512, 4097, size=b).astype(np.int32)
+    cap = int(lens.max()) + steps
+    cache, kc, vc = make_cache(nne, cuda, b, hkv, cap, d, lens, rng)
+    for s in range(steps):
+        q, kn, vn = rnd(rng, b, hq, 1, d), rnd(rng, b, hkv, 1, d), rnd(rng, b, hkv, 1, d)
+        out = host(cache.decode_step(0, dev(q, cuda), dev(kn, cuda), dev(vn, cuda)))
+        ref, kc, vc, lens = T.ref_decode_step(q, kc, vc, lens, kn, vn)
+        T.assert_close(out, ref, what="config3 step %d" % s)
+    assert list(cache.lens_host[0]) == list(lens)
+
+
+def test_config3_full_batch_one_step(nne, cuda):
+    """Full config 3 batch: B=32 sequences, Hq=32, Hkv=8, d=128, L ~ U[512, 4096]."""
+    rng = np.random.default_rng(0x5EED0033)
+    b, hq, hkv, d = 32, 32, 8, 128
+    lens = rng.integers(512, 4097, size=b).astype(np.int32)
+    cap = 4096 + 64
+    cache, kc, vc = make_cache(nne, cuda, b, hkv, cap, d, lens, rng)
+    q, kn, vn = rnd(rng, b, hq, 1, d), rnd(rng, b, hkv, 1, d), rnd(rng, b, hkv, 1, d)
+    out = host(cache.decode_step(0, dev(q, cuda), dev(kn, cuda), dev(vn, cuda)))
+    ref, *_ = T.ref_decode_step(q, kc, vc, lens, kn, vn)
+    T.assert_close(out, ref, what="config3 full batch")
+
+
+def test_decode_matches_last_row_of_gpu_prefill(nne, cuda):
+    """Cached decode == the corresponding row of the causal prefill kernel
+    (kv_cache_tests.rs:68-103 pattern), across the two GPU kernels."""
+    rng = np.random.default_rng(9)
+    b, hq, hkv, t, d = 2, 8, 2, 300, 64
+    q, k, v = rnd(rng, b, hq, t, d), rnd(rng, b, hkv, t, d), rnd(rng, b, hkv, t, d)
+    full = host(nne.attention_forward(dev(q, cuda), dev(k, cuda), dev(v, cuda), True))
+    cache = nne.KVCache(1, b, hkv, t, d, device=cuda)
+    cache.update(0, dev(k[:, :, :t - 1], cuda), dev(v[:, :, :t - 1], cuda))
+    out = host(cache.decode_step(0, dev(q[:, :, t - 1:], cuda), dev(k[:, :, t - 1:], cuda),
+                                 dev(v[:, :, t - 1:], cuda)))
+    T.assert_close(out[:, :, 0], full[:, :, t - 1], what="decode vs prefill row")
+
+
+def test_workspace_argument_paths(nne, cuda):
+    """Caller workspace, library-allocated workspace, and a too-small one."""
+    import ctypes
+    import torch
+    rng = np.random.default_rng(11)
+    b, hq, hkv, d, cap = 2, 8, 2, 64, 5000
+    lens = np.array([4000, 4990], np.int32)
+    cache, kc, vc = make_cache(nne, cuda, b, hkv, cap, d, lens, rng)
+    q = dev(rnd(rng, b, hq, 1, d), cuda)
+    ref = T.ref_decode_attend(host(q), kc, vc, lens)
+    lib = nne.lib()
+    i32p = ctypes.POINTER(ctypes.c_int32)
+    for ws in (None, "small"):
+        out = torch.empty_like(q)
+        if ws is None:
+            ptr, nbytes = None, 0
+        else:
+            buf = torch.empty(16, dtype=torch.uint8, device=cuda)
+            ptr, nbytes = buf.data_ptr(), 16
+        rc = lib.nne_decode_attention(q.data_ptr(), None, cache.k[0].data_ptr(),
+                                      cache.v[0].data_ptr(), cache.lens_dev[0].data_ptr(),
+                                      cache.lens_host[0].ctypes.data_as(i32p), out.data_ptr(),
+                                      None, b, hq, hkv, cap, d, 0, 0.0, ptr, nbytes,
+                                      nne._stream())
+        if ws is None:
+            assert rc == 0
+            T.assert_close(host(out), ref, what="library workspace")
+        else:
+            assert rc == nne.NNE_EINVAL

@@ -1,0 +1,208 @@
+"""GPU parity of the prefill path (MFMA FlashAttention kernel and, for few-query
+problems, the split-K kernel) against the CPU oracle and the golden vectors.
+
+Bar: per element |gpu - ref| <= 1e-4 + 1e-3 * |ref| (f32 vs the reference's
+f32 path).  Inputs are seeded; every case prints its name before running.
+"""
+import numpy as np
+import pytest
+
+import nne_testlib as T
+
+pytestmark = pytest.mark.gpu
+
+
+def rnd(seed, *shape, std=1.0):
+    return (np.random.default_rng(seed).standard_normal(shape) * std).astype(np.float32)
+
+
+def dev(x, cuda):
+    import torch
+    return torch.from_numpy(np.ascontiguousarray(x)).to(cuda)
+
+
+def host(t):
+    import torch
+    torch.cuda.synchronize()
+    return t.cpu().numpy()
+
+
+@pytest.mark.parametrize("name", T.golden_names("flash"))
+def test_flash_golden(nne, cuda, name):
+    print("case", name, flush=True)
+    g = T.load_golden(name)
+    out = nne.flash_attention_forward(dev(g["q"], cuda), dev(g["k"], cuda), dev(g["v"], cuda),
+                                      bool(g["causal"]))
+    got = host(out)
+    T.assert_close(got, g["out"], what=name)
+    T.assert_close(got, T.ref_flash(g["q"], g["k"], g["v"], bool(g["causal"])), what=name)
+
+
+@pytest.mark.parametrize("name", T.golden_names("gqa") + T.golden_names("cross"))
+def test_gqa_and_cross_golden(nne, cuda, name):
+    print("case", name, flush=True)
+    g = T.load_golden(name)
+    causal = bool(g["causal"])
+    out = nne.attention_forward(dev(g["q"], cuda), dev(g["k"], cuda), dev(g["v"], cuda), causal,
+                                q_offset=int(g["q_offset"]))
+    got = host(out)
+    T.assert_close(got, g["out"], what=name)
+    ref = T.ref_standard(g["q"], g["k"], g["v"], masked=causal, start_pos=int(g["q_offset"]))
+    T.assert_close(got, ref, what=name)
+
+
+def test_config1_causal_b1h4t256d64(nne, cuda):
+    """Config 1 exactly: B=1, H=4, T=256, d=64, causal, N(0,1)."""
+    q, k, v = rnd(0x5EED0001, 1, 4, 256, 64), rnd(0x5EED0002, 1, 4, 256, 64), rnd(0x5EED0003, 1, 4, 256, 64)
+    got = host(nne.flash_attention_forward(dev(q, cuda), dev(k, cuda), dev(v, cuda), True))
+    T.assert_close(got, T.ref_flash(q, k, v, True), what="config1")
+
+
+@pytest.mark.parametrize("b,h,tq,tk,d,causal", [
+    (1, 2, 33, 33, 64, True), (2, 3, 64, 64, 128, False), (1, 1, 95, 95, 32, True),
+    (1, 2, 200, 130, 64, False), (1, 1, 130, 200, 128, True), (1, 2, 1, 300, 64, True),
+    (2, 1, 257, 257, 16, True), (1, 1, 64, 64, 8, False),
+])
+def test_flash_shapes(nne, cuda, b, h, tq, tk, d, causal):
+    print("case", b, h, tq, tk, d, causal, flush=True)
+    s = 1000 * tq + d
+    q, k, v = rnd(s, b, h, tq, d), rnd(s + 1, b, h, tk, d), rnd(s + 2, b, h, tk, d)
+    got = host(nne.flash_attention_forward(dev(q, cuda), dev(k, cuda), dev(v, cuda), causal))
+    T.assert_close(got, T.ref_flash(q, k, v, causal), what="flash shape")
+
+
+def test_flash_strided_views_match_contiguous(nne, cuda):
+    """[B, T, H, d] projections read through strides (FlashAttention layer
+    layout, flash_attention.rs:259-261), output written through strides."""
+    import torch
+    b, t, h, d = 2, 100, 4, 64
+    x = rnd(5, b, t, h, d)
+    y = rnd(6, b, t, h, d)
+    z = rnd(7, b, t, h, d)
+    qb, kb, vb = dev(x, cuda), dev(y, cuda), dev(z, cuda)
+    q, k, v = qb.transpose(1, 2), kb.transpose(1, 2), vb.transpose(1, 2)
+    out = torch.empty(b, t, h, d, device=cuda)
+    nne.flash_attention_forward(q, k, v, True, out=out.transpose(1, 2))
+    ref = T.ref_flash(x.transpose(0, 2, 1, 3), y.transpose(0, 2, 1, 3), z.transpose(0, 2, 1, 3), True)
+    T.assert_close(host(out).transpose(0, 2, 1, 3), ref, what="strided")
+
+
+def test_flash_scalar_path_odd_head_dim_and_dim_stride(nne, cuda):
+    """d % 4 != 0 and a non-unit dim stride take the scalar-load kernel."""
+    q, k, v = rnd(8, 1, 2, 70, 30), rnd(9, 1, 2, 70, 30), rnd(10, 1, 2, 70, 30)
+    got = host(nne.flash_attention_forward(dev(q, cuda), dev(k, cuda), dev(v, cuda), True))
+    T.assert_close(got, T.ref_flash(q, k, v, True), what="d=30")
+    big = rnd(11, 1, 2, 70, 64)
+    view = dev(big, cuda)[..., ::2]        # dim stride 2 -> scalar path
+    got = host(nne.flash_attention_forward(view, view, view, False))
+    sub = np.ascontiguousarray(big[..., ::2])
+    T.assert_close(got, T.ref_flash(sub, sub, sub, False), what="dim stride 2")
+
+
+def test_explicit_scale(nne, cuda):
+    q, k, v = rnd(12, 1, 2, 50, 64), rnd(13, 1, 2, 50, 64), rnd(14, 1, 2, 50, 64)
+    got = host(nne.flash_attention_forward(dev(q, cuda), dev(k, cuda), dev(v, cuda), False,
+                                           scale=0.05))
+    T.assert_close(got, T.ref_flash(q, k, v, False, scale=0.05), what="scale")
+
+
+def test_empty_keys_and_fully_masked_rows_are_zero(nne, cuda):
+    import torch
+    q = dev(rnd(15, 1, 2, 40, 64), cuda)
+    e = torch.zeros(1, 2, 0, 64, device=cuda)
+    out = nne.flash_attention_forward(q, e, e, False)
+    assert not host(out).any()
+    # negative offset: rows r < 5 see no key (c <= r - 5) and stay zero
+    k, v = rnd(16, 1, 2, 40, 64), rnd(17, 1, 2, 40, 64)
+    got = host(nne.attention_forward(q, dev(k, cuda), dev(v, cuda), True, q_offset=-5))
+    assert not got[:, :, :5].any()
+    qn = host(q)
+    ref = T.ref_standard(qn[:, :, 5:], k, v, True, start_pos=0)
+    T.assert_close(got[:, :, 5:], ref, what="negative offset")
+
+
+@pytest.mark.parametrize("g", [1, 2, 4, 8, 3])
+def test_gqa_group_sizes(nne, cuda, g):
+    hkv, t, d = 2, 97, 64
+    q, k, v = rnd(20 + g, 1, hkv * g, t, d), rnd(30 + g, 1, hkv, t, d), rnd(40 + g, 1, hkv, t, d)
+    got = host(nne.attention_forward(dev(q, cuda), dev(k, cuda), dev(v, cuda), True))
+    T.assert_close(got, T.ref_standard(q, k, v, True), what="gqa g=%d" % g)
+
+
+def _config2_inputs(b, hq, hkv, t, d, seed):
+    """Config 2 inputs: N(0,1) Q/K/V with a per-position scale in [0.5, 1.5]
+    applied to Q and K (all heads, all dims)."""
+    rng = np.random.default_rng(seed)
+    s = rng.uniform(0.5, 1.5, size=t).astype(np.float32)
+    q = rng.standard_normal((b, hq, t, d)).astype(np.float32) * s[None, None, :, None]
+    k = rng.standard_normal((b, hkv, t, d)).astype(np.float32) * s[None, None, :, None]
+    v = rng.standard_normal((b, hkv, t, d)).astype(np.float32)
+    return q, k, v
+
+
+def test_config2_reduced_gqa_prefill(nne, cuda):
+    q, k, v = _config2_inputs(1, 8, 2, 512, 128, 0x5EED0002)
+    got = host(nne.attention_forward(dev(q, cuda), dev(k, cuda), dev(v, cuda), True))
+    T.assert_close(got, T.ref_standard(q, k, v, True), what="config2 reduced")
+
+
+def test_config2_full_size_sampled_heads(nne, cuda):
+    """Full config 2 (B=4, Hq=32, Hkv=8, T=2048, d=128): every output finite,
+    causal row 0 equals V[0], and sampled heads match the oracle exactly-sized."""
+    b, hq, hkv, t, d = 4, 32, 8, 2048, 128
+    q, k, v = _config2_inputs(b, hq, hkv, t, d, 0x5EED0002)
+    out = host(nne.attention_forward(dev(q, cuda), dev(k, cuda), dev(v, cuda), True))
+    assert np.isfinite(out).all()
+    np.testing.assert_allclose(out[:, :, 0], np.repeat(v[:, :, 0], hq // hkv, axis=1),
+                               rtol=1e-6, atol=1e-6)
+    for bi, h in [(0, 0), (3, 31), (1, 13)]:
+        kv = h // (hq // hkv)
+        ref = T.ref_standard(q[bi:bi + 1, h:h + 1], k[bi:bi + 1, kv:kv + 1],
+                             v[bi:bi + 1, kv:kv + 1], True)
+        T.assert_close(out[bi:bi + 1, h:h + 1], ref, what="config2 head (%d,%d)" % (bi, h))
+
+
+def test_config4_reduced_long_causal(nne, cuda):
+    q, k, v = (rnd(0x5EED0004 + i, 1, 2, 2048, 64, std=0.5) for i in range(3))
+    got = host(nne.flash_attention_forward(dev(q, cuda), dev(k, cuda), dev(v, cuda), True))
+    T.assert_close(got, T.ref_flash(q, k, v, True), what="config4 reduced")
+
+
+def test_config5_noncausal_t1500_and_cross(nne, cuda):
+    q, k, v = (rnd(0x5EED0005 + i, 2, 2, 1500, 64) for i in range(3))
+    got = host(nne.flash_attention_forward(dev(q, cuda), dev(k, cuda), dev(v, cuda), False))
+    T.assert_close(got, T.ref_flash(q, k, v, False), what="config5a reduced")
+    qx = rnd(0x5EED0015, 2, 2, 8, 64)
+    got = host(nne.attention_forward(dev(qx, cuda), dev(k, cuda), dev(v, cuda), False))
+    T.assert_close(got, T.ref_standard(qx, k, v, False), what="config5b reduced")
+
+
+def test_linearity_in_v_full_config4_shape(nne, cuda):
+    """O is linear in V: f(a V1 + b V2) = a f(V1) + b f(V2) at T = 16384."""
+    t = 16384
+    q, k = dev(rnd(50, 1, 2, t, 64, std=0.5), cuda), dev(rnd(51, 1, 2, t, 64, std=0.5), cuda)
+    v1, v2 = dev(rnd(52, 1, 2, t, 64), cuda), dev(rnd(53, 1, 2, t, 64), cuda)
+    o1 = nne.flash_attention_forward(q, k, v1, True)
+    o2 = nne.flash_attention_forward(q, k, v2, True)
+    o3 = nne.flash_attention_forward(q, k, 0.75 * v1 - 1.5 * v2, True)
+    T.assert_close(host(o3), host(0.75 * o1 - 1.5 * o2), what="linearity")
+    # the last rows (which see every key) against the oracle
+    qn, kn, vn = host(q), host(k), host(v1)
+    ref_rows = T.ref_standard(qn[:, :, -4:], kn, vn, True, start_pos=t - 4)
+    T.assert_close(host(o1)[:, :, -4:], ref_rows, what="config4 last rows")
+
+
+def test_flash_layer_matches_composition(nne, cuda):
+    layer = nne.FlashAttention(64, 4, True, device=cuda, seed=3)
+    x = dev(rnd(60, 2, 16, 64), cuda)
+    got = host(layer(x))
+    # reference composition (flash_attention.rs:254-275) with the oracle core
+    xs = host(x)
+    def lin(p, a):
+        return a @ host(p[0]).T + host(p[1])
+    b, t, c = xs.shape
+    q = lin(layer.q_proj, xs).reshape(b, t, 4, 16).transpose(0, 2, 1, 3)
+    k = lin(layer.k_proj, xs).reshape(b, t, 4, 16).transpose(0, 2, 1, 3)
+    v = lin(layer.v_proj, xs).reshape(b, t, 4, 16).transpose(0, 2, 1, 3)
+    core = T.ref_flash(q, k, v, True).transpose(0, 2, 1, 3).reshape(b, t, c)
+    T.assert_close(got, lin(layer.out_proj, core), atol=2e-4, rtol=2e-3, what="layer")
