@@ -98,22 +98,29 @@ int nne_kv_append(float *k_cache, float *v_cache, int32_t *lens_dev, int32_t *le
                   int64_t d, int64_t t_new, void *stream);
 
 /* Device workspace bytes needed by nne_decode_attention / nne_decode_step for
- * sequences up to max_len keys (0 means none is needed). */
+ * sequences up to max_len keys (0 for invalid geometry).  It holds per-split
+ * partial results; calls that share a workspace must not overlap in time. */
 uint64_t nne_decode_workspace_bytes(int64_t B, int64_t Hq, int64_t Hkv, int64_t d, int64_t max_len);
+
 
 /* Single-token decode attention over the cache: q [B, Hq, 1, d] attends to
  * the first lens[b] rows of its sequence, no mask (llama.rs:239-296 with
- * t = 1).  Ragged lengths are allowed.  workspace may be NULL (the library
- * then allocates stream-ordered scratch) or a device buffer of at least
- * nne_decode_workspace_bytes(B, Hq, Hkv, d, max(lens_host)) bytes. */
+ * t = 1).  Ragged lengths are allowed; Hq / Hkv <= 16.  workspace may be NULL
+ * (the library then allocates stream-ordered scratch) or a device buffer of
+ * at least nne_decode_workspace_bytes(B, Hq, Hkv, d, max(lens_host)) bytes. */
 int nne_decode_attention(const float *q, const int64_t q_strides[4], const float *k_cache,
                          const float *v_cache, const int32_t *lens_dev, const int32_t *lens_host,
                          float *o, const int64_t o_strides[4], int64_t B, int64_t Hq, int64_t Hkv,
                          int64_t capacity, int64_t d, int has_scale, float scale, void *workspace,
                          uint64_t workspace_bytes, void *stream);
 
-/* One decode step: nne_kv_append of one row, then nne_decode_attention --
- * the append-then-attend order of llama.rs:239-296 and attention.rs:79-122. */
+/* One decode step with the semantics of nne_kv_append of one row followed by
+ * nne_decode_attention -- the append-then-attend order of llama.rs:239-296
+ * and attention.rs:79-122 -- fused: the new row is attended from k_new /
+ * v_new directly and stored into the cache by the attention kernel, and
+ * lens_dev / lens_host advance by one.  Workspace sized for max(lens_host) + 1
+ * keys (or NULL).
+ * NNE_ECAPACITY (nothing written) if a sequence is full. */
 int nne_decode_step(const float *q, const int64_t q_strides[4], float *k_cache, float *v_cache,
                     int32_t *lens_dev, int32_t *lens_host, const float *k_new,
                     const int64_t k_new_strides[4], const float *v_new,

@@ -249,6 +249,7 @@ class KVCache:
         return self.k[layer_idx][:, :, :L], self.v[layer_idx][:, :, :L]
 
     def workspace(self, num_heads):
+        """Decode workspace sized for full sequences (allocated once)."""
         import torch
         need = lib().nne_decode_workspace_bytes(self.batch, num_heads, self.num_kv_heads,
                                                 self.head_dim, self.capacity)

@@ -101,7 +101,8 @@ int run_attention(const float* q, const int64_t* qs_, const int64_t* qst, const 
     const bool all_visible = !causal || (int64_t)qoff >= (int64_t)Tk - 1;
     const int64_t rows = (int64_t)G * Tq;
 
-    if (vec && all_visible && rows <= nne::splitk_max_rows() && Tk > 0) {
+    if (vec && all_visible && rows <= nne::splitk_max_rows() && Tk > 0 &&
+        B <= nne::splitk_max_seqs() && (int64_t)B * Hkv * Tk < INT32_MAX) {
         nne::SplitKParams p{};
         p.q = make_view(q, qst);
         p.k = k; p.v = v;
@@ -109,21 +110,17 @@ int run_attention(const float* q, const int64_t* qs_, const int64_t* qst, const 
         p.vsb = vst[0]; p.vsh = vst[1]; p.vst = vst[2];
         p.lens = nullptr;
         p.tk = Tk;
+        p.max_keys = Tk;
         p.o = make_out(o, ost);
         p.B = B; p.Hq = Hq; p.Hkv = Hkv; p.Tq = Tq; p.d = d;
         p.qscale = scale * nne::kLog2e;
-        const int kps = nne::splitk_keys_per_split(Tk, B * Hkv);
+        const nne::SplitKWorkspace w = nne::splitk_workspace_layout(B, Hkv, (int)rows, d);
         void* ws = nullptr;
-        if (Tk > kps) {
-            const uint64_t bytes = nne::splitk_workspace_bytes(B, Hkv, (int)rows, d, Tk, kps);
-            hipError_t e = hipMallocAsync(&ws, bytes, stream);
-            if (e != hipSuccess) return hip_fail(e, "hipMallocAsync(split-K workspace)");
-        }
-        hipError_t e = nne::launch_splitk(p, Tk, kps, ws, stream);
-        if (ws) {
-            hipError_t e2 = hipFreeAsync(ws, stream);
-            if (e == hipSuccess) e = e2;
-        }
+        hipError_t e = hipMallocAsync(&ws, w.total_bytes, stream);
+        if (e != hipSuccess) return hip_fail(e, "hipMallocAsync(split-K workspace)");
+        e = nne::launch_splitk(p, (int64_t)B * Hkv * Tk, Tk, ws, stream);
+        hipError_t e2 = hipFreeAsync(ws, stream);
+        if (e == hipSuccess) e = e2;
         if (e != hipSuccess) return hip_fail(e, "split-K attention launch");
         return NNE_OK;
     }
@@ -311,17 +308,22 @@ int nne_kv_append(float* k_cache, float* v_cache, int32_t* lens_dev, int32_t* le
 }
 
 uint64_t nne_decode_workspace_bytes(int64_t B, int64_t Hq, int64_t Hkv, int64_t d, int64_t max_len) {
-    if (B <= 0 || Hkv <= 0 || Hq <= 0 || Hq % Hkv != 0 || d <= 0 || max_len <= 0) return 0;
-    const int kps = nne::splitk_keys_per_split((int)max_len, (int)(B * Hkv));
-    if (max_len <= kps) return 0;
-    return nne::splitk_workspace_bytes((int)B, (int)Hkv, (int)(Hq / Hkv), (int)d, (int)max_len, kps);
+    if (B <= 0 || Hkv <= 0 || Hq <= 0 || Hq % Hkv != 0 || d <= 0 || max_len < 0 ||
+        nne::splitk_padded_dim((int)d) == 0 || Hq / Hkv > nne::splitk_max_rows() ||
+        B > nne::splitk_max_seqs())
+        return 0;
+    return nne::splitk_workspace_layout((int)B, (int)Hkv, (int)(Hq / Hkv), (int)d).total_bytes;
 }
 
-int nne_decode_attention(const float* q, const int64_t q_strides[4], const float* k_cache,
-                         const float* v_cache, const int32_t* lens_dev, const int32_t* lens_host,
-                         float* o, const int64_t o_strides[4], int64_t B, int64_t Hq, int64_t Hkv,
-                         int64_t capacity, int64_t d, int has_scale, float scale, void* workspace,
-                         uint64_t workspace_bytes, void* stream) {
+namespace {
+
+// Shared body of nne_decode_attention and nne_decode_step.
+int run_decode(const float* q, const int64_t* q_strides, const float* k_cache, const float* v_cache,
+               const int32_t* lens_dev, int32_t* lens_dev_w, int32_t* lens_host, const float* k_new,
+               const int64_t* kn_strides, const float* v_new, const int64_t* vn_strides, float* o,
+               const int64_t* o_strides, int64_t B, int64_t Hq, int64_t Hkv, int64_t capacity,
+               int64_t d, int has_scale, float scale, void* workspace, uint64_t workspace_bytes,
+               hipStream_t s) {
     int rc = check_kv_cache_args(B, Hq, Hkv, capacity, d);
     if (rc) return rc;
     if (Hq / Hkv > nne::splitk_max_rows())
@@ -331,23 +333,45 @@ int nne_decode_attention(const float* q, const int64_t q_strides[4], const float
     if (B == 0 || Hq == 0) return NNE_OK;
     if (!lens_host)
         return fail(NNE_EINVAL, "Invalid configuration or argument: lens_host is null");
+    if (B > nne::splitk_max_seqs())
+        return fail(NNE_EINVAL, "Invalid configuration or argument: decode batch of %lld sequences "
+                                "exceeds %d", (long long)B, nne::splitk_max_seqs());
+    const bool append = k_new != nullptr;
     int max_len = 0;
+    int64_t total_keys = 0;
     for (int64_t b = 0; b < B; ++b) {
-        if (lens_host[b] < 0 || lens_host[b] > capacity)
+        const int64_t L = (int64_t)lens_host[b] + (append ? 1 : 0);
+        if (lens_host[b] < 0 || L > capacity) {
+            if (append)
+                return fail(NNE_ECAPACITY, "GPU compute error: KV cache append of 1 row to sequence "
+                                           "%lld of length %d exceeds capacity %lld",
+                            (long long)b, lens_host[b], (long long)capacity);
             return fail(NNE_EINVAL, "Invalid configuration or argument: sequence %lld length %d "
                                     "outside [0, %lld]", (long long)b, lens_host[b],
                         (long long)capacity);
-        max_len = std::max(max_len, (int)lens_host[b]);
+        }
+        max_len = std::max(max_len, (int)L);
+        total_keys += L * Hkv;
     }
+    if (total_keys >= INT32_MAX)
+        return fail(NNE_EINVAL, "Invalid configuration or argument: %lld cached rows exceed the "
+                                "decode kernel's 2^31 limit", (long long)total_keys);
     const int64_t qshape[4] = {B, Hq, 1, d};
-    int64_t c[4];
+    const int64_t kvshape[4] = {B, Hkv, 1, d};
+    int64_t c[4], ckv[4];
     contiguous_strides(qshape, c);
+    contiguous_strides(kvshape, ckv);
     const int64_t* qst = q_strides ? q_strides : c;
     const int64_t* ost = o_strides ? o_strides : c;
+    const int64_t* knst = kn_strides ? kn_strides : ckv;
+    const int64_t* vnst = vn_strides ? vn_strides : ckv;
     if (qst[3] != 1 || ost[3] != 1)
         return fail(NNE_EINVAL, "Invalid configuration or argument: decode q/o need unit dim stride");
     if (!aligned16(k_cache) || !aligned16(v_cache))
         return fail(NNE_EINVAL, "Invalid configuration or argument: KV cache must be 16-byte aligned");
+    if (append && (!vec_view(k_new, knst) || !vec_view(v_new, vnst)))
+        return fail(NNE_EINVAL, "Invalid configuration or argument: new K/V rows need unit dim "
+                                "stride, 16-byte alignment and strides that are multiples of 4");
 
     nne::SplitKParams p{};
     p.q = make_view(q, qst);
@@ -356,33 +380,52 @@ int nne_decode_attention(const float* q, const int64_t q_strides[4], const float
     p.vsb = p.ksb; p.vsh = p.ksh; p.vst = p.kst;
     p.lens = lens_dev;
     p.tk = 0;
+    p.max_keys = max_len;
     p.o = make_out(o, ost);
     p.B = (int)B; p.Hq = (int)Hq; p.Hkv = (int)Hkv; p.Tq = 1; p.d = (int)d;
     p.qscale = softmax_scale(has_scale, scale, d) * nne::kLog2e;
-    const int ml = std::max(max_len, 1);
-    const int kps = nne::splitk_keys_per_split(ml, (int)(B * Hkv));
-    const uint64_t need = ml > kps ? nne::splitk_workspace_bytes((int)B, (int)Hkv, (int)(Hq / Hkv),
-                                                                 (int)d, ml, kps)
-                                   : 0;
-    hipStream_t s = as_stream(stream);
+    if (append) {
+        p.k_new = k_new; p.v_new = v_new;
+        p.kn_sb = knst[0]; p.kn_sh = knst[1];
+        p.vn_sb = vnst[0]; p.vn_sh = vnst[1];
+        p.lens_w = lens_dev_w;
+    }
+    const nne::SplitKWorkspace w =
+        nne::splitk_workspace_layout((int)B, (int)Hkv, (int)(Hq / Hkv), (int)d);
     void* ws = workspace;
     bool owned = false;
-    if (need > 0 && !ws) {
-        hipError_t e = hipMallocAsync(&ws, need, s);
+    hipError_t e = hipSuccess;
+    if (!ws) {
+        e = hipMallocAsync(&ws, w.total_bytes, s);
         if (e != hipSuccess) return hip_fail(e, "hipMallocAsync(decode workspace)");
         owned = true;
-    } else if (need > workspace_bytes) {
+    } else if (w.total_bytes > workspace_bytes) {
         return fail(NNE_EINVAL, "Invalid configuration or argument: decode workspace of %llu bytes "
                                 "is smaller than the %llu required",
-                    (unsigned long long)workspace_bytes, (unsigned long long)need);
+                    (unsigned long long)workspace_bytes, (unsigned long long)w.total_bytes);
     }
-    hipError_t e = nne::launch_splitk(p, ml, kps, ws, s);
+    e = nne::launch_splitk(p, total_keys, max_len, ws, s);
     if (owned) {
         hipError_t e2 = hipFreeAsync(ws, s);
         if (e == hipSuccess) e = e2;
     }
     if (e != hipSuccess) return hip_fail(e, "decode attention launch");
+    if (append)
+        for (int64_t b = 0; b < B; ++b) lens_host[b] += 1;
     return NNE_OK;
+}
+
+}  // namespace
+
+int nne_decode_attention(const float* q, const int64_t q_strides[4], const float* k_cache,
+                         const float* v_cache, const int32_t* lens_dev, const int32_t* lens_host,
+                         float* o, const int64_t o_strides[4], int64_t B, int64_t Hq, int64_t Hkv,
+                         int64_t capacity, int64_t d, int has_scale, float scale, void* workspace,
+                         uint64_t workspace_bytes, void* stream) {
+    return run_decode(q, q_strides, k_cache, v_cache, lens_dev, nullptr,
+                      const_cast<int32_t*>(lens_host), nullptr, nullptr, nullptr, nullptr, o,
+                      o_strides, B, Hq, Hkv, capacity, d, has_scale, scale, workspace,
+                      workspace_bytes, as_stream(stream));
 }
 
 int nne_decode_step(const float* q, const int64_t q_strides[4], float* k_cache, float* v_cache,
@@ -392,14 +435,11 @@ int nne_decode_step(const float* q, const int64_t q_strides[4], float* k_cache, 
                     int64_t B, int64_t Hq, int64_t Hkv, int64_t capacity, int64_t d,
                     int has_scale, float scale, void* workspace, uint64_t workspace_bytes,
                     void* stream) {
-    int rc = check_kv_cache_args(B, Hq, Hkv, capacity, d);
-    if (rc) return rc;
-    rc = nne_kv_append(k_cache, v_cache, lens_dev, lens_host, k_new, k_new_strides, v_new,
-                       v_new_strides, B, Hkv, capacity, d, 1, stream);
-    if (rc) return rc;
-    return nne_decode_attention(q, q_strides, k_cache, v_cache, lens_dev, lens_host, o, o_strides,
-                                B, Hq, Hkv, capacity, d, has_scale, scale, workspace,
-                                workspace_bytes, stream);
+    if (!k_new || !v_new)
+        return fail(NNE_EINVAL, "Invalid configuration or argument: decode step needs k_new and v_new");
+    return run_decode(q, q_strides, k_cache, v_cache, lens_dev, lens_dev, lens_host, k_new,
+                      k_new_strides, v_new, v_new_strides, o, o_strides, B, Hq, Hkv, capacity, d,
+                      has_scale, scale, workspace, workspace_bytes, as_stream(stream));
 }
 
 }  // extern "C"

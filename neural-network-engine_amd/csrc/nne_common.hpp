@@ -17,6 +17,10 @@
 namespace nne {
 
 typedef float floatx16 __attribute__((ext_vector_type(16)));
+// Native 4-float vector for register tiles and 16-byte loads/stores.  (HIP's
+// float4 is a struct whose copies lower to memcpy through private memory,
+// which can keep register arrays of it out of registers.)
+typedef float vf4 __attribute__((ext_vector_type(4)));
 
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kNegInf = -__builtin_huge_valf();
@@ -59,12 +63,22 @@ struct SplitKParams {
     int64_t vsb, vsh, vst;   // V strides (dim stride 1)
     const int32_t* lens;     // per-sequence key counts (device), or null
     int tk;                  // key count when lens == null
+    int max_keys;            // host-validated upper bound on every key count
     OutView4 o;
     int B, Hq, Hkv, G, Tq, d, R;
     float qscale;            // softmax scale * log2(e)
-    int n_chunks;            // chunk slots per (b, kv head) in the workspace
-    float* ws_o;             // [B*Hkv][n_chunks][R][D] unnormalised partial O
-    float* ws_ml;            // [B*Hkv][n_chunks][R][2] partial (max, sum)
+    int n_wg;                // workgroups of the split kernel
+    int chunk;               // flattened keys per workgroup
+    // decode step only (k_new != null): the new row [B, Hkv, 1, d] is attended
+    // as key lens[b] and stored into the cache; lens_w[b] is advanced.
+    const float* k_new;
+    const float* v_new;
+    int64_t kn_sb, kn_sh, vn_sb, vn_sh;
+    int32_t* lens_w;
+    // workspace
+    int32_t* ws_pref;        // [B+1] flattened start of each sequence (this launch)
+    float* ws_ml;            // [slots][R][2] partial (max, sum); slot = workgroup + head
+    float* ws_o;             // [slots][R][D] unnormalised partial O
 };
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }

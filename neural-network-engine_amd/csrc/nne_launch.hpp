@@ -17,11 +17,19 @@ int splitk_max_rows();
 // 16-byte aligned base pointers and row/head/batch strides that are multiples of 4.
 hipError_t launch_prefill(PrefillParams p, bool causal, bool vec, hipStream_t stream);
 
-// Keys handled by one split-K workgroup for a given longest sequence and
-// number of (sequence, KV head) pairs.
-int splitk_keys_per_split(int max_len, int n_heads);
-uint64_t splitk_workspace_bytes(int B, int Hkv, int R, int d, int max_len, int keys_per_split);
-hipError_t launch_splitk(SplitKParams p, int max_len, int keys_per_split, void* workspace,
+// Split-K workspace: per-sequence prefix (B+1 ints) and partial records for
+// up to splitk_max_workgroups() + B*Hkv (workgroup, head) pairs.
+struct SplitKWorkspace {
+    uint64_t ml_offset;
+    uint64_t o_offset;
+    uint64_t total_bytes;
+};
+int splitk_max_seqs();
+int splitk_max_workgroups();
+SplitKWorkspace splitk_workspace_layout(int B, int Hkv, int R, int d);
+// Launches the split kernel over total_keys flattened (sequence, KV head, key)
+// rows, then the per-head combine kernel.  max_len bounds every sequence.
+hipError_t launch_splitk(SplitKParams p, int64_t total_keys, int max_len, void* workspace,
                          hipStream_t stream);
 
 hipError_t launch_kv_append(float* kc, float* vc, int32_t* lens_dev, View4 kn, View4 vn, int B,

@@ -8,18 +8,35 @@
 // separate B = 1 calls.
 //
 // MI355X mapping.  The work is HBM-bound (about 2 FLOP per byte of K/V), so the
-// kernel is organised around streaming each KV head's cache exactly once:
-//   * a workgroup owns one split (a run of 64-key tiles) of one
-//     (sequence, KV head) and serves all R = G * T_q query rows that read that
-//     KV head, so grouped-query sharing costs no extra HBM traffic;
-//   * K and V tiles are read with fully coalesced 16-byte loads (32 lanes per
-//     512-byte row at d = 128) and staged in LDS; the next tile's loads are
-//     issued before the current tile is computed;
-//   * per tile: scores on VALU from LDS (query rows broadcast from LDS), a
-//     one-wave-per-row online softmax, then P V accumulated in registers;
-//   * splits of one sequence are merged by a small combine kernel from
-//     partial (max, sum, O) records; single-split sequences write their output
-//     directly.
+// kernel is organised around streaming each KV head's cache exactly once and
+// keeping everything else off the critical path:
+//   * the (sequence, KV head, key) rows of the whole batch are flattened and
+//     cut into equal chunks, one per workgroup, launched as exactly one
+//     resident wave of workgroups: every CU streams the same number of bytes
+//     whatever the ragged lengths (per-head splits leave a long tail);
+//   * a workgroup serves all R = G * T_q <= 16 query rows that read a KV head,
+//     so grouped-query sharing costs no extra HBM traffic;
+//   * its 4 waves run independently over interleaved 16-key blocks (no
+//     workgroup barrier until the final merge).  Per block, on
+//     v_mfma_f32_16x16x4_f32:
+//       S^T = K Q^T  (keys x query rows; Q^T lives in registers, K is staged
+//                     through a wave-private LDS slice to reach MFMA layout),
+//       online softmax in registers: a query row's 16 scores sit in 4
+//       registers of 4 lanes, so its max / sum are 3 in-lane ops plus two
+//       lane swaps (v_permlane16_swap, v_permlane32_swap),
+//       O^T += V^T P^T (P^T register r is the B operand of step r; V is loaded
+//                     straight from HBM in operand layout, one 16-byte load
+//                     feeding four MFMAs);
+//     the next block's K and V loads are in flight while a block computes;
+//   * the 4 waves' (max, sum, O) are merged through LDS; a head covered by
+//     one workgroup is written directly, otherwise each workgroup leaves a
+//     partial record that the per-head combine kernel merges;
+//   * in a decode step the new K/V row is read straight from the caller's
+//     k_new / v_new and written into the cache by the workgroup whose split
+//     holds it; the combine kernel then advances lens[b].
+// No cross-workgroup synchronisation is used inside the split kernel: on
+// gfx950 an agent-scope fence is a whole-L2 writeback and invalidate, far more
+// expensive than the second launch.
 #include "nne_common.hpp"
 #include "nne_launch.hpp"
 
@@ -27,262 +44,375 @@ namespace nne {
 
 namespace {
 
-constexpr int KT = 64;   // keys per tile
+typedef float floatx4 __attribute__((ext_vector_type(4)));
 
-__device__ __forceinline__ float wave_max(float x) {
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) x = fmaxf(x, __shfl_xor(x, off));
-    return x;
+constexpr int KB = 16;            // keys per block (one 16x16x4 MFMA tile of keys)
+constexpr int MAX_SEQS = 2048;    // sequences per launch (prefix array in LDS)
+constexpr int MAX_PARTS = 512;    // workgroups sharing one head (combine weights in LDS)
+constexpr int MAX_WG = 2048;      // workgroups of one split launch
+
+__device__ __forceinline__ int clamp_len(int L, int max_keys) {
+    return L < 0 ? 0 : (L > max_keys ? max_keys : L);
 }
 
-__device__ __forceinline__ float wave_sum(float x) {
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) x += __shfl_xor(x, off);
-    return x;
+// Reduce over the 4 lanes {l, l^16, l^32, l^48} (rows of 16 lanes).
+__device__ __forceinline__ float quad_rows_max(float x) {
+    auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    x = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+    auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
 }
 
-template <int D, int RMAX>
-__global__ __launch_bounds__(256, 2) void splitk_kernel(const SplitKParams p, int keys_per_split) {
-    constexpr int KS = D + 4;                 // LDS row stride
-    constexpr int C4 = D / 4;                 // float4 per row
-    constexpr int NV = KT * C4 / 256;         // float4 per thread per tile
-    constexpr int NG = 256 / C4;              // key groups in the P V layout
-    constexpr int KPG = KT / NG;              // keys per group per tile
-    static_assert(4 * RMAX * D <= KT * KS, "reduction buffer must fit in the K tile");
+__device__ __forceinline__ float quad_rows_sum(float x) {
+    auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    x = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+    auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+}
 
-    __shared__ __attribute__((aligned(16))) float Ks[KT * KS];
-    __shared__ __attribute__((aligned(16))) float Vs[KT * KS];
-    __shared__ __attribute__((aligned(16))) float qs[RMAX * D];
-    __shared__ float sc[RMAX * KT];
-    __shared__ float m_run[RMAX], l_run[RMAX], alph[RMAX];
+// Orders this wave's LDS accesses on both sides of a cross-lane exchange.
+__device__ __forceinline__ void wave_lds_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
 
-    const int head = blockIdx.x / p.n_chunks;
-    const int split = blockIdx.x % p.n_chunks;
-    const int bi = head / p.Hkv, kvh = head % p.Hkv;
-    const int L = p.lens ? p.lens[bi] : p.tk;
-    const int key_begin = split * keys_per_split;
-    if (key_begin >= L) return;
-    const int key_end = min(L, key_begin + keys_per_split);
-    const int n_splits = (L + keys_per_split - 1) / keys_per_split;
-    const int n_tiles = (key_end - key_begin + KT - 1) / KT;
+// Flattened key space: head h = b*Hkv + kvh owns keys [pref[b] + kvh*L_b,
+// pref[b] + (kvh+1)*L_b) where pref[b] = Hkv * sum_{b' < b} L_b'.  Workgroup w
+// takes [w*chunk, (w+1)*chunk): every workgroup streams the same number of
+// K/V rows, whatever the ragged lengths, and a range may span several heads.
 
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+// Key count of sequence b in this launch (the cached rows, plus the new row
+// in a decode step), clamped to what the host validated.
+template <bool APPEND>
+__device__ __forceinline__ int seq_len(const SplitKParams& p, int b) {
+    if (!p.lens) return p.tk;
+    const int L_old = clamp_len(p.lens[b], p.max_keys);
+    return APPEND ? clamp_len(L_old + 1, p.max_keys) : L_old;
+}
 
-    // Query rows -> LDS, pre-scaled by scale*log2(e).
-    for (int e = tid; e < RMAX * D; e += 256) {
-        const int rr = e / D, dd = e % D;
-        float x = 0.f;
-        if (rr < p.R && dd < p.d) {
-            const int hq = kvh * p.G + rr / p.Tq, t = rr % p.Tq;
-            x = p.q.p[bi * p.q.sb + hq * p.q.sh + t * p.q.st + dd] * p.qscale;
-        }
-        qs[e] = x;
-    }
-    if (tid < RMAX) { m_run[tid] = kNegInf; l_run[tid] = 0.f; }
-
-    const float* kb = p.k + bi * p.ksb + kvh * p.ksh;
-    const float* vb = p.v + bi * p.vsb + kvh * p.vsh;
-
-    // Tile loads: float4 index tid + 256*i -> (row, col4).
-    float4 kr[NV], vr[NV];
-    auto load_tile = [&](int key0) {
+// Builds pref[0..B] in LDS with wave 0 (a wave-wide scan per 64 sequences).
+template <bool APPEND>
+__device__ __forceinline__ void build_prefix(const SplitKParams& p, int* pref, int lane, int wave) {
+    if (wave == 0) {
+        int carry = 0;
+        if (lane == 0) pref[0] = 0;
+        for (int base = 0; base < p.B; base += 64) {
+            const int b = base + lane;
+            int x = b < p.B ? p.Hkv * seq_len<APPEND>(p, b) : 0;
 #pragma unroll
-        for (int i = 0; i < NV; ++i) {
-            const int idx = tid + 256 * i;
-            const int row = idx / C4, c = (idx % C4) * 4;
-            const int key = key0 + row;
-            const bool ok = key < key_end && c < p.d;
-            kr[i] = ok ? *reinterpret_cast<const float4*>(kb + key * p.kst + c)
-                       : make_float4(0.f, 0.f, 0.f, 0.f);
-            vr[i] = ok ? *reinterpret_cast<const float4*>(vb + key * p.vst + c)
-                       : make_float4(0.f, 0.f, 0.f, 0.f);
-        }
-    };
-
-    const int c4 = tid % C4, kg = tid / C4;   // P V layout
-    float4 o[RMAX];
-#pragma unroll
-    for (int rr = 0; rr < RMAX; ++rr) o[rr] = make_float4(0.f, 0.f, 0.f, 0.f);
-
-    load_tile(key_begin);
-    for (int it = 0; it < n_tiles; ++it) {
-        const int key0 = key_begin + it * KT;
-#pragma unroll
-        for (int i = 0; i < NV; ++i) {
-            const int idx = tid + 256 * i;
-            const int row = idx / C4, c = (idx % C4) * 4;
-            *reinterpret_cast<float4*>(Ks + row * KS + c) = kr[i];
-            *reinterpret_cast<float4*>(Vs + row * KS + c) = vr[i];
-        }
-        __syncthreads();
-        if (it + 1 < n_tiles) load_tile(key0 + KT);
-
-        // Scores: thread -> key kk, rows wave + 4j.
-        {
-            const int kk = tid % KT;
-            const int rg = tid / KT;
-            float acc[RMAX / 4];
-#pragma unroll
-            for (int j = 0; j < RMAX / 4; ++j) acc[j] = 0.f;
-            const float* krow = Ks + kk * KS;
-#pragma unroll 8
-            for (int c = 0; c < D; c += 4) {
-                const float4 kv = *reinterpret_cast<const float4*>(krow + c);
-#pragma unroll
-                for (int j = 0; j < RMAX / 4; ++j) {
-                    const float4 qv = *reinterpret_cast<const float4*>(qs + (rg + 4 * j) * D + c);
-                    acc[j] += kv.x * qv.x + kv.y * qv.y + kv.z * qv.z + kv.w * qv.w;
-                }
+            for (int off = 1; off < 64; off <<= 1) {
+                const int y = __shfl_up(x, off);
+                if (lane >= off) x += y;
             }
-            const bool kvis = key0 + kk < key_end;
-#pragma unroll
-            for (int j = 0; j < RMAX / 4; ++j) {
-                const int rr = rg + 4 * j;
-                if (rr < p.R) sc[rr * KT + kk] = kvis ? acc[j] : kNegInf;
-            }
-        }
-        __syncthreads();
-
-        // Online softmax, one wave per row (64 keys = 64 lanes).
-        for (int rr = wave; rr < p.R; rr += 4) {
-            const float x = sc[rr * KT + lane];
-            const float mt = wave_max(x);
-            const float m_old = m_run[rr];
-            const float m_new = fmaxf(m_old, mt);
-            const float m_use = (m_new == kNegInf) ? 0.f : m_new;
-            const float pv = fast_exp2(x - m_use);
-            sc[rr * KT + lane] = pv;
-            const float ls = wave_sum(pv);
-            if (lane == 0) {
-                const float alpha = fast_exp2(m_old - m_use);
-                alph[rr] = alpha;
-                l_run[rr] = alpha * l_run[rr] + ls;
-                m_run[rr] = m_new;
-            }
-        }
-        __syncthreads();
-
-        // O += P V for this thread's 4 dims over its key group.
-#pragma unroll
-        for (int rr = 0; rr < RMAX; ++rr) {
-            if (rr < p.R) {
-                const float a = alph[rr];
-                o[rr].x *= a; o[rr].y *= a; o[rr].z *= a; o[rr].w *= a;
-            }
-        }
-#pragma unroll
-        for (int i = 0; i < KPG; ++i) {
-            const int key = kg + NG * i;
-            const float4 v4 = *reinterpret_cast<const float4*>(Vs + key * KS + 4 * c4);
-#pragma unroll
-            for (int rr = 0; rr < RMAX; ++rr) {
-                if (rr < p.R) {
-                    const float pv = sc[rr * KT + key];
-                    o[rr].x += pv * v4.x; o[rr].y += pv * v4.y;
-                    o[rr].z += pv * v4.z; o[rr].w += pv * v4.w;
-                }
-            }
-        }
-        __syncthreads();
-    }
-
-    // Reduce O over key groups: first inside the wave (lanes differing in the
-    // bits above log2(C4)), then across the 4 waves through LDS.
-#pragma unroll
-    for (int off = C4; off < 64; off <<= 1) {
-#pragma unroll
-        for (int rr = 0; rr < RMAX; ++rr) {
-            o[rr].x += __shfl_xor(o[rr].x, off);
-            o[rr].y += __shfl_xor(o[rr].y, off);
-            o[rr].z += __shfl_xor(o[rr].z, off);
-            o[rr].w += __shfl_xor(o[rr].w, off);
+            if (b < p.B) pref[b + 1] = carry + x;
+            carry += __shfl(x, 63);
         }
     }
-    float* red = Ks;   // [4 waves][RMAX][D]
-    if (lane < C4) {
-#pragma unroll
-        for (int rr = 0; rr < RMAX; ++rr)
-            *reinterpret_cast<float4*>(red + (wave * RMAX + rr) * D + 4 * c4) = o[rr];
-    }
+}
+
+template <int D, bool APPEND>
+__global__ __launch_bounds__(256, 2) void splitk_kernel(const SplitKParams p) {
+    constexpr int KS = D + 4;            // LDS row stride (16-byte reads conflict-free)
+    constexpr int LPR = D / 4;           // lanes per K row in the coalesced load
+    constexpr int RPI = 64 / LPR;        // K rows per load instruction
+    constexpr int NK = KB / RPI;         // K float4 loads per lane per block
+    constexpr int NH = D / 64;           // V float4 loads per key step
+    constexpr int NQ = D / 4;            // Q^T registers per lane
+    constexpr int NB = D / 16;           // 16-dim output blocks
+    static_assert(4 * 16 * D <= 4 * KB * KS, "merge buffer must fit in the K slices");
+
+    __shared__ __attribute__((aligned(16))) float lds[4 * KB * KS];
+    __shared__ float ml_s[4][16][2];
+    __shared__ int pref[MAX_SEQS + 1];
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    // Wave index as a scalar: keeps the per-wave block loop uniform, so the
+    // compiler neither masks it nor drains the prefetched loads at its head.
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int col = lane & 15, grp = lane >> 4;
+    const int wg = blockIdx.x;
+
+    build_prefix<APPEND>(p, pref, lane, wave);
     __syncthreads();
+    if (wg == 0)   // snapshot for the combine kernel (lens may advance meanwhile)
+        for (int b = tid; b <= p.B; b += 256) p.ws_pref[b] = pref[b];
 
-    const bool direct = n_splits == 1;
-    for (int e = tid; e < p.R * D; e += 256) {
-        const int rr = e / D, dd = e % D;
-        const float acc = red[(0 * RMAX + rr) * D + dd] + red[(1 * RMAX + rr) * D + dd] +
-                          red[(2 * RMAX + rr) * D + dd] + red[(3 * RMAX + rr) * D + dd];
-        if (direct) {
-            if (dd < p.d) {
-                const int hq = kvh * p.G + rr / p.Tq, t = rr % p.Tq;
-                const float l = l_run[rr];
-                p.o.p[bi * p.o.sb + hq * p.o.sh + t * p.o.st + dd] = l > 0.f ? acc / l : 0.f;
-            }
-        } else {
-            p.ws_o[((int64_t)(head * p.n_chunks + split) * p.R + rr) * D + dd] = acc;
+    const int total = pref[p.B];
+    int g = wg * p.chunk;
+    const int g_end = min(total, g + p.chunk);
+    if (g >= g_end) return;
+    // first sequence whose keys reach past g
+    int b = 0;
+    {
+        int lo = 0, hi = p.B - 1;
+        while (lo < hi) {
+            const int mid = (lo + hi + 1) >> 1;
+            if (pref[mid] <= g) lo = mid; else hi = mid - 1;
         }
+        b = lo;
     }
-    if (!direct && tid < p.R) {
-        float* ml = p.ws_ml + ((int64_t)(head * p.n_chunks + split) * p.R + tid) * 2;
-        ml[0] = m_run[tid];
-        ml[1] = l_run[tid];
+
+    float* Kw = lds + wave * KB * KS;    // this wave's K slice
+    int v_col[NH];
+#pragma unroll
+    for (int h = 0; h < NH; ++h) v_col[h] = min(64 * h + 4 * col, p.d - 4);
+    const int kc_col = min(4 * (lane % LPR), p.d - 4);
+
+    while (g < g_end) {
+        const int Lb = (pref[b + 1] - pref[b]) / p.Hkv;
+        if (Lb == 0 || g >= pref[b + 1]) { ++b; continue; }
+        const int kvh = (g - pref[b]) / Lb;
+        const int h_start = pref[b] + kvh * Lb;
+        const int key_begin = g - h_start;
+        const int key_end = min(g_end, h_start + Lb) - h_start;
+        const int head = b * p.Hkv + kvh;
+        const bool whole = key_begin == 0 && key_end == Lb;
+
+        const float* kb = p.k + b * p.ksb + kvh * p.ksh;
+        const float* vb = p.v + b * p.vsb + kvh * p.vsh;
+
+        // Decode step: the segment holding the new row (key Lb - 1) stores it
+        // into the cache first and then reads it back like any cached row.
+        if (APPEND && key_end == Lb) {
+            const int row = Lb - 1;
+            if (tid < D / 4 && 4 * tid < p.d) {
+                const float* knb = p.k_new + b * p.kn_sb + kvh * p.kn_sh;
+                const float* vnb = p.v_new + b * p.vn_sb + kvh * p.vn_sh;
+                *reinterpret_cast<vf4*>(const_cast<float*>(kb) + (int64_t)row * p.kst + 4 * tid) =
+                    *reinterpret_cast<const vf4*>(knb + 4 * tid);
+                *reinterpret_cast<vf4*>(const_cast<float*>(vb) + (int64_t)row * p.vst + 4 * tid) =
+                    *reinterpret_cast<const vf4*>(vnb + 4 * tid);
+            }
+            __syncthreads();
+        }
+
+        // Q^T fragment: lane holds query row `col`, dims grp*D/4 .. +D/4, pre-scaled.
+        float qf[NQ];
+        {
+            const bool rok = col < p.R;
+            const int hq = kvh * p.G + (rok ? col / p.Tq : 0), t = rok ? col % p.Tq : 0;
+            const float* qp = p.q.p + b * p.q.sb + hq * p.q.sh + t * p.q.st;
+#pragma unroll
+            for (int s4 = 0; s4 < NQ / 4; ++s4) {
+                const int c = grp * NQ + 4 * s4;
+                vf4 x = (rok && c < p.d) ? *reinterpret_cast<const vf4*>(qp + c) : vf4{0.f, 0.f, 0.f, 0.f};
+                qf[4 * s4 + 0] = x.x * p.qscale;
+                qf[4 * s4 + 1] = x.y * p.qscale;
+                qf[4 * s4 + 2] = x.z * p.qscale;
+                qf[4 * s4 + 3] = x.w * p.qscale;
+            }
+        }
+
+        // Keys past the segment end are clamped to its last row (their scores
+        // are masked to -inf, so the finite data gets weight 0); columns past d
+        // read the row's last 4 floats (their Q columns are zero, their O
+        // columns are never stored).  Loads are branch-free, so the next block
+        // stays in flight while the current one computes.
+        auto load_block = [&](vf4 (&kr)[NK], vf4 (&vr)[4 * NH], int kb0) __attribute__((always_inline)) {
+#pragma unroll
+            for (int i = 0; i < NK; ++i) {
+                const int key = min(kb0 + lane / LPR + RPI * i, key_end - 1);
+                kr[i] = *reinterpret_cast<const vf4*>(kb + (int64_t)key * p.kst + kc_col);
+            }
+#pragma unroll
+            for (int st = 0; st < 4; ++st) {
+                const int key = min(kb0 + 4 * grp + st, key_end - 1);
+#pragma unroll
+                for (int h = 0; h < NH; ++h)
+                    vr[st * NH + h] = *reinterpret_cast<const vf4*>(vb + (int64_t)key * p.vst + v_col[h]);
+            }
+        };
+
+        floatx4 o[NB];
+#pragma unroll
+        for (int bb = 0; bb < NB; ++bb) o[bb] = floatx4{0.f, 0.f, 0.f, 0.f};
+        float m_run = kNegInf, l_run = 0.f;
+
+        // One 16-key block: stage K, S^T = K Q^T, online softmax, O^T += V^T P^T.
+        auto block = [&](const vf4 (&kr)[NK], const vf4 (&vr)[4 * NH], int kb0) __attribute__((always_inline)) {
+            wave_lds_sync();
+#pragma unroll
+            for (int i = 0; i < NK; ++i)
+                *reinterpret_cast<vf4*>(Kw + (lane / LPR + RPI * i) * KS + 4 * (lane % LPR)) = kr[i];
+            wave_lds_sync();
+
+            floatx4 s = floatx4{0.f, 0.f, 0.f, 0.f};
+            const float* krow = Kw + col * KS + grp * NQ;
+#pragma unroll
+            for (int t = 0; t < NQ / 4; ++t) {
+                const vf4 kq = *reinterpret_cast<const vf4*>(krow + 4 * t);
+                s = __builtin_amdgcn_mfma_f32_16x16x4f32(kq.x, qf[4 * t + 0], s, 0, 0, 0);
+                s = __builtin_amdgcn_mfma_f32_16x16x4f32(kq.y, qf[4 * t + 1], s, 0, 0, 0);
+                s = __builtin_amdgcn_mfma_f32_16x16x4f32(kq.z, qf[4 * t + 2], s, 0, 0, 0);
+                s = __builtin_amdgcn_mfma_f32_16x16x4f32(kq.w, qf[4 * t + 3], s, 0, 0, 0);
+            }
+            // s[r] = score of key kb0 + 4*grp + r for query row `col`.
+            if (kb0 + KB > key_end) {
+#pragma unroll
+                for (int r = 0; r < 4; ++r) s[r] = (kb0 + 4 * grp + r < key_end) ? s[r] : kNegInf;
+            }
+            float mt = fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3]));
+            mt = quad_rows_max(mt);
+            const float m_new = fmaxf(m_run, mt);
+            const float m_use = (m_new == kNegInf) ? 0.f : m_new;
+            const float alpha = fast_exp2(m_run - m_use);
+            float ls = 0.f;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                s[r] = fast_exp2(s[r] - m_use);
+                ls += s[r];
+            }
+            l_run = alpha * l_run + ls;     // this lane's 4 keys; summed over lanes below
+            m_run = m_new;
+#pragma unroll
+            for (int bb = 0; bb < NB; ++bb) o[bb] *= alpha;
+
+            // O^T += V^T P^T.  Step st pairs key kb0 + 4*grp + st (= register st
+            // of P^T); dim block 4h + c covers dims 64h + 4*i + c, i = lane % 16.
+#pragma unroll
+            for (int st = 0; st < 4; ++st)
+#pragma unroll
+                for (int h = 0; h < NH; ++h) {
+                    const vf4 vv = vr[st * NH + h];
+                    o[4 * h + 0] = __builtin_amdgcn_mfma_f32_16x16x4f32(vv.x, s[st], o[4 * h + 0], 0, 0, 0);
+                    o[4 * h + 1] = __builtin_amdgcn_mfma_f32_16x16x4f32(vv.y, s[st], o[4 * h + 1], 0, 0, 0);
+                    o[4 * h + 2] = __builtin_amdgcn_mfma_f32_16x16x4f32(vv.z, s[st], o[4 * h + 2], 0, 0, 0);
+                    o[4 * h + 3] = __builtin_amdgcn_mfma_f32_16x16x4f32(vv.w, s[st], o[4 * h + 3], 0, 0, 0);
+                }
+        };
+
+        // Ping-pong over this wave's blocks (wave, wave+4, ...): while one
+        // block computes, the next one's loads are in flight.
+        const int n_blocks = (key_end - key_begin + KB - 1) / KB;
+        vf4 ka[NK], va[4 * NH], kb2[NK], vb2[4 * NH];
+        load_block(ka, va, key_begin + wave * KB);
+        for (int blk = wave; blk < n_blocks; blk += 8) {
+            const int kb0 = key_begin + blk * KB;
+            load_block(kb2, vb2, kb0 + 4 * KB);
+            block(ka, va, kb0);
+            if (blk + 4 >= n_blocks) break;
+            load_block(ka, va, kb0 + 8 * KB);
+            block(kb2, vb2, kb0 + 4 * KB);
+        }
+        const float l_tot = quad_rows_sum(l_run);
+
+        // Merge the 4 waves through LDS: O[row col][dim] with
+        // dim = 64h + 16*grp + 4*reg + c  for  o[4h + c][reg].
+        __syncthreads();                  // every wave is done with its K slice
+        float* ob = lds;                  // [4 waves][16 rows][D]
+#pragma unroll
+        for (int h = 0; h < NH; ++h)
+#pragma unroll
+            for (int reg = 0; reg < 4; ++reg)
+                *reinterpret_cast<vf4*>(ob + (wave * 16 + col) * D + 64 * h + 16 * grp + 4 * reg) =
+                    vf4{o[4 * h + 0][reg], o[4 * h + 1][reg], o[4 * h + 2][reg], o[4 * h + 3][reg]};
+        if (grp == 0) { ml_s[wave][col][0] = m_run; ml_s[wave][col][1] = l_tot; }
+        __syncthreads();
+
+        const int64_t slot = (int64_t)wg + head;    // unique per (workgroup, head)
+        for (int e = tid; e < p.R * D; e += 256) {
+            const int rr = e / D, dd = e % D;
+            float M = kNegInf;
+#pragma unroll
+            for (int w = 0; w < 4; ++w) M = fmaxf(M, ml_s[w][rr][0]);
+            const float M_use = M == kNegInf ? 0.f : M;
+            float l = 0.f, acc = 0.f;
+#pragma unroll
+            for (int w = 0; w < 4; ++w) {
+                const float f = fast_exp2(ml_s[w][rr][0] - M_use);
+                l += f * ml_s[w][rr][1];
+                acc += f * ob[(w * 16 + rr) * D + dd];
+            }
+            if (whole) {
+                if (dd < p.d) {
+                    const int hq = kvh * p.G + rr / p.Tq, t = rr % p.Tq;
+                    p.o.p[b * p.o.sb + hq * p.o.sh + t * p.o.st + dd] = l > 0.f ? acc / l : 0.f;
+                }
+            } else {
+                p.ws_o[(slot * p.R + rr) * D + dd] = acc;
+                if (dd == 0) {
+                    p.ws_ml[(slot * p.R + rr) * 2] = M;
+                    p.ws_ml[(slot * p.R + rr) * 2 + 1] = l;
+                }
+            }
+        }
+        __syncthreads();                  // LDS is reused by the next segment
+        g = h_start + key_end;
     }
 }
 
-// Merges the per-split partials of one (sequence, KV head, row).
+// Per (sequence, KV head): zero output for an empty sequence, merge the
+// partial records of the workgroups that shared the head, and in a decode step
+// publish the sequence's new length.
 template <int D>
-__global__ __launch_bounds__(64) void splitk_combine_kernel(const SplitKParams p, int keys_per_split) {
-    const int item = blockIdx.x;             // (head, rr)
-    const int head = item / p.R, rr = item % p.R;
-    const int bi = head / p.Hkv, kvh = head % p.Hkv;
-    const int L = p.lens ? p.lens[bi] : p.tk;
-    const int n = (L + keys_per_split - 1) / keys_per_split;
-    if (n == 1) return;                      // written directly by the split kernel
-    const int hq = kvh * p.G + rr / p.Tq, t = rr % p.Tq;
-    float* op = p.o.p + bi * p.o.sb + hq * p.o.sh + t * p.o.st;
-    if (n == 0) {                            // empty sequence: output stays zero
-        for (int dd = threadIdx.x; dd < p.d; dd += 64) op[dd] = 0.f;
+__global__ __launch_bounds__(256) void splitk_combine_kernel(const SplitKParams p) {
+    __shared__ float w_s[MAX_PARTS][16];
+    const int head = blockIdx.x;
+    const int b = head / p.Hkv, kvh = head % p.Hkv;
+    const int tid = threadIdx.x;
+    const int p0 = p.ws_pref[b], p1 = p.ws_pref[b + 1];
+    const int Lb = (p1 - p0) / p.Hkv;
+    if (p.lens_w && kvh == 0 && tid == 0) p.lens_w[b] = Lb;
+    auto out_ptr = [&](int rr) {
+        const int hq = kvh * p.G + rr / p.Tq, t = rr % p.Tq;
+        return p.o.p + b * p.o.sb + hq * p.o.sh + t * p.o.st;
+    };
+    if (Lb == 0) {
+        for (int e = tid; e < p.R * p.d; e += 256) out_ptr(e / p.d)[e % p.d] = 0.f;
         return;
     }
-    const float* ml = p.ws_ml + ((int64_t)head * p.n_chunks * p.R + rr) * 2;
-    float M = kNegInf;
-    for (int c = 0; c < n; ++c) M = fmaxf(M, ml[(int64_t)c * p.R * 2]);
-    const float M_use = M == kNegInf ? 0.f : M;
-    float den = 0.f;
-    for (int c = 0; c < n; ++c)
-        den += fast_exp2(ml[(int64_t)c * p.R * 2] - M_use) * ml[(int64_t)c * p.R * 2 + 1];
-    const float inv = den > 0.f ? 1.f / den : 0.f;
-    const float* wo = p.ws_o + ((int64_t)head * p.n_chunks * p.R + rr) * D;
-    for (int dd = threadIdx.x; dd < p.d; dd += 64) {
-        float acc = 0.f;
+    const int h_start = p0 + kvh * Lb;
+    const int w_first = h_start / p.chunk, w_last = (h_start + Lb - 1) / p.chunk;
+    const int n = w_last - w_first + 1;
+    if (n <= 1) return;                   // written directly by the split kernel
+    const int64_t s0 = (int64_t)w_first + head;   // slots s0 .. s0 + n - 1
+    for (int e = tid; e < n * p.R; e += 256) {
+        const int c = e / p.R, rr = e % p.R;
+        w_s[c][rr] = p.ws_ml[((s0 + c) * p.R + rr) * 2];
+    }
+    __syncthreads();
+    if (tid < p.R) {
+        float M = kNegInf;
+        for (int c = 0; c < n; ++c) M = fmaxf(M, w_s[c][tid]);
+        const float M_use = M == kNegInf ? 0.f : M;
+        float den = 0.f;
         for (int c = 0; c < n; ++c)
-            acc += fast_exp2(ml[(int64_t)c * p.R * 2] - M_use) * wo[(int64_t)c * p.R * D + dd];
-        op[dd] = acc * inv;
+            den += fast_exp2(w_s[c][tid] - M_use) * p.ws_ml[((s0 + c) * p.R + tid) * 2 + 1];
+        const float inv = den > 0.f ? 1.f / den : 0.f;
+        for (int c = 0; c < n; ++c) w_s[c][tid] = fast_exp2(w_s[c][tid] - M_use) * inv;
+    }
+    __syncthreads();
+    for (int e = tid; e < p.R * p.d; e += 256) {
+        const int rr = e / p.d, dd = e % p.d;
+        const float* src = p.ws_o + (s0 * p.R + rr) * D + dd;
+        float acc = 0.f;
+        int c = 0;
+        for (; c + 4 <= n; c += 4) {
+            const float a0 = src[(int64_t)(c + 0) * p.R * D], a1 = src[(int64_t)(c + 1) * p.R * D];
+            const float a2 = src[(int64_t)(c + 2) * p.R * D], a3 = src[(int64_t)(c + 3) * p.R * D];
+            acc += w_s[c][rr] * a0 + w_s[c + 1][rr] * a1 + w_s[c + 2][rr] * a2 + w_s[c + 3][rr] * a3;
+        }
+        for (; c < n; ++c) acc += w_s[c][rr] * src[(int64_t)c * p.R * D];
+        out_ptr(rr)[dd] = acc;
     }
 }
 
-template <int D, int RMAX>
-hipError_t launch_splitk_t(const SplitKParams& p, int keys_per_split, hipStream_t stream) {
-    const int grid = p.B * p.Hkv * p.n_chunks;
-    if (grid > 0)
-        hipLaunchKernelGGL((splitk_kernel<D, RMAX>), dim3(grid), dim3(256), 0, stream, p,
-                           keys_per_split);
-    hipError_t e = hipGetLastError();
-    if (e != hipSuccess) return e;
-    const int cgrid = p.B * p.Hkv * p.R;
-    if (cgrid > 0)
-        hipLaunchKernelGGL((splitk_combine_kernel<D>), dim3(cgrid), dim3(64), 0, stream, p,
-                           keys_per_split);
+template <int D>
+hipError_t launch_splitk_d(const SplitKParams& p, hipStream_t stream) {
+    if (p.n_wg > 0) {
+        if (p.k_new)
+            hipLaunchKernelGGL((splitk_kernel<D, true>), dim3(p.n_wg), dim3(256), 0, stream, p);
+        else
+            hipLaunchKernelGGL((splitk_kernel<D, false>), dim3(p.n_wg), dim3(256), 0, stream, p);
+        hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+    }
+    hipLaunchKernelGGL((splitk_combine_kernel<D>), dim3(p.B * p.Hkv), dim3(256), 0, stream, p);
     return hipGetLastError();
 }
 
-template <int D>
-hipError_t launch_splitk_d(const SplitKParams& p, int kps, hipStream_t stream) {
-    if (p.R <= 4) return launch_splitk_t<D, 4>(p, kps, stream);
-    if (p.R <= 8) return launch_splitk_t<D, 8>(p, kps, stream);
-    return launch_splitk_t<D, 16>(p, kps, stream);
-}
-
-// ---- KV append --------------------------------------------------------------
+// ---- KV append (prefill-style, many rows) ---------------------------------
 
 // Writes new rows [B, Hkv, t_new, d] at row lens[b] + t of each (b, kv head).
 __global__ void kv_append_kernel(float* kc, float* vc, const int32_t* lens, View4 kn, View4 vn,
@@ -295,7 +425,9 @@ __global__ void kv_append_kernel(float* kc, float* vc, const int32_t* lens, View
         const int t = r % t_new; r /= t_new;
         const int h = r % Hkv;
         const int b = r / Hkv;
-        const int64_t dst = (((int64_t)b * Hkv + h) * cap + lens[b] + t) * d + dd;
+        const int row = lens[b] + t;
+        if (row < 0 || row >= cap) continue;   // host validated; never taken when consistent
+        const int64_t dst = (((int64_t)b * Hkv + h) * cap + row) * d + dd;
         kc[dst] = kn.p[b * kn.sb + h * kn.sh + t * kn.st + dd * kn.sd];
         vc[dst] = vn.p[b * vn.sb + h * vn.sh + t * vn.st + dd * vn.sd];
     }
@@ -309,44 +441,77 @@ __global__ void lens_bump_kernel(int32_t* lens, int B, int t_new) {
 }  // namespace
 
 int splitk_padded_dim(int d) {
-    if (d <= 32) return 32;
     if (d <= 64) return 64;
     if (d <= 128) return 128;
     return 0;
 }
 
 int splitk_max_rows() { return 16; }
+int splitk_max_seqs() { return MAX_SEQS; }
+int splitk_max_workgroups() { return MAX_WG; }
 
-int splitk_keys_per_split(int max_len, int n_heads) {
-    // Enough splits to give each of the 256 CUs several workgroups, in whole
-    // 64-key tiles; at least 4 tiles per split so partials stay a small
-    // fraction of the K/V bytes.
-    int tiles = (max_len + KT - 1) / KT;
-    int want_splits = (4 * 256 + n_heads - 1) / (n_heads > 0 ? n_heads : 1);
-    int tps = (tiles + want_splits - 1) / (want_splits > 0 ? want_splits : 1);
-    if (tps < 4) tps = 4;
-    return tps * KT;
-}
-
-uint64_t splitk_workspace_bytes(int B, int Hkv, int R, int d, int max_len, int keys_per_split) {
+SplitKWorkspace splitk_workspace_layout(int B, int Hkv, int R, int d) {
+    SplitKWorkspace w;
     const int D = splitk_padded_dim(d);
-    const int n_chunks = (max_len + keys_per_split - 1) / keys_per_split;
-    return (uint64_t)B * Hkv * (n_chunks > 0 ? n_chunks : 1) * R * (D + 2) * sizeof(float);
+    const uint64_t slots = (uint64_t)MAX_WG + (uint64_t)B * Hkv;
+    w.ml_offset = ((uint64_t)(B + 1) * 4 + 255) / 256 * 256;
+    w.o_offset = w.ml_offset + (slots * R * 2 * 4 + 255) / 256 * 256;
+    w.total_bytes = w.o_offset + slots * R * D * 4;
+    return w;
 }
 
-hipError_t launch_splitk(SplitKParams p, int max_len, int keys_per_split, void* workspace,
+namespace {
+
+// Resident workgroups of the split kernel on the current device: one full
+// wave of them covers the flattened key range exactly once.
+template <int D, bool APPEND>
+int resident_workgroups() {
+    static int cached[64] = {0};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
+    if (cached[dev] == 0) {
+        int cus = 0, per_cu = 0;
+        if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+            cus = 256;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, splitk_kernel<D, APPEND>, 256, 0) !=
+                hipSuccess || per_cu < 1)
+            per_cu = 1;
+        int n = cus * per_cu;
+        cached[dev] = n < MAX_WG ? n : MAX_WG;
+    }
+    return cached[dev];
+}
+
+template <int D>
+hipError_t launch_flat(SplitKParams p, int64_t total_keys, int max_len, hipStream_t stream) {
+    const int slots = p.k_new ? resident_workgroups<D, true>() : resident_workgroups<D, false>();
+    // Equal flattened chunks, whole 16-key blocks, and at most MAX_PARTS - 2
+    // workgroups sharing any one head.
+    int64_t chunk = (total_keys + slots - 1) / (slots > 0 ? slots : 1);
+    const int64_t min_chunk = (max_len + (MAX_PARTS - 2) - 1) / (MAX_PARTS - 2);
+    if (chunk < min_chunk) chunk = min_chunk;
+    chunk = (chunk + KB - 1) / KB * KB;
+    if (chunk < KB) chunk = KB;
+    p.chunk = (int)chunk;
+    int64_t n_wg = (total_keys + chunk - 1) / chunk;
+    p.n_wg = (int)(n_wg < 1 ? 1 : n_wg);
+    return launch_splitk_d<D>(p, stream);
+}
+
+}  // namespace
+
+hipError_t launch_splitk(SplitKParams p, int64_t total_keys, int max_len, void* workspace,
                          hipStream_t stream) {
     p.G = p.Hq / p.Hkv;
     p.R = p.G * p.Tq;
-    p.n_chunks = (max_len + keys_per_split - 1) / keys_per_split;
-    if (p.n_chunks < 1) p.n_chunks = 1;
-    const int D = splitk_padded_dim(p.d);
-    p.ws_o = static_cast<float*>(workspace);
-    p.ws_ml = p.ws_o + (int64_t)p.B * p.Hkv * p.n_chunks * p.R * D;
-    switch (D) {
-        case 32: return launch_splitk_d<32>(p, keys_per_split, stream);
-        case 64: return launch_splitk_d<64>(p, keys_per_split, stream);
-        case 128: return launch_splitk_d<128>(p, keys_per_split, stream);
+    const SplitKWorkspace w = splitk_workspace_layout(p.B, p.Hkv, p.R, p.d);
+    char* base = static_cast<char*>(workspace);
+    p.ws_pref = reinterpret_cast<int32_t*>(base);
+    p.ws_ml = reinterpret_cast<float*>(base + w.ml_offset);
+    p.ws_o = reinterpret_cast<float*>(base + w.o_offset);
+    switch (splitk_padded_dim(p.d)) {
+        case 64: return launch_flat<64>(p, total_keys, max_len, stream);
+        case 128: return launch_flat<128>(p, total_keys, max_len, stream);
         default: return hipErrorInvalidValue;
     }
 }

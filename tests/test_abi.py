@@ -94,12 +94,24 @@ def test_decode_rejects_bad_geometry(nne):
 
 def test_decode_workspace_size(nne):
     lib = nne.lib()
-    assert lib.nne_decode_workspace_bytes(1, 4, 4, 64, 0) == 0
     assert lib.nne_decode_workspace_bytes(1, 4, 3, 64, 100) == 0   # 3 does not divide 4
-    small = lib.nne_decode_workspace_bytes(32, 32, 8, 128, 256)
+    assert lib.nne_decode_workspace_bytes(1, 4, 4, 256, 100) == 0  # head dim > 128
+    assert lib.nne_decode_workspace_bytes(1, 32, 1, 64, 100) == 0  # 32 rows per KV head > 16
+    small = lib.nne_decode_workspace_bytes(2, 4, 2, 64, 4160)
     big = lib.nne_decode_workspace_bytes(32, 32, 8, 128, 4160)
-    assert small == 0 or small < big
-    assert big > 0
+    assert 0 < small < big
+    # partial records for (workgroups + heads) slots of 4 rows x (128 + 2) floats
+    assert big >= (2048 + 32 * 8) * 4 * 130 * 4
+
+
+def test_decode_step_capacity_error_leaves_lengths(nne):
+    lib = nne.lib()
+    lens = np.array([3, 8], np.int32)
+    lp = lens.ctypes.data_as(ctypes.POINTER(ctypes.c_int32))
+    rc = lib.nne_decode_step(FAKE, None, FAKE, FAKE, FAKE, lp, FAKE, None, FAKE, None, FAKE, None,
+                             2, 4, 2, 8, 16, 0, 0.0, None, 0, None)
+    assert rc == nne.NNE_ECAPACITY
+    assert list(lens) == [3, 8]
 
 
 def test_python_mirror_rejects_non_4d(nne):

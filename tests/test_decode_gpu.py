@@ -113,7 +113,9 @@ def test_config3_multi_step_decode(nne, cuda):
         out = host(cache.decode_step(0, dev(q, cuda), dev(kn, cuda), dev(vn, cuda)))
         ref, kc, vc, lens = T.ref_decode_step(q, kc, vc, lens, kn, vn)
         T.assert_close(out, ref, what="config3 step %d" % s)
+        assert list(host(cache.lens_dev[0])) == list(lens)
     assert list(cache.lens_host[0]) == list(lens)
+    assert np.array_equal(host(cache.k[0]), kc) and np.array_equal(host(cache.v[0]), vc)
 
 
 def test_config3_full_batch_one_step(nne, cuda):
