@@ -28,6 +28,14 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 PEAK_FP32_MATRIX_TFLOPS = 157.3
 PEAK_HBM_GBS = 8000.0
 
+# HBM bytes per launch measured with rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE on
+# the `--probe` workload, each scaled by its reading for a plain 1 GiB device copy
+# (FETCH_SIZE x2.00, WRITE_SIZE x1.00).  Config 2 prefill: 215.8 MB read + 134.2 MB
+# written (algorithmic 201.3 + 134.2).  Config 3 decode step (split + combine):
+# 647.4 MB read + 2.4 MB written (algorithmic ~646 + ~1.3).
+TRAFFIC_PREFILL_CONFIG2 = int(215.8e6 + 134.2e6)
+TRAFFIC_DECODE_CONFIG3_STEP = int(647.4e6 + 2.4e6)
+
 
 def load_pkg():
     sys.path.insert(0, os.path.join(ROOT, "tests"))
@@ -110,7 +118,8 @@ def bench_decode(nne, torch, dev, steps=64, warmup=4, seed=0x5EED0003):
             "steps": steps, "ms_per_step": round(ms / steps, 4),
             "bytes_per_step": round(total / steps),
             "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS,
-                         "unit": "GB/s", "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": None},
+                         "unit": "GB/s", "frac": round(gbs / PEAK_HBM_GBS, 4),
+                         "traffic": TRAFFIC_DECODE_CONFIG3_STEP},
             "config": {"workload": "config3: decode B=32 Hq=32 Hkv=8 d=128 "
                                    "L0~U[512,4096] ragged, 64 steps append+attend, f32"}}
 
@@ -145,6 +154,26 @@ def cpu_baseline(target_seconds=15.0):
                       "(unmasked pairs only)" % (heads, el)}
 
 
+def probe(nne, torch, dev):
+    """Fixed, short workload for rocprofv3 --pmc runs (one counter set per run)."""
+    x = torch.empty(1 << 28, dtype=torch.float32, device=dev)     # 1 GiB
+    x.fill_(1.0)
+    y = torch.empty_like(x)
+    for _ in range(3):
+        y.copy_(x)
+    torch.cuda.synchronize()
+    del x, y
+    q, k, v = config2_inputs(torch, dev)
+    out = torch.empty_like(q)
+    for _ in range(3):
+        nne.attention_forward(q, k, v, True, out=out)
+    torch.cuda.synchronize()
+    del q, k, v, out
+    bench_decode(nne, torch, dev, steps=8, warmup=1)
+    torch.cuda.synchronize()
+    print("probe done", file=sys.stderr, flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -153,6 +182,9 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-decode", action="store_true")
     ap.add_argument("--all", action="store_true", help="also print lines for configs 1, 4, 5")
+    ap.add_argument("--probe", action="store_true",
+                    help="counter-collection run: a 1 GiB device copy (calibrates FETCH_SIZE/"
+                         "WRITE_SIZE), 3 config-2 prefills and 8 config-3 decode steps")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
@@ -163,6 +195,9 @@ def main():
     nne = load_pkg()
     nne.lib()
     dev = torch.device("cuda:0")
+    if args.probe:
+        probe(nne, torch, dev)
+        return
 
     b, hq, hkv, t, d = 4, 32, 8, 2048, 128
     q, k, v = config2_inputs(torch, dev)
@@ -183,7 +218,8 @@ def main():
                    "global_batch": b, "seq_len": t, "parallelism": "none (1 GPU)"},
         "roofline": {"bound": "mfma", "achieved": round(achieved, 3),
                      "peak": PEAK_FP32_MATRIX_TFLOPS, "unit": "TFLOP/s",
-                     "frac": round(achieved / PEAK_FP32_MATRIX_TFLOPS, 4), "traffic": None,
+                     "frac": round(achieved / PEAK_FP32_MATRIX_TFLOPS, 4),
+                     "traffic": TRAFFIC_PREFILL_CONFIG2,
                      "kernel": "prefill_mfma_kernel<128,causal,vec>",
                      "kernel_ms": round(kms, 4)},
     }

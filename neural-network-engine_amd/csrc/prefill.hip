@@ -109,10 +109,7 @@ __global__ __launch_bounds__(256, 2) void prefill_mfma_kernel(const PrefillParam
     const int wgi = p.n_wg - 1 - (logical % p.n_wg);   // longest causal work first
     const int bi = head / p.Hkv, kvh = head % p.Hkv;
 
-    const int tid = threadIdx.x, lane = tid & 63;
-    // Wave index as a scalar so everything derived from it (row block, head,
-    // tile range) is wave-uniform and the tile loop's branches stay scalar.
-    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int l32 = lane & 31, half = lane >> 5;
 
     const int unit = wgi * 4 + wave;
