@@ -22,7 +22,8 @@
 //     (the key order of that reduction is chosen to match), so P never
 //     leaves registers,
 //   * every O^T accumulator of a lane belongs to that lane's query row, so the
-//     online-softmax rescale is a lane-local multiply.
+//     online-softmax rescale is a lane-local multiply -- done lazily, only
+//     when a row max grows by more than 2^8.
 // K and V tiles (32 keys) are staged through LDS, double buffered, with the
 // next tile's global loads in flight while the current tile is computed.  The
 // G query heads that share a KV head run as waves of one workgroup and read
@@ -182,6 +183,9 @@ __global__ __launch_bounds__(256, 2) void prefill_mfma_kernel(const PrefillParam
 #pragma unroll
             for (int r = 0; r < 16; ++r) s[r] = 0.f;
             const float* krow = Ks + l32 * KS + half * (D / 2);
+            // Raised issue priority while this wave feeds the MFMA pipe, so the
+            // two waves sharing a SIMD alternate MFMA and softmax phases.
+            __builtin_amdgcn_s_setprio(1);
 #pragma unroll
             for (int t = 0; t < D / 8; ++t) {
                 const float4 kq = *reinterpret_cast<const float4*>(krow + 4 * t);
@@ -191,6 +195,7 @@ __global__ __launch_bounds__(256, 2) void prefill_mfma_kernel(const PrefillParam
                 s = __builtin_amdgcn_mfma_f32_32x32x2f32(kq.w, qf[4 * t + 3], s, 0, 0, 0);
             }
 
+            __builtin_amdgcn_s_setprio(0);
             // Mask keys past T_k and (causal) keys after row + q_offset.
             const int key0 = kt * 32;
             const bool need_mask = (key0 + 32 > p.Tk) || (CAUSAL && key0 + 31 > row0 + p.q_offset);
@@ -204,27 +209,35 @@ __global__ __launch_bounds__(256, 2) void prefill_mfma_kernel(const PrefillParam
             }
 
             // Online softmax for this lane's row (keys split over the lane pair).
+            // m_run is the reference max the exponentials use.  It is raised,
+            // and O and l rescaled, only when some row's tile max exceeds it by
+            // more than 8 (log2 units): P values stay <= 2^8, the ratio O/l is
+            // unchanged, and most tiles skip the 4*NB*4 multiplies.
             float mt = s[0];
 #pragma unroll
             for (int r = 1; r < 16; ++r) mt = fmaxf(mt, s[r]);
             mt = pair_max(mt);
-            const float m_new = fmaxf(m_run, mt);
-            const float m_use = (m_new == kNegInf) ? 0.f : m_new;
-            const float alpha = fast_exp2(m_run - m_use);
+            if (__builtin_amdgcn_ballot_w64(mt > m_run + 8.f) != 0) {
+                const float m_new = fmaxf(m_run, mt);
+                const float alpha = fast_exp2(m_run - ((m_new == kNegInf) ? 0.f : m_new));
+                l_run *= alpha;
+#pragma unroll
+                for (int b = 0; b < NB; ++b)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) o[b][r] *= alpha;
+                m_run = m_new;
+            }
+            const float m_use = (m_run == kNegInf) ? 0.f : m_run;
             float ls = 0.f;
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
                 s[r] = fast_exp2(s[r] - m_use);
                 ls += s[r];
             }
-            l_run = alpha * l_run + ls;
-            m_run = m_new;
-#pragma unroll
-            for (int b = 0; b < NB; ++b)
-#pragma unroll
-                for (int r = 0; r < 16; ++r) o[b][r] *= alpha;
+            l_run += ls;
 
             // O^T += V^T P^T ; reduction step r pairs key 8*(r/4)+4*half+r%4.
+            __builtin_amdgcn_s_setprio(1);
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
                 const float* vrow = Vs + (8 * (r >> 2) + 4 * half + (r & 3)) * VS + l32;
@@ -232,6 +245,7 @@ __global__ __launch_bounds__(256, 2) void prefill_mfma_kernel(const PrefillParam
                 for (int b = 0; b < NB; ++b)
                     o[b] = __builtin_amdgcn_mfma_f32_32x32x2f32(vrow[32 * b], s[r], o[b], 0, 0, 0);
             }
+            __builtin_amdgcn_s_setprio(0);
         }
 
         if (has_next) {
