@@ -11,6 +11,7 @@
 #include <cstdarg>
 #include <cstdio>
 #include <string>
+#include <vector>
 
 #include "nne_attn.h"
 #include "nne_launch.hpp"
@@ -102,7 +103,8 @@ int run_attention(const float* q, const int64_t* qs_, const int64_t* qst, const 
     const int64_t rows = (int64_t)G * Tq;
 
     if (vec && all_visible && rows <= nne::splitk_max_rows() && Tk > 0 &&
-        B <= nne::splitk_max_seqs() && (int64_t)B * Hkv * Tk < INT32_MAX) {
+        B <= nne::splitk_max_seqs() && (int64_t)B * Hkv * Tk < INT32_MAX &&
+        (int64_t)Tk * kst[2] < INT32_MAX && (int64_t)Tk * vst[2] < INT32_MAX) {
         nne::SplitKParams p{};
         p.q = make_view(q, qst);
         p.k = k; p.v = v;
@@ -118,7 +120,7 @@ int run_attention(const float* q, const int64_t* qs_, const int64_t* qst, const 
         void* ws = nullptr;
         hipError_t e = hipMallocAsync(&ws, w.total_bytes, stream);
         if (e != hipSuccess) return hip_fail(e, "hipMallocAsync(split-K workspace)");
-        e = nne::launch_splitk(p, (int64_t)B * Hkv * Tk, Tk, ws, stream);
+        e = nne::launch_splitk(p, (int64_t)B * Hkv * Tk, Tk, ws, stream, nullptr);
         hipError_t e2 = hipFreeAsync(ws, stream);
         if (e == hipSuccess) e = e2;
         if (e != hipSuccess) return hip_fail(e, "split-K attention launch");
@@ -339,6 +341,7 @@ int run_decode(const float* q, const int64_t* q_strides, const float* k_cache, c
     const bool append = k_new != nullptr;
     int max_len = 0;
     int64_t total_keys = 0;
+    std::vector<int32_t> seq_lens((size_t)B);
     for (int64_t b = 0; b < B; ++b) {
         const int64_t L = (int64_t)lens_host[b] + (append ? 1 : 0);
         if (lens_host[b] < 0 || L > capacity) {
@@ -352,7 +355,12 @@ int run_decode(const float* q, const int64_t* q_strides, const float* k_cache, c
         }
         max_len = std::max(max_len, (int)L);
         total_keys += L * Hkv;
+        seq_lens[(size_t)b] = (int32_t)L;
     }
+    if (capacity * d >= INT32_MAX)
+        return fail(NNE_EINVAL, "Invalid configuration or argument: KV cache rows of one head "
+                                "(capacity %lld x d %lld) exceed 2^31 floats",
+                    (long long)capacity, (long long)d);
     if (total_keys >= INT32_MAX)
         return fail(NNE_EINVAL, "Invalid configuration or argument: %lld cached rows exceed the "
                                 "decode kernel's 2^31 limit", (long long)total_keys);
@@ -404,7 +412,7 @@ int run_decode(const float* q, const int64_t* q_strides, const float* k_cache, c
                                 "is smaller than the %llu required",
                     (unsigned long long)workspace_bytes, (unsigned long long)w.total_bytes);
     }
-    e = nne::launch_splitk(p, total_keys, max_len, ws, s);
+    e = nne::launch_splitk(p, total_keys, max_len, ws, s, seq_lens.data());
     if (owned) {
         hipError_t e2 = hipFreeAsync(ws, s);
         if (e == hipSuccess) e = e2;

@@ -55,6 +55,9 @@ struct PrefillParams {
 // Split-K few-query kernel parameters (decode and cross-attention).  Each KV
 // head serves R = G * Tq query rows; row rr maps to query head kvh*G + rr/Tq
 // and query position rr % Tq.  Every row sees every key of its sequence.
+// Sequences whose flattened prefix travels in the kernel arguments.
+constexpr int kArgSeqs = 128;
+
 struct SplitKParams {
     View4 q;
     const float* k;
@@ -75,6 +78,11 @@ struct SplitKParams {
     const float* v_new;
     int64_t kn_sb, kn_sh, vn_sb, vn_sh;
     int32_t* lens_w;
+    // Flattened start of each sequence, pref[b] = Hkv * sum_{b' < b} L_b',
+    // computed by the host when B <= kArgSeqs (arg_pref valid), else by the
+    // split kernel from lens into ws_pref.
+    int arg_pref_valid;
+    int arg_pref[kArgSeqs + 1];
     // workspace
     int32_t* ws_pref;        // [B+1] flattened start of each sequence (this launch)
     float* ws_ml;            // [slots][R][2] partial (max, sum); slot = workgroup + head

@@ -29,8 +29,10 @@ int splitk_max_workgroups();
 SplitKWorkspace splitk_workspace_layout(int B, int Hkv, int R, int d);
 // Launches the split kernel over total_keys flattened (sequence, KV head, key)
 // rows, then the per-head combine kernel.  max_len bounds every sequence.
+// seq_lens (host) are this launch's key counts per sequence (including a
+// decode step's new row), or null when every sequence has p.tk keys.
 hipError_t launch_splitk(SplitKParams p, int64_t total_keys, int max_len, void* workspace,
-                         hipStream_t stream);
+                         hipStream_t stream, const int32_t* seq_lens);
 
 hipError_t launch_kv_append(float* kc, float* vc, int32_t* lens_dev, View4 kn, View4 vn, int B,
                             int Hkv, int cap, int d, int t_new, hipStream_t stream);

@@ -91,10 +91,15 @@ __device__ __forceinline__ int seq_len(const SplitKParams& p, int b) {
     return APPEND ? clamp_len(L_old + 1, p.max_keys) : L_old;
 }
 
-// Builds pref[0..B] in LDS with wave 0 (a wave-wide scan per 64 sequences).
+// Builds pref[0..B] in LDS: copied from the kernel arguments when the host
+// computed it, else scanned from lens by wave 0 (a wave-wide scan per 64
+// sequences).
 template <bool APPEND>
-__device__ __forceinline__ void build_prefix(const SplitKParams& p, int* pref, int lane, int wave) {
-    if (wave == 0) {
+__device__ __forceinline__ void build_prefix(const SplitKParams& p, int* pref, int tid, int lane,
+                                             int wave) {
+    if (p.arg_pref_valid) {
+        for (int b = tid; b <= p.B; b += 256) pref[b] = p.arg_pref[b];
+    } else if (wave == 0) {
         int carry = 0;
         if (lane == 0) pref[0] = 0;
         for (int base = 0; base < p.B; base += 64) {
@@ -120,7 +125,8 @@ __global__ __launch_bounds__(256, 2) void splitk_kernel(const SplitKParams p) {
     constexpr int NH = D / 64;           // V float4 loads per key step
     constexpr int NQ = D / 4;            // Q^T registers per lane
     constexpr int NB = D / 16;           // 16-dim output blocks
-    static_assert(4 * 16 * D <= 4 * KB * KS, "merge buffer must fit in the K slices");
+    constexpr int OS = D + 4;            // merge-buffer row stride (rows start 4 banks apart)
+    static_assert(4 * 16 * OS <= 4 * KB * KS, "merge buffer must fit in the K slices");
 
     __shared__ __attribute__((aligned(16))) float lds[4 * KB * KS];
     __shared__ float ml_s[4][16][2];
@@ -133,9 +139,9 @@ __global__ __launch_bounds__(256, 2) void splitk_kernel(const SplitKParams p) {
     const int col = lane & 15, grp = lane >> 4;
     const int wg = blockIdx.x;
 
-    build_prefix<APPEND>(p, pref, lane, wave);
+    build_prefix<APPEND>(p, pref, tid, lane, wave);
     __syncthreads();
-    if (wg == 0)   // snapshot for the combine kernel (lens may advance meanwhile)
+    if (wg == 0 && !p.arg_pref_valid)   // snapshot for the combine kernel (lens may advance meanwhile)
         for (int b = tid; b <= p.B; b += 256) p.ws_pref[b] = pref[b];
 
     const int total = pref[p.B];
@@ -158,6 +164,8 @@ __global__ __launch_bounds__(256, 2) void splitk_kernel(const SplitKParams p) {
 #pragma unroll
     for (int h = 0; h < NH; ++h) v_col[h] = min(64 * h + 4 * col, p.d - 4);
     const int kc_col = min(4 * (lane % LPR), p.d - 4);
+    // Row strides in 32 bits: the host guarantees rows * stride < 2^31 per head.
+    const int kst = (int)p.kst, vst = (int)p.vst;
 
     while (g < g_end) {
         const int Lb = (pref[b + 1] - pref[b]) / p.Hkv;
@@ -213,14 +221,14 @@ __global__ __launch_bounds__(256, 2) void splitk_kernel(const SplitKParams p) {
 #pragma unroll
             for (int i = 0; i < NK; ++i) {
                 const int key = min(kb0 + lane / LPR + RPI * i, key_end - 1);
-                kr[i] = *reinterpret_cast<const vf4*>(kb + (int64_t)key * p.kst + kc_col);
+                kr[i] = *reinterpret_cast<const vf4*>(kb + key * kst + kc_col);
             }
 #pragma unroll
             for (int st = 0; st < 4; ++st) {
                 const int key = min(kb0 + 4 * grp + st, key_end - 1);
 #pragma unroll
                 for (int h = 0; h < NH; ++h)
-                    vr[st * NH + h] = *reinterpret_cast<const vf4*>(vb + (int64_t)key * p.vst + v_col[h]);
+                    vr[st * NH + h] = *reinterpret_cast<const vf4*>(vb + key * vst + v_col[h]);
             }
         };
 
@@ -300,12 +308,12 @@ __global__ __launch_bounds__(256, 2) void splitk_kernel(const SplitKParams p) {
         // Merge the 4 waves through LDS: O[row col][dim] with
         // dim = 64h + 16*grp + 4*reg + c  for  o[4h + c][reg].
         __syncthreads();                  // every wave is done with its K slice
-        float* ob = lds;                  // [4 waves][16 rows][D]
+        float* ob = lds;                  // [4 waves][16 rows][OS]
 #pragma unroll
         for (int h = 0; h < NH; ++h)
 #pragma unroll
             for (int reg = 0; reg < 4; ++reg)
-                *reinterpret_cast<vf4*>(ob + (wave * 16 + col) * D + 64 * h + 16 * grp + 4 * reg) =
+                *reinterpret_cast<vf4*>(ob + (wave * 16 + col) * OS + 64 * h + 16 * grp + 4 * reg) =
                     vf4{o[4 * h + 0][reg], o[4 * h + 1][reg], o[4 * h + 2][reg], o[4 * h + 3][reg]};
         if (grp == 0) { ml_s[wave][col][0] = m_run; ml_s[wave][col][1] = l_tot; }
         __syncthreads();
@@ -322,7 +330,7 @@ __global__ __launch_bounds__(256, 2) void splitk_kernel(const SplitKParams p) {
             for (int w = 0; w < 4; ++w) {
                 const float f = fast_exp2(ml_s[w][rr][0] - M_use);
                 l += f * ml_s[w][rr][1];
-                acc += f * ob[(w * 16 + rr) * D + dd];
+                acc += f * ob[(w * 16 + rr) * OS + dd];
             }
             if (whole) {
                 if (dd < p.d) {
@@ -351,7 +359,8 @@ __global__ __launch_bounds__(256) void splitk_combine_kernel(const SplitKParams 
     const int head = blockIdx.x;
     const int b = head / p.Hkv, kvh = head % p.Hkv;
     const int tid = threadIdx.x;
-    const int p0 = p.ws_pref[b], p1 = p.ws_pref[b + 1];
+    const int* pr = p.arg_pref_valid ? p.arg_pref : p.ws_pref;
+    const int p0 = pr[b], p1 = pr[b + 1];
     const int Lb = (p1 - p0) / p.Hkv;
     if (p.lens_w && kvh == 0 && tid == 0) p.lens_w[b] = Lb;
     auto out_ptr = [&](int rr) {
@@ -501,7 +510,15 @@ hipError_t launch_flat(SplitKParams p, int64_t total_keys, int max_len, hipStrea
 }  // namespace
 
 hipError_t launch_splitk(SplitKParams p, int64_t total_keys, int max_len, void* workspace,
-                         hipStream_t stream) {
+                         hipStream_t stream, const int32_t* seq_lens) {
+    // Small batches carry the flattened prefix in the arguments, which saves
+    // every workgroup the scan over lens.
+    p.arg_pref_valid = p.B <= kArgSeqs ? 1 : 0;
+    if (p.arg_pref_valid) {
+        p.arg_pref[0] = 0;
+        for (int b = 0; b < p.B; ++b)
+            p.arg_pref[b + 1] = p.arg_pref[b] + p.Hkv * (seq_lens ? seq_lens[b] : p.tk);
+    }
     p.G = p.Hq / p.Hkv;
     p.R = p.G * p.Tq;
     const SplitKWorkspace w = splitk_workspace_layout(p.B, p.Hkv, p.R, p.d);
