@@ -37,6 +37,8 @@
 // No cross-workgroup synchronisation is used inside the split kernel: on
 // gfx950 an agent-scope fence is a whole-L2 writeback and invalidate, far more
 // expensive than the second launch.
+#include <utility>
+
 #include "nne_common.hpp"
 #include "nne_launch.hpp"
 
@@ -68,6 +70,44 @@ __device__ __forceinline__ float quad_rows_sum(float x) {
     x = __uint_as_float(a[0]) + __uint_as_float(a[1]);
     auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
     return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+}
+
+// Reductions over a row of 16 lanes (DPP row_ror 8, 4, 2, 1); every lane of
+// the row ends with the result.
+template <int CTRL>
+__device__ __forceinline__ float dpp_row(float x) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, 0xF, 0xF, false));
+}
+__device__ __forceinline__ float row16_max(float x) {
+    x = fmaxf(x, dpp_row<0x128>(x));
+    x = fmaxf(x, dpp_row<0x124>(x));
+    x = fmaxf(x, dpp_row<0x122>(x));
+    return fmaxf(x, dpp_row<0x121>(x));
+}
+__device__ __forceinline__ float row16_sum(float x) {
+    x += dpp_row<0x128>(x);
+    x += dpp_row<0x124>(x);
+    x += dpp_row<0x122>(x);
+    return x + dpp_row<0x121>(x);
+}
+
+// f(std::integral_constant<int, 0>) ... f(std::integral_constant<int, N-1>):
+// MFMA broadcast selectors must be compile-time constants.
+template <typename F, int... I>
+__device__ __forceinline__ void static_for_impl(F& f, std::integer_sequence<int, I...>) {
+    (f(std::integral_constant<int, I>{}), ...);
+}
+template <int N, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+    static_for_impl(f, std::make_integer_sequence<int, N>{});
+}
+
+// v_mfma_f32_4x4x1_16b_f32: 16 blocks of 4 lanes; lane 4b + i supplies A_b[i]
+// and B_b[i], and register r of lane 4b + j receives D_b[r][j].  With CB > 0,
+// each group of 2^CB blocks takes A from its block AB.
+template <int CB, int AB>
+__device__ __forceinline__ floatx4 mfma4(float a, float b, floatx4 c) {
+    return __builtin_amdgcn_mfma_f32_4x4x1f32(a, b, c, CB, AB, 0);
 }
 
 // Orders this wave's LDS accesses on both sides of a cross-lane exchange.
@@ -116,8 +156,19 @@ __device__ __forceinline__ void build_prefix(const SplitKParams& p, int* pref, i
     }
 }
 
-template <int D, bool APPEND>
+// ROWS = 16: R <= 16 query rows per KV head on v_mfma_f32_16x16x4_f32 (above).
+// ROWS = 4: R <= 4 rows (single-token decode with G <= 4) on
+// v_mfma_f32_4x4x1_16b_f32, which wastes no MFMA work on padding rows:
+//   S = Q K^T: lane l scores key l % 16 over dim group l / 16 (D/4 dims); Q is
+//     the broadcast A operand (8 dims of 4 rows per register), K comes from
+//     the LDS slice; the 4 dim groups are summed with two lane swaps;
+//   O += P V: V keeps the coalesced row layout of its load (LPR lanes per key
+//     row, 64 / LPR keys per load), P is the broadcast A operand (one register
+//     holds the 16 keys' probabilities, regrouped through LDS); each key group
+//     accumulates its own partial O, summed once per segment.
+template <int D, bool APPEND, int ROWS>
 __global__ __launch_bounds__(256, 2) void splitk_kernel(const SplitKParams p) {
+    constexpr bool NARROW = ROWS == 4;
     constexpr int KS = D + 4;            // LDS row stride (16-byte reads conflict-free)
     constexpr int LPR = D / 4;           // lanes per K row in the coalesced load
     constexpr int RPI = 64 / LPR;        // K rows per load instruction
@@ -126,10 +177,15 @@ __global__ __launch_bounds__(256, 2) void splitk_kernel(const SplitKParams p) {
     constexpr int NQ = D / 4;            // Q^T registers per lane
     constexpr int NB = D / 16;           // 16-dim output blocks
     constexpr int OS = D + 4;            // merge-buffer row stride (rows start 4 banks apart)
-    static_assert(4 * 16 * OS <= 4 * KB * KS, "merge buffer must fit in the K slices");
+    constexpr int NQN = D / 16;          // narrow: Q registers per lane
+    constexpr int CBV = D == 128 ? 3 : 2;  // narrow: PV broadcast group (LPR / 4 blocks)
+    static_assert(ROWS == 16 || ROWS == 4, "row tile");
+    static_assert(4 * ROWS * OS <= 4 * KB * KS, "merge buffer must fit in the K slices");
+    static_assert(NK == 4 * NH, "K and V loads per block");
 
     __shared__ __attribute__((aligned(16))) float lds[4 * KB * KS];
     __shared__ float ml_s[4][16][2];
+    __shared__ vf4 p_s[4][16];           // narrow: P of a wave's 16 keys
     __shared__ int pref[MAX_SEQS + 1];
 
     const int tid = threadIdx.x, lane = tid & 63;
@@ -137,6 +193,10 @@ __global__ __launch_bounds__(256, 2) void splitk_kernel(const SplitKParams p) {
     // compiler neither masks it nor drains the prefetched loads at its head.
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int col = lane & 15, grp = lane >> 4;
+    // narrow lane roles: QK broadcast block within the dim group, A row, and
+    // the P element supplied to PV (key RPI * block + key group, row).
+    const int na = (lane >> 2) & 3, ni = lane & 3;
+    const int p_idx = 4 * (RPI * ((lane % LPR) >> 2) + lane / LPR) + ni;
     const int wg = blockIdx.x;
 
     build_prefix<APPEND>(p, pref, tid, lane, wave);
@@ -196,8 +256,18 @@ __global__ __launch_bounds__(256, 2) void splitk_kernel(const SplitKParams p) {
         }
 
         // Q^T fragment: lane holds query row `col`, dims grp*D/4 .. +D/4, pre-scaled.
-        float qf[NQ];
-        {
+        // Narrow: lane 16g + 4a + i holds row i, dims g*D/4 + 4t + a (t < D/16).
+        float qf[NARROW ? NQN : NQ];
+        if constexpr (NARROW) {
+            const bool rok = ni < p.R;
+            const int hq = kvh * p.G + (rok ? ni / p.Tq : 0), t = rok ? ni % p.Tq : 0;
+            const float* qp = p.q.p + b * p.q.sb + hq * p.q.sh + t * p.q.st;
+#pragma unroll
+            for (int t4 = 0; t4 < NQN; ++t4) {
+                const int c = grp * (D / 4) + 4 * t4 + na;
+                qf[t4] = (rok && c < p.d) ? qp[c] * p.qscale : 0.f;
+            }
+        } else {
             const bool rok = col < p.R;
             const int hq = kvh * p.G + (rok ? col / p.Tq : 0), t = rok ? col % p.Tq : 0;
             const float* qp = p.q.p + b * p.q.sb + hq * p.q.sh + t * p.q.st;
@@ -223,19 +293,29 @@ __global__ __launch_bounds__(256, 2) void splitk_kernel(const SplitKParams p) {
                 const int key = min(kb0 + lane / LPR + RPI * i, key_end - 1);
                 kr[i] = *reinterpret_cast<const vf4*>(kb + key * kst + kc_col);
             }
+            if constexpr (NARROW) {
 #pragma unroll
-            for (int st = 0; st < 4; ++st) {
-                const int key = min(kb0 + 4 * grp + st, key_end - 1);
+                for (int i = 0; i < NK; ++i) {
+                    const int key = min(kb0 + lane / LPR + RPI * i, key_end - 1);
+                    vr[i] = *reinterpret_cast<const vf4*>(vb + key * vst + kc_col);
+                }
+            } else {
 #pragma unroll
-                for (int h = 0; h < NH; ++h)
-                    vr[st * NH + h] = *reinterpret_cast<const vf4*>(vb + key * vst + v_col[h]);
+                for (int st = 0; st < 4; ++st) {
+                    const int key = min(kb0 + 4 * grp + st, key_end - 1);
+#pragma unroll
+                    for (int h = 0; h < NH; ++h)
+                        vr[st * NH + h] = *reinterpret_cast<const vf4*>(vb + key * vst + v_col[h]);
+                }
             }
         };
 
-        floatx4 o[NB];
+        floatx4 o[NARROW ? 4 : NB];
 #pragma unroll
-        for (int bb = 0; bb < NB; ++bb) o[bb] = floatx4{0.f, 0.f, 0.f, 0.f};
+        for (int bb = 0; bb < (NARROW ? 4 : NB); ++bb) o[bb] = floatx4{0.f, 0.f, 0.f, 0.f};
         float m_run = kNegInf, l_run = 0.f;
+        floatx4 m4 = floatx4{kNegInf, kNegInf, kNegInf, kNegInf};   // narrow: per row
+        floatx4 l4 = floatx4{0.f, 0.f, 0.f, 0.f};                   // narrow: per row, this lane's key
 
         // One 16-key block: stage K, S^T = K Q^T, online softmax, O^T += V^T P^T.
         auto block = [&](const vf4 (&kr)[NK], const vf4 (&vr)[4 * NH], int kb0) __attribute__((always_inline)) {
@@ -245,6 +325,59 @@ __global__ __launch_bounds__(256, 2) void splitk_kernel(const SplitKParams p) {
                 *reinterpret_cast<vf4*>(Kw + (lane / LPR + RPI * i) * KS + 4 * (lane % LPR)) = kr[i];
             wave_lds_sync();
 
+          if constexpr (NARROW) {
+            floatx4 s = floatx4{0.f, 0.f, 0.f, 0.f};
+            const float* krow = Kw + col * KS + grp * (D / 4);
+#pragma unroll
+            for (int t = 0; t < NQN; ++t) {
+                const vf4 kq = *reinterpret_cast<const vf4*>(krow + 4 * t);
+                s = mfma4<2, 0>(qf[t], kq.x, s);
+                s = mfma4<2, 1>(qf[t], kq.y, s);
+                s = mfma4<2, 2>(qf[t], kq.z, s);
+                s = mfma4<2, 3>(qf[t], kq.w, s);
+            }
+            // s[r] = score of query row r for key kb0 + col (summed over dim groups).
+#pragma unroll
+            for (int r = 0; r < 4; ++r) s[r] = quad_rows_sum(s[r]);
+            if (kb0 + KB > key_end) {
+                const bool ok = kb0 + col < key_end;
+#pragma unroll
+                for (int r = 0; r < 4; ++r) s[r] = ok ? s[r] : kNegInf;
+            }
+            // Lazy rescale: keep each row's reference max until a score exceeds
+            // it by 8 (a factor 256 in exp2), so most blocks skip the row max.
+            bool grow = false;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) grow |= s[r] > m4[r] + 8.f;
+            if (__builtin_amdgcn_ballot_w64(grow) != 0) {
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const float m_new = fmaxf(m4[r], row16_max(s[r]));
+                    const float alpha = fast_exp2(m4[r] - (m_new == kNegInf ? 0.f : m_new));
+                    l4[r] *= alpha;
+#pragma unroll
+                    for (int c = 0; c < 4; ++c) o[c][r] *= alpha;
+                    m4[r] = m_new;
+                }
+            }
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                s[r] = fast_exp2(s[r] - (m4[r] == kNegInf ? 0.f : m4[r]));
+                l4[r] += s[r];
+            }
+            // Regroup P for the PV broadcast: lane supplies P[row ni][key p_idx / 4].
+            if (lane < 16) p_s[wave][lane] = vf4{s[0], s[1], s[2], s[3]};
+            wave_lds_sync();
+            const float pa = reinterpret_cast<const float*>(p_s[wave])[p_idx];
+            static_for<NK>([&](auto vi) __attribute__((always_inline)) {
+                constexpr int V = decltype(vi)::value;
+                const vf4 vv = vr[V];
+                o[0] = mfma4<CBV, V>(pa, vv.x, o[0]);
+                o[1] = mfma4<CBV, V>(pa, vv.y, o[1]);
+                o[2] = mfma4<CBV, V>(pa, vv.z, o[2]);
+                o[3] = mfma4<CBV, V>(pa, vv.w, o[3]);
+            });
+          } else {
             floatx4 s = floatx4{0.f, 0.f, 0.f, 0.f};
             const float* krow = Kw + col * KS + grp * NQ;
 #pragma unroll
@@ -288,6 +421,7 @@ __global__ __launch_bounds__(256, 2) void splitk_kernel(const SplitKParams p) {
                     o[4 * h + 2] = __builtin_amdgcn_mfma_f32_16x16x4f32(vv.z, s[st], o[4 * h + 2], 0, 0, 0);
                     o[4 * h + 3] = __builtin_amdgcn_mfma_f32_16x16x4f32(vv.w, s[st], o[4 * h + 3], 0, 0, 0);
                 }
+          }
         };
 
         // Ping-pong over this wave's blocks (wave, wave+4, ...): while one
@@ -303,19 +437,41 @@ __global__ __launch_bounds__(256, 2) void splitk_kernel(const SplitKParams p) {
             load_block(ka, va, kb0 + 8 * KB);
             block(kb2, vb2, kb0 + 4 * KB);
         }
-        const float l_tot = quad_rows_sum(l_run);
-
-        // Merge the 4 waves through LDS: O[row col][dim] with
-        // dim = 64h + 16*grp + 4*reg + c  for  o[4h + c][reg].
-        __syncthreads();                  // every wave is done with its K slice
-        float* ob = lds;                  // [4 waves][16 rows][OS]
+        float* ob = lds;                  // [4 waves][ROWS rows][OS]
+        if constexpr (NARROW) {
+            // Sum the key groups' partial O: o[c][r] = O[row r][dim 4 (lane % LPR) + c].
 #pragma unroll
-        for (int h = 0; h < NH; ++h)
+            for (int c = 0; c < 4; ++c)
 #pragma unroll
-            for (int reg = 0; reg < 4; ++reg)
-                *reinterpret_cast<vf4*>(ob + (wave * 16 + col) * OS + 64 * h + 16 * grp + 4 * reg) =
-                    vf4{o[4 * h + 0][reg], o[4 * h + 1][reg], o[4 * h + 2][reg], o[4 * h + 3][reg]};
-        if (grp == 0) { ml_s[wave][col][0] = m_run; ml_s[wave][col][1] = l_tot; }
+                for (int r = 0; r < 4; ++r)
+                    o[c][r] = RPI == 2 ? pair_sum(o[c][r]) : quad_rows_sum(o[c][r]);
+            float l_tot[4];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) l_tot[r] = row16_sum(l4[r]);
+            __syncthreads();              // every wave is done with its K slice
+            if (lane < LPR) {
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+                    *reinterpret_cast<vf4*>(ob + (wave * 4 + r) * OS + 4 * lane) =
+                        vf4{o[0][r], o[1][r], o[2][r], o[3][r]};
+            }
+            if (lane == 0) {
+#pragma unroll
+                for (int r = 0; r < 4; ++r) { ml_s[wave][r][0] = m4[r]; ml_s[wave][r][1] = l_tot[r]; }
+            }
+        } else {
+            const float l_tot = quad_rows_sum(l_run);
+            // Merge the 4 waves through LDS: O[row col][dim] with
+            // dim = 64h + 16*grp + 4*reg + c  for  o[4h + c][reg].
+            __syncthreads();              // every wave is done with its K slice
+#pragma unroll
+            for (int h = 0; h < NH; ++h)
+#pragma unroll
+                for (int reg = 0; reg < 4; ++reg)
+                    *reinterpret_cast<vf4*>(ob + (wave * 16 + col) * OS + 64 * h + 16 * grp + 4 * reg) =
+                        vf4{o[4 * h + 0][reg], o[4 * h + 1][reg], o[4 * h + 2][reg], o[4 * h + 3][reg]};
+            if (grp == 0) { ml_s[wave][col][0] = m_run; ml_s[wave][col][1] = l_tot; }
+        }
         __syncthreads();
 
         const int64_t slot = (int64_t)wg + head;    // unique per (workgroup, head)
@@ -330,7 +486,7 @@ __global__ __launch_bounds__(256, 2) void splitk_kernel(const SplitKParams p) {
             for (int w = 0; w < 4; ++w) {
                 const float f = fast_exp2(ml_s[w][rr][0] - M_use);
                 l += f * ml_s[w][rr][1];
-                acc += f * ob[(w * 16 + rr) * OS + dd];
+                acc += f * ob[(w * ROWS + rr) * OS + dd];
             }
             if (whole) {
                 if (dd < p.d) {
@@ -410,10 +566,15 @@ __global__ __launch_bounds__(256) void splitk_combine_kernel(const SplitKParams 
 template <int D>
 hipError_t launch_splitk_d(const SplitKParams& p, hipStream_t stream) {
     if (p.n_wg > 0) {
-        if (p.k_new)
-            hipLaunchKernelGGL((splitk_kernel<D, true>), dim3(p.n_wg), dim3(256), 0, stream, p);
+        const bool narrow = p.R <= 4;
+        if (p.k_new && narrow)
+            hipLaunchKernelGGL((splitk_kernel<D, true, 4>), dim3(p.n_wg), dim3(256), 0, stream, p);
+        else if (p.k_new)
+            hipLaunchKernelGGL((splitk_kernel<D, true, 16>), dim3(p.n_wg), dim3(256), 0, stream, p);
+        else if (narrow)
+            hipLaunchKernelGGL((splitk_kernel<D, false, 4>), dim3(p.n_wg), dim3(256), 0, stream, p);
         else
-            hipLaunchKernelGGL((splitk_kernel<D, false>), dim3(p.n_wg), dim3(256), 0, stream, p);
+            hipLaunchKernelGGL((splitk_kernel<D, false, 16>), dim3(p.n_wg), dim3(256), 0, stream, p);
         hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;
     }
@@ -473,7 +634,7 @@ namespace {
 
 // Resident workgroups of the split kernel on the current device: one full
 // wave of them covers the flattened key range exactly once.
-template <int D, bool APPEND>
+template <int D, bool APPEND, int ROWS>
 int resident_workgroups() {
     static int cached[64] = {0};
     int dev = 0;
@@ -482,7 +643,7 @@ int resident_workgroups() {
         int cus = 0, per_cu = 0;
         if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
             cus = 256;
-        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, splitk_kernel<D, APPEND>, 256, 0) !=
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, splitk_kernel<D, APPEND, ROWS>, 256, 0) !=
                 hipSuccess || per_cu < 1)
             per_cu = 1;
         int n = cus * per_cu;
@@ -493,7 +654,9 @@ int resident_workgroups() {
 
 template <int D>
 hipError_t launch_flat(SplitKParams p, int64_t total_keys, int max_len, hipStream_t stream) {
-    const int slots = p.k_new ? resident_workgroups<D, true>() : resident_workgroups<D, false>();
+    const bool narrow = p.R <= 4;
+    const int slots = p.k_new ? (narrow ? resident_workgroups<D, true, 4>() : resident_workgroups<D, true, 16>())
+                              : (narrow ? resident_workgroups<D, false, 4>() : resident_workgroups<D, false, 16>());
     // Equal flattened chunks, whole 16-key blocks, and at most MAX_PARTS - 2
     // workgroups sharing any one head.
     int64_t chunk = (total_keys + slots - 1) / (slots > 0 ? slots : 1);

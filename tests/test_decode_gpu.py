@@ -78,7 +78,8 @@ def test_append_is_bit_exact_and_capacity_checked(nne, cuda):
     assert np.array_equal(host(cache2.k[0]), kc3) and np.array_equal(host(cache2.v[0]), vc3)
 
 
-@pytest.mark.parametrize("g,d", [(4, 128), (1, 64), (8, 64), (16, 32), (2, 16)])
+@pytest.mark.parametrize("g,d", [(4, 128), (1, 64), (8, 64), (16, 32), (2, 16), (3, 96),
+                                 (1, 128), (4, 64), (2, 128)])
 def test_decode_ragged_group_sizes(nne, cuda, g, d):
     print("case g=%d d=%d" % (g, d), flush=True)
     rng = np.random.default_rng(100 + g + d)

@@ -177,6 +177,21 @@ def test_config5_noncausal_t1500_and_cross(nne, cuda):
     T.assert_close(got, T.ref_standard(qx, k, v, False), what="config5b reduced")
 
 
+@pytest.mark.parametrize("g,tq,tk,d", [(1, 1, 300, 128), (2, 2, 77, 64), (4, 1, 1029, 128),
+                                        (1, 4, 64, 96), (3, 1, 515, 32), (2, 3, 200, 128),
+                                        (5, 3, 150, 64), (16, 1, 333, 128)])
+def test_few_query_split_k_row_tiles(nne, cuda, g, tq, tk, d):
+    """Few-query cross-attention runs on the split-K kernel: G*Tq <= 4 rows on
+    the 4-row tile, up to 16 on the 16-row tile."""
+    print("case g=%d tq=%d tk=%d d=%d" % (g, tq, tk, d), flush=True)
+    hkv = 2
+    q = rnd(700 + g + tq, 2, hkv * g, tq, d)
+    k = rnd(701 + tk, 2, hkv, tk, d)
+    v = rnd(702 + d, 2, hkv, tk, d)
+    got = host(nne.attention_forward(dev(q, cuda), dev(k, cuda), dev(v, cuda), False))
+    T.assert_close(got, T.ref_standard(q, k, v, False), what="few-query g=%d tq=%d" % (g, tq))
+
+
 def test_linearity_in_v_full_config4_shape(nne, cuda):
     """O is linear in V: f(a V1 + b V2) = a f(V1) + b f(V2) at T = 16384."""
     t = 16384
