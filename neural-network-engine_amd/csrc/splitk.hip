@@ -240,9 +240,18 @@ __global__ __launch_bounds__(256, 2) void splitk_kernel(const SplitKParams p) {
         const float* kb = p.k + b * p.ksb + kvh * p.ksh;
         const float* vb = p.v + b * p.vsb + kvh * p.vsh;
 
-        // Decode step: the segment holding the new row (key Lb - 1) stores it
-        // into the cache first and then reads it back like any cached row.
-        if (APPEND && key_end == Lb) {
+        // Decode step, segment holding the new row (key Lb - 1).  4-row tile:
+        // the row is prefetched into registers here, patched into the last
+        // block's operands, and stored into the cache after the block loop, so
+        // no load waits on it.  16-row tile: stored into the cache first and
+        // read back like any cached row.
+        const bool has_new = APPEND && key_end == Lb;
+        vf4 nk = vf4{0.f, 0.f, 0.f, 0.f}, nv = nk;
+        if (NARROW && has_new) {
+            nk = *reinterpret_cast<const vf4*>(p.k_new + b * p.kn_sb + kvh * p.kn_sh + kc_col);
+            nv = *reinterpret_cast<const vf4*>(p.v_new + b * p.vn_sb + kvh * p.vn_sh + kc_col);
+        }
+        if (!NARROW && has_new) {
             const int row = Lb - 1;
             if (tid < D / 4 && 4 * tid < p.d) {
                 const float* knb = p.k_new + b * p.kn_sb + kvh * p.kn_sh;
@@ -318,7 +327,16 @@ __global__ __launch_bounds__(256, 2) void splitk_kernel(const SplitKParams p) {
         floatx4 l4 = floatx4{0.f, 0.f, 0.f, 0.f};                   // narrow: per row, this lane's key
 
         // One 16-key block: stage K, S^T = K Q^T, online softmax, O^T += V^T P^T.
-        auto block = [&](const vf4 (&kr)[NK], const vf4 (&vr)[4 * NH], int kb0) __attribute__((always_inline)) {
+        auto block = [&](vf4 (&kr)[NK], vf4 (&vr)[4 * NH], int kb0) __attribute__((always_inline)) {
+            if (NARROW && has_new && kb0 + KB >= key_end) {
+                // Rows at or past the new one (clamped loads) take the new row.
+#pragma unroll
+                for (int i = 0; i < NK; ++i) {
+                    const bool fresh = kb0 + lane / LPR + RPI * i >= key_end - 1;
+                    kr[i] = fresh ? nk : kr[i];
+                    vr[i] = fresh ? nv : vr[i];
+                }
+            }
             wave_lds_sync();
 #pragma unroll
             for (int i = 0; i < NK; ++i)
@@ -426,16 +444,24 @@ __global__ __launch_bounds__(256, 2) void splitk_kernel(const SplitKParams p) {
 
         // Ping-pong over this wave's blocks (wave, wave+4, ...): while one
         // block computes, the next one's loads are in flight.
+        // The loop has a single exit at its end, which lets the next block's
+        // loads issue before the wait for the current block's data.
         const int n_blocks = (key_end - key_begin + KB - 1) / KB;
+        const int n_mine = wave < n_blocks ? (n_blocks - wave + 3) / 4 : 0;
         vf4 ka[NK], va[4 * NH], kb2[NK], vb2[4 * NH];
         load_block(ka, va, key_begin + wave * KB);
-        for (int blk = wave; blk < n_blocks; blk += 8) {
-            const int kb0 = key_begin + blk * KB;
+        int kb0 = key_begin + wave * KB;
+        for (int i = 0; i + 2 <= n_mine; i += 2, kb0 += 8 * KB) {
             load_block(kb2, vb2, kb0 + 4 * KB);
             block(ka, va, kb0);
-            if (blk + 4 >= n_blocks) break;
             load_block(ka, va, kb0 + 8 * KB);
             block(kb2, vb2, kb0 + 4 * KB);
+        }
+        if (n_mine & 1) block(ka, va, kb0);
+        if (NARROW && has_new && wave == 0 && lane < LPR && 4 * lane < p.d) {
+            const int row = Lb - 1;
+            *reinterpret_cast<vf4*>(const_cast<float*>(kb) + row * kst + 4 * lane) = nk;
+            *reinterpret_cast<vf4*>(const_cast<float*>(vb) + row * vst + 4 * lane) = nv;
         }
         float* ob = lds;                  // [4 waves][ROWS rows][OS]
         if constexpr (NARROW) {
@@ -508,10 +534,14 @@ __global__ __launch_bounds__(256, 2) void splitk_kernel(const SplitKParams p) {
 
 // Per (sequence, KV head): zero output for an empty sequence, merge the
 // partial records of the workgroups that shared the head, and in a decode step
-// publish the sequence's new length.
+// publish the sequence's new length.  Every global load is issued before the
+// first barrier (partial O rows into registers, (max, sum) pairs into LDS), so
+// the kernel costs one memory round trip.
 template <int D>
 __global__ __launch_bounds__(256) void splitk_combine_kernel(const SplitKParams p) {
-    __shared__ float w_s[MAX_PARTS][16];
+    constexpr int EPT = 16 * D / 256;     // output elements per thread (R <= 16)
+    constexpr int NPRE = 4;               // partials per element held in registers
+    __shared__ float2 ml_s[MAX_PARTS][16];
     const int head = blockIdx.x;
     const int b = head / p.Hkv, kvh = head % p.Hkv;
     const int tid = threadIdx.x;
@@ -532,34 +562,43 @@ __global__ __launch_bounds__(256) void splitk_combine_kernel(const SplitKParams 
     const int n = w_last - w_first + 1;
     if (n <= 1) return;                   // written directly by the split kernel
     const int64_t s0 = (int64_t)w_first + head;   // slots s0 .. s0 + n - 1
+    const int RD = p.R * D;
+    const float* o_src = p.ws_o + s0 * RD;
+
+    float pre[EPT][NPRE];
+#pragma unroll
+    for (int j = 0; j < EPT; ++j) {
+        const int e = tid + 256 * j;
+#pragma unroll
+        for (int c = 0; c < NPRE; ++c)
+            pre[j][c] = (e < RD && c < n) ? o_src[(int64_t)c * RD + e] : 0.f;
+    }
     for (int e = tid; e < n * p.R; e += 256) {
         const int c = e / p.R, rr = e % p.R;
-        w_s[c][rr] = p.ws_ml[((s0 + c) * p.R + rr) * 2];
+        ml_s[c][rr] = *reinterpret_cast<const float2*>(p.ws_ml + ((s0 + c) * p.R + rr) * 2);
     }
     __syncthreads();
-    if (tid < p.R) {
+    if (tid < p.R) {                      // weights: exp2(m_c - M) / sum_c exp2(m_c - M) l_c
         float M = kNegInf;
-        for (int c = 0; c < n; ++c) M = fmaxf(M, w_s[c][tid]);
+        for (int c = 0; c < n; ++c) M = fmaxf(M, ml_s[c][tid].x);
         const float M_use = M == kNegInf ? 0.f : M;
         float den = 0.f;
-        for (int c = 0; c < n; ++c)
-            den += fast_exp2(w_s[c][tid] - M_use) * p.ws_ml[((s0 + c) * p.R + tid) * 2 + 1];
+        for (int c = 0; c < n; ++c) den += fast_exp2(ml_s[c][tid].x - M_use) * ml_s[c][tid].y;
         const float inv = den > 0.f ? 1.f / den : 0.f;
-        for (int c = 0; c < n; ++c) w_s[c][tid] = fast_exp2(w_s[c][tid] - M_use) * inv;
+        for (int c = 0; c < n; ++c) ml_s[c][tid].x = fast_exp2(ml_s[c][tid].x - M_use) * inv;
     }
     __syncthreads();
-    for (int e = tid; e < p.R * p.d; e += 256) {
-        const int rr = e / p.d, dd = e % p.d;
-        const float* src = p.ws_o + (s0 * p.R + rr) * D + dd;
+#pragma unroll
+    for (int j = 0; j < EPT; ++j) {
+        const int e = tid + 256 * j;
+        if (e >= RD) break;
+        const int rr = e / D, dd = e % D;
         float acc = 0.f;
-        int c = 0;
-        for (; c + 4 <= n; c += 4) {
-            const float a0 = src[(int64_t)(c + 0) * p.R * D], a1 = src[(int64_t)(c + 1) * p.R * D];
-            const float a2 = src[(int64_t)(c + 2) * p.R * D], a3 = src[(int64_t)(c + 3) * p.R * D];
-            acc += w_s[c][rr] * a0 + w_s[c + 1][rr] * a1 + w_s[c + 2][rr] * a2 + w_s[c + 3][rr] * a3;
-        }
-        for (; c < n; ++c) acc += w_s[c][rr] * src[(int64_t)c * p.R * D];
-        out_ptr(rr)[dd] = acc;
+#pragma unroll
+        for (int c = 0; c < NPRE; ++c)
+            if (c < n) acc += ml_s[c][rr].x * pre[j][c];
+        for (int c = NPRE; c < n; ++c) acc += ml_s[c][rr].x * o_src[(int64_t)c * RD + e];
+        if (dd < p.d) out_ptr(rr)[dd] = acc;
     }
 }
 
