@@ -10,7 +10,9 @@
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
+#include <mutex>
 #include <string>
+#include <thread>
 #include <vector>
 
 #include "nne_attn.h"
@@ -57,6 +59,72 @@ bool dims_ok(const int64_t* s) {
 }
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+// Per-stream resources of the split-K kernel, one set per (device, stream) --
+// per calling thread for the per-thread default stream.  Launches on one
+// stream run in order, so they share the set:
+//   * arrival counters of the in-launch combine, zeroed by a fill kernel when
+//     allocated and left zeroed by every launch;
+//   * the workspace used when the caller passes none.
+// Both grow on demand (stream-ordered allocation; the replaced buffer is freed
+// in stream order after the launches queued before it) and are kept until the
+// process ends.
+struct StreamResources {
+    int dev;
+    hipStream_t stream;
+    std::thread::id thread;
+    uint32_t* counters;
+    int64_t n_counters;
+    void* ws;
+    uint64_t ws_bytes;
+};
+std::mutex g_res_mu;
+std::vector<StreamResources> g_res;
+
+// Counters for n heads and, when ws_bytes > 0, a workspace of that size.
+hipError_t stream_resources(int64_t n, uint64_t ws_bytes, hipStream_t s, uint32_t** counters,
+                            void** ws) {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return e;
+    const std::thread::id th =
+        s == hipStreamPerThread ? std::this_thread::get_id() : std::thread::id();
+    std::lock_guard<std::mutex> lock(g_res_mu);
+    StreamResources* r = nullptr;
+    for (auto& x : g_res)
+        if (x.dev == dev && x.stream == s && x.thread == th) r = &x;
+    if (!r) {
+        g_res.push_back(StreamResources{dev, s, th, nullptr, 0, nullptr, 0});
+        r = &g_res.back();
+    }
+    if (r->n_counters < n) {
+        int64_t cap = 1 << 16;
+        while (cap < n) cap <<= 1;
+        uint32_t* p = nullptr;
+        e = hipMallocAsync(reinterpret_cast<void**>(&p), (size_t)cap * 4, s);
+        if (e != hipSuccess) return e;
+        e = nne::zero_counters(p, cap, s);
+        if (e != hipSuccess) return e;
+        if (r->counters) (void)hipFreeAsync(r->counters, s);
+        r->counters = p;
+        r->n_counters = cap;
+    }
+    *counters = r->counters;
+    if (ws_bytes > 0) {
+        if (r->ws_bytes < ws_bytes) {
+            uint64_t cap = 1u << 20;
+            while (cap < ws_bytes) cap <<= 1;
+            void* p = nullptr;
+            e = hipMallocAsync(&p, cap, s);
+            if (e != hipSuccess) return e;
+            if (r->ws) (void)hipFreeAsync(r->ws, s);
+            r->ws = p;
+            r->ws_bytes = cap;
+        }
+        *ws = r->ws;
+    }
+    return hipSuccess;
+}
 
 // 16-byte vector access is valid for this view: unit dim stride and every
 // other stride a multiple of 4 floats, 16-byte aligned base.
@@ -117,12 +185,11 @@ int run_attention(const float* q, const int64_t* qs_, const int64_t* qst, const 
         p.B = B; p.Hq = Hq; p.Hkv = Hkv; p.Tq = Tq; p.d = d;
         p.qscale = scale * nne::kLog2e;
         const nne::SplitKWorkspace w = nne::splitk_workspace_layout(B, Hkv, (int)rows, d);
+        uint32_t* counters = nullptr;
         void* ws = nullptr;
-        hipError_t e = hipMallocAsync(&ws, w.total_bytes, stream);
-        if (e != hipSuccess) return hip_fail(e, "hipMallocAsync(split-K workspace)");
-        e = nne::launch_splitk(p, (int64_t)B * Hkv * Tk, Tk, ws, stream, nullptr);
-        hipError_t e2 = hipFreeAsync(ws, stream);
-        if (e == hipSuccess) e = e2;
+        hipError_t e = stream_resources((int64_t)B * Hkv, w.total_bytes, stream, &counters, &ws);
+        if (e != hipSuccess) return hip_fail(e, "split-K workspace");
+        e = nne::launch_splitk(p, (int64_t)B * Hkv * Tk, Tk, ws, stream, nullptr, counters);
         if (e != hipSuccess) return hip_fail(e, "split-K attention launch");
         return NNE_OK;
     }
@@ -401,22 +468,14 @@ int run_decode(const float* q, const int64_t* q_strides, const float* k_cache, c
     const nne::SplitKWorkspace w =
         nne::splitk_workspace_layout((int)B, (int)Hkv, (int)(Hq / Hkv), (int)d);
     void* ws = workspace;
-    bool owned = false;
-    hipError_t e = hipSuccess;
-    if (!ws) {
-        e = hipMallocAsync(&ws, w.total_bytes, s);
-        if (e != hipSuccess) return hip_fail(e, "hipMallocAsync(decode workspace)");
-        owned = true;
-    } else if (w.total_bytes > workspace_bytes) {
+    if (ws && w.total_bytes > workspace_bytes)
         return fail(NNE_EINVAL, "Invalid configuration or argument: decode workspace of %llu bytes "
                                 "is smaller than the %llu required",
                     (unsigned long long)workspace_bytes, (unsigned long long)w.total_bytes);
-    }
-    e = nne::launch_splitk(p, total_keys, max_len, ws, s, seq_lens.data());
-    if (owned) {
-        hipError_t e2 = hipFreeAsync(ws, s);
-        if (e == hipSuccess) e = e2;
-    }
+    uint32_t* counters = nullptr;
+    hipError_t e = stream_resources(B * Hkv, ws ? 0 : w.total_bytes, s, &counters, &ws);
+    if (e != hipSuccess) return hip_fail(e, "decode workspace");
+    e = nne::launch_splitk(p, total_keys, max_len, ws, s, seq_lens.data(), counters);
     if (e != hipSuccess) return hip_fail(e, "decode attention launch");
     if (append)
         for (int64_t b = 0; b < B; ++b) lens_host[b] += 1;

@@ -83,6 +83,12 @@ struct SplitKParams {
     // split kernel from lens into ws_pref.
     int arg_pref_valid;
     int arg_pref[kArgSeqs + 1];
+    // Fused combine (arg_pref_valid launches): the last workgroup to finish a
+    // split head merges its partial records; ws_cnt[head] counts arrivals and
+    // is left at zero.  max_parts bounds the workgroups sharing one head.
+    int fused;
+    int max_parts;
+    uint32_t* ws_cnt;        // [B*Hkv] arrival counters, zero between launches
     // workspace
     int32_t* ws_pref;        // [B+1] flattened start of each sequence (this launch)
     float* ws_ml;            // [slots][R][2] partial (max, sum); slot = workgroup + head

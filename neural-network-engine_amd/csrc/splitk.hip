@@ -37,6 +37,7 @@
 // No cross-workgroup synchronisation is used inside the split kernel: on
 // gfx950 an agent-scope fence is a whole-L2 writeback and invalidate, far more
 // expensive than the second launch.
+#include <algorithm>
 #include <utility>
 
 #include "nne_common.hpp"
@@ -110,6 +111,34 @@ __device__ __forceinline__ floatx4 mfma4(float a, float b, floatx4 c) {
     return __builtin_amdgcn_mfma_f32_4x4x1f32(a, b, c, CB, AB, 0);
 }
 
+// Partial records cross workgroups without a fence: they are written with
+// agent-scope relaxed atomic stores (global_store sc1, written through to the
+// device coherence point) and read with agent-scope relaxed atomic loads
+// (global_load sc1, never served from a stale per-XCD L2 line).  A writer waits
+// for its stores (vmcnt(0)) before its arrival is counted, and a reader loads
+// only after the count says every writer has arrived.  An agent-scope
+// release/acquire pair would also write back and invalidate the whole L2 of
+// each XCD, which costs tens of microseconds per launch.
+__device__ __forceinline__ void store_coherent(float* p, float x) {
+    __hip_atomic_store(p, x, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float load_coherent(const float* p) {
+    return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void wait_stores_performed() {
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0), expcnt/lgkmcnt unconstrained
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
+// Monotonic map of floats (incl. -inf) to unsigned, for LDS atomic max.
+__device__ __forceinline__ unsigned float_order(float x) {
+    const unsigned u = __float_as_uint(x);
+    return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+__device__ __forceinline__ float float_unorder(unsigned k) {
+    return __uint_as_float((k & 0x80000000u) ? (k & 0x7fffffffu) : ~k);
+}
+
 // Orders this wave's LDS accesses on both sides of a cross-lane exchange.
 __device__ __forceinline__ void wave_lds_sync() {
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -156,6 +185,64 @@ __device__ __forceinline__ void build_prefix(const SplitKParams& p, int* pref, i
     }
 }
 
+// Merges the n partial records (slots s0 .. s0+n-1) of one head into its
+// output, then clears the head's arrival counter.  n * R <= 1024 (the host
+// bounds the workgroups per head), so each thread holds at most 4 records.
+template <int D>
+__device__ __forceinline__ void merge_head_records(const SplitKParams& p, int b, int kvh, int head,
+                                                   int64_t s0, int n, float* w_s, unsigned* red_m,
+                                                   float* red_l, int tid) {
+    const int NR = n * p.R;
+    float mv[4], lv[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        const int e = tid + 256 * k;
+        const int c = e / p.R, rr = e % p.R;
+        mv[k] = e < NR ? load_coherent(p.ws_ml + ((s0 + c) * p.R + rr) * 2) : kNegInf;
+        lv[k] = e < NR ? load_coherent(p.ws_ml + ((s0 + c) * p.R + rr) * 2 + 1) : 0.f;
+    }
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        const int e = tid + 256 * k;
+        if (e < NR) atomicMax(red_m + e % p.R, float_order(mv[k]));
+    }
+    __syncthreads();
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        const int e = tid + 256 * k;
+        if (e < NR) {
+            const float M = float_unorder(red_m[e % p.R]);
+            const float f = fast_exp2(mv[k] - (M == kNegInf ? 0.f : M));
+            w_s[e] = f;
+            atomicAdd(red_l + e % p.R, f * lv[k]);
+        }
+    }
+    __syncthreads();
+    const int RD = p.R * D;
+    const float* o_src = p.ws_o + s0 * RD;
+    for (int e = tid; e < RD; e += 256) {
+        const int rr = e / D, dd = e % D;
+        float acc = 0.f;
+        int c = 0;
+        for (; c + 4 <= n; c += 4) {
+            const float a0 = load_coherent(o_src + (int64_t)(c + 0) * RD + e);
+            const float a1 = load_coherent(o_src + (int64_t)(c + 1) * RD + e);
+            const float a2 = load_coherent(o_src + (int64_t)(c + 2) * RD + e);
+            const float a3 = load_coherent(o_src + (int64_t)(c + 3) * RD + e);
+            acc += w_s[(c + 0) * p.R + rr] * a0 + w_s[(c + 1) * p.R + rr] * a1 +
+                   w_s[(c + 2) * p.R + rr] * a2 + w_s[(c + 3) * p.R + rr] * a3;
+        }
+        for (; c < n; ++c) acc += w_s[c * p.R + rr] * load_coherent(o_src + (int64_t)c * RD + e);
+        if (dd < p.d) {
+            const float den = red_l[rr];
+            const int hq = kvh * p.G + rr / p.Tq, t = rr % p.Tq;
+            p.o.p[b * p.o.sb + hq * p.o.sh + t * p.o.st + dd] = den > 0.f ? acc / den : 0.f;
+        }
+    }
+    if (tid == 0)
+        __hip_atomic_store(p.ws_cnt + head, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 // ROWS = 16: R <= 16 query rows per KV head on v_mfma_f32_16x16x4_f32 (above).
 // ROWS = 4: R <= 4 rows (single-token decode with G <= 4) on
 // v_mfma_f32_4x4x1_16b_f32, which wastes no MFMA work on padding rows:
@@ -186,6 +273,10 @@ __global__ __launch_bounds__(256, 2) void splitk_kernel(const SplitKParams p) {
     __shared__ __attribute__((aligned(16))) float lds[4 * KB * KS];
     __shared__ float ml_s[4][16][2];
     __shared__ vf4 p_s[4][16];           // narrow: P of a wave's 16 keys
+    __shared__ unsigned red_m[16];       // fused combine: per-row max (ordered)
+    __shared__ float red_l[16];          // fused combine: per-row denominator
+    __shared__ int pend_s[2][3];         // fused combine: heads this workgroup merges
+    __shared__ int n_pend_s;
     __shared__ int pref[MAX_SEQS + 1];
 
     const int tid = threadIdx.x, lane = tid & 63;
@@ -205,6 +296,17 @@ __global__ __launch_bounds__(256, 2) void splitk_kernel(const SplitKParams p) {
         for (int b = tid; b <= p.B; b += 256) p.ws_pref[b] = pref[b];
 
     const int total = pref[p.B];
+    if (tid == 0) n_pend_s = 0;
+    if (p.fused && wg == 0) {            // sequences with no keys: zero output
+        for (int bb = 0; bb < p.B; ++bb) {
+            if (pref[bb + 1] != pref[bb]) continue;
+            for (int e = tid; e < p.Hkv * p.R * p.d; e += 256) {
+                const int dd = e % p.d, rest = e / p.d, rr = rest % p.R, kv = rest / p.R;
+                const int hq = kv * p.G + rr / p.Tq, t = rr % p.Tq;
+                p.o.p[bb * p.o.sb + hq * p.o.sh + t * p.o.st + dd] = 0.f;
+            }
+        }
+    }
     int g = wg * p.chunk;
     const int g_end = min(total, g + p.chunk);
     if (g >= g_end) return;
@@ -246,6 +348,7 @@ __global__ __launch_bounds__(256, 2) void splitk_kernel(const SplitKParams p) {
         // no load waits on it.  16-row tile: stored into the cache first and
         // read back like any cached row.
         const bool has_new = APPEND && key_end == Lb;
+        if (p.fused && has_new && p.lens_w && kvh == 0 && tid == 0) p.lens_w[b] = Lb;
         vf4 nk = vf4{0.f, 0.f, 0.f, 0.f}, nv = nk;
         if (NARROW && has_new) {
             nk = *reinterpret_cast<const vf4*>(p.k_new + b * p.kn_sb + kvh * p.kn_sh + kc_col);
@@ -272,22 +375,24 @@ __global__ __launch_bounds__(256, 2) void splitk_kernel(const SplitKParams p) {
             const int hq = kvh * p.G + (rok ? ni / p.Tq : 0), t = rok ? ni % p.Tq : 0;
             const float* qp = p.q.p + b * p.q.sb + hq * p.q.sh + t * p.q.st;
 #pragma unroll
-            for (int t4 = 0; t4 < NQN; ++t4) {
+            for (int t4 = 0; t4 < NQN; ++t4) {   // clamped loads, then select: no waits between them
                 const int c = grp * (D / 4) + 4 * t4 + na;
-                qf[t4] = (rok && c < p.d) ? qp[c] * p.qscale : 0.f;
+                const float x = qp[min(c, p.d - 1)];
+                qf[t4] = (rok && c < p.d) ? x * p.qscale : 0.f;
             }
         } else {
             const bool rok = col < p.R;
             const int hq = kvh * p.G + (rok ? col / p.Tq : 0), t = rok ? col % p.Tq : 0;
             const float* qp = p.q.p + b * p.q.sb + hq * p.q.sh + t * p.q.st;
 #pragma unroll
-            for (int s4 = 0; s4 < NQ / 4; ++s4) {
+            for (int s4 = 0; s4 < NQ / 4; ++s4) {   // clamped loads, then select
                 const int c = grp * NQ + 4 * s4;
-                vf4 x = (rok && c < p.d) ? *reinterpret_cast<const vf4*>(qp + c) : vf4{0.f, 0.f, 0.f, 0.f};
-                qf[4 * s4 + 0] = x.x * p.qscale;
-                qf[4 * s4 + 1] = x.y * p.qscale;
-                qf[4 * s4 + 2] = x.z * p.qscale;
-                qf[4 * s4 + 3] = x.w * p.qscale;
+                const vf4 x = *reinterpret_cast<const vf4*>(qp + min(c, p.d - 4));
+                const bool ok = rok && c < p.d;
+                qf[4 * s4 + 0] = ok ? x.x * p.qscale : 0.f;
+                qf[4 * s4 + 1] = ok ? x.y * p.qscale : 0.f;
+                qf[4 * s4 + 2] = ok ? x.z * p.qscale : 0.f;
+                qf[4 * s4 + 3] = ok ? x.w * p.qscale : 0.f;
             }
         }
 
@@ -520,15 +625,45 @@ __global__ __launch_bounds__(256, 2) void splitk_kernel(const SplitKParams p) {
                     p.o.p[b * p.o.sb + hq * p.o.sh + t * p.o.st + dd] = l > 0.f ? acc / l : 0.f;
                 }
             } else {
-                p.ws_o[(slot * p.R + rr) * D + dd] = acc;
+                store_coherent(p.ws_o + (slot * p.R + rr) * D + dd, acc);
                 if (dd == 0) {
-                    p.ws_ml[(slot * p.R + rr) * 2] = M;
-                    p.ws_ml[(slot * p.R + rr) * 2 + 1] = l;
+                    store_coherent(p.ws_ml + (slot * p.R + rr) * 2, M);
+                    store_coherent(p.ws_ml + (slot * p.R + rr) * 2 + 1, l);
+                }
+            }
+        }
+        if (p.fused && !whole) {
+            // Count this workgroup in.  The last of the head's n workgroups
+            // merges it after its own segments (a workgroup has at most two
+            // split heads: its first and its last segment).
+            wait_stores_performed();
+            __syncthreads();
+            if (tid == 0) {
+                const int w_first = h_start / p.chunk, w_last = (h_start + Lb - 1) / p.chunk;
+                const unsigned old = __hip_atomic_fetch_add(p.ws_cnt + head, 1u, __ATOMIC_RELAXED,
+                                                            __HIP_MEMORY_SCOPE_AGENT);
+                if (old == (unsigned)(w_last - w_first) && n_pend_s < 2) {
+                    pend_s[n_pend_s][0] = b;
+                    pend_s[n_pend_s][1] = kvh;
+                    pend_s[n_pend_s][2] = w_first;
+                    ++n_pend_s;
                 }
             }
         }
         __syncthreads();                  // LDS is reused by the next segment
         g = h_start + key_end;
+    }
+    const int n_pend = n_pend_s;
+    for (int i = 0; i < n_pend; ++i) {
+        const int bb = pend_s[i][0], kv = pend_s[i][1], w_first = pend_s[i][2];
+        const int L = (pref[bb + 1] - pref[bb]) / p.Hkv;
+        const int h0 = pref[bb] + kv * L;
+        const int n = (h0 + L - 1) / p.chunk - w_first + 1;
+        if (tid < 16) { red_m[tid] = float_order(kNegInf); red_l[tid] = 0.f; }
+        __syncthreads();
+        merge_head_records<D>(p, bb, kv, bb * p.Hkv + kv, (int64_t)w_first + bb * p.Hkv + kv, n,
+                              lds, red_m, red_l, tid);
+        __syncthreads();
     }
 }
 
@@ -617,6 +752,7 @@ hipError_t launch_splitk_d(const SplitKParams& p, hipStream_t stream) {
         hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;
     }
+    if (p.fused) return hipSuccess;
     hipLaunchKernelGGL((splitk_combine_kernel<D>), dim3(p.B * p.Hkv), dim3(256), 0, stream, p);
     return hipGetLastError();
 }
@@ -640,6 +776,12 @@ __global__ void kv_append_kernel(float* kc, float* vc, const int32_t* lens, View
         kc[dst] = kn.p[b * kn.sb + h * kn.sh + t * kn.st + dd * kn.sd];
         vc[dst] = vn.p[b * vn.sb + h * vn.sh + t * vn.st + dd * vn.sd];
     }
+}
+
+__global__ void zero_u32_kernel(uint32_t* x, int64_t n) {
+    for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n;
+         i += (int64_t)gridDim.x * blockDim.x)
+        x[i] = 0u;
 }
 
 __global__ void lens_bump_kernel(int32_t* lens, int B, int t_new) {
@@ -696,10 +838,10 @@ hipError_t launch_flat(SplitKParams p, int64_t total_keys, int max_len, hipStrea
     const bool narrow = p.R <= 4;
     const int slots = p.k_new ? (narrow ? resident_workgroups<D, true, 4>() : resident_workgroups<D, true, 16>())
                               : (narrow ? resident_workgroups<D, false, 4>() : resident_workgroups<D, false, 16>());
-    // Equal flattened chunks, whole 16-key blocks, and at most MAX_PARTS - 2
-    // workgroups sharing any one head.
+    // Equal flattened chunks, whole 16-key blocks, and at most max_parts
+    // workgroups sharing any one head (a chunk boundary can add two).
     int64_t chunk = (total_keys + slots - 1) / (slots > 0 ? slots : 1);
-    const int64_t min_chunk = (max_len + (MAX_PARTS - 2) - 1) / (MAX_PARTS - 2);
+    const int64_t min_chunk = (max_len + (p.max_parts - 2) - 1) / (p.max_parts - 2);
     if (chunk < min_chunk) chunk = min_chunk;
     chunk = (chunk + KB - 1) / KB * KB;
     if (chunk < KB) chunk = KB;
@@ -712,7 +854,7 @@ hipError_t launch_flat(SplitKParams p, int64_t total_keys, int max_len, hipStrea
 }  // namespace
 
 hipError_t launch_splitk(SplitKParams p, int64_t total_keys, int max_len, void* workspace,
-                         hipStream_t stream, const int32_t* seq_lens) {
+                         hipStream_t stream, const int32_t* seq_lens, uint32_t* counters) {
     // Small batches carry the flattened prefix in the arguments, which saves
     // every workgroup the scan over lens.
     p.arg_pref_valid = p.B <= kArgSeqs ? 1 : 0;
@@ -723,9 +865,14 @@ hipError_t launch_splitk(SplitKParams p, int64_t total_keys, int max_len, void* 
     }
     p.G = p.Hq / p.Hkv;
     p.R = p.G * p.Tq;
+    // Fused combine needs the prefix in the arguments (no workgroup reads
+    // lens, so the lens bump can happen inside the launch) and n * R <= 1024.
+    p.fused = p.arg_pref_valid && counters != nullptr;
+    p.max_parts = p.fused ? std::min(MAX_PARTS, 1024 / p.R) : MAX_PARTS;
     const SplitKWorkspace w = splitk_workspace_layout(p.B, p.Hkv, p.R, p.d);
     char* base = static_cast<char*>(workspace);
     p.ws_pref = reinterpret_cast<int32_t*>(base);
+    p.ws_cnt = counters;
     p.ws_ml = reinterpret_cast<float*>(base + w.ml_offset);
     p.ws_o = reinterpret_cast<float*>(base + w.o_offset);
     switch (splitk_padded_dim(p.d)) {
@@ -733,6 +880,14 @@ hipError_t launch_splitk(SplitKParams p, int64_t total_keys, int max_len, void* 
         case 128: return launch_flat<128>(p, total_keys, max_len, stream);
         default: return hipErrorInvalidValue;
     }
+}
+
+hipError_t zero_counters(uint32_t* counters, int64_t n, hipStream_t stream) {
+    if (n <= 0) return hipSuccess;
+    int64_t blocks = (n + 255) / 256;
+    if (blocks > 1024) blocks = 1024;
+    hipLaunchKernelGGL(zero_u32_kernel, dim3((unsigned)blocks), dim3(256), 0, stream, counters, n);
+    return hipGetLastError();
 }
 
 hipError_t launch_kv_append(float* kc, float* vc, int32_t* lens_dev, View4 kn, View4 vn, int B,

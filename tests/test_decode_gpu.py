@@ -175,3 +175,61 @@ def test_workspace_argument_paths(nne, cuda):
             T.assert_close(host(out), ref, what="library workspace")
         else:
             assert rc == nne.NNE_EINVAL
+
+
+def test_split_head_handoff_alternating_inputs(nne, cuda):
+    """Heads split across workgroups are merged inside the launch by the last
+    workgroup to arrive.  Back-to-back calls on one stream alternate between
+    two unrelated caches and queries with the same geometry, with no host
+    synchronisation between them, so a merge that read another call's partial
+    records would not match its own reference."""
+    import torch
+    rng = np.random.default_rng(21)
+    b, hq, hkv, d = 3, 16, 4, 128
+    lens = np.array([9000, 17, 6000], np.int32)
+    cap = 9100
+    caches = [make_cache(nne, cuda, b, hkv, cap, d, lens, rng) for _ in range(2)]
+    qs = [rnd(rng, b, hq, 1, d) for _ in range(2)]
+    refs = [T.ref_decode_attend(qs[i], caches[i][1], caches[i][2], lens) for i in range(2)]
+    qd = [dev(q, cuda) for q in qs]
+    outs = [torch.empty(b, hq, 1, d, device=cuda) for _ in range(12)]
+    for j, o in enumerate(outs):
+        caches[j % 2][0].attend(0, qd[j % 2], out=o)
+    for j, o in enumerate(outs):
+        T.assert_close(host(o), refs[j % 2], what="alternating call %d" % j)
+
+
+def test_few_query_handoff_alternating_inputs(nne, cuda):
+    """The same check for few-query cross-attention (prefill entry point)."""
+    import torch
+    rng = np.random.default_rng(22)
+    q = [rnd(rng, 2, 8, 2, 64) for _ in range(2)]
+    k = [rnd(rng, 2, 4, 7000, 64) for _ in range(2)]
+    v = [rnd(rng, 2, 4, 7000, 64) for _ in range(2)]
+    refs = [T.ref_standard(q[i], k[i], v[i], False) for i in range(2)]
+    qd, kd, vd = ([dev(x, cuda) for x in xs] for xs in (q, k, v))
+    outs = [torch.empty(2, 8, 2, 64, device=cuda) for _ in range(10)]
+    for j, o in enumerate(outs):
+        nne.attention_forward(qd[j % 2], kd[j % 2], vd[j % 2], False, out=o)
+    for j, o in enumerate(outs):
+        T.assert_close(host(o), refs[j % 2], what="alternating cross call %d" % j)
+
+
+def test_large_batch_uses_combine_kernel(nne, cuda):
+    """More than 128 sequences: the prefix is scanned on the GPU and a second
+    kernel merges the split heads; includes empty sequences and a decode step."""
+    rng = np.random.default_rng(23)
+    b, hq, hkv, d = 150, 8, 2, 64
+    lens = rng.integers(0, 700, size=b).astype(np.int32)
+    lens[[3, 77]] = 0
+    lens[10] = 3000
+    cap = 3100
+    cache, kc, vc = make_cache(nne, cuda, b, hkv, cap, d, lens, rng)
+    q = rnd(rng, b, hq, 1, d)
+    out = host(cache.attend(0, dev(q, cuda)))
+    T.assert_close(out, T.ref_decode_attend(q, kc, vc, lens), what="B=150 attend")
+    kn, vn = rnd(rng, b, hkv, 1, d), rnd(rng, b, hkv, 1, d)
+    out = host(cache.decode_step(0, dev(q, cuda), dev(kn, cuda), dev(vn, cuda)))
+    ref, kc, vc, lens = T.ref_decode_step(q, kc, vc, lens, kn, vn)
+    T.assert_close(out, ref, what="B=150 step")
+    assert list(host(cache.lens_dev[0])) == list(lens)
