@@ -188,11 +188,24 @@ __device__ __forceinline__ void build_prefix(const SplitKParams& p, int* pref, i
 // Merges the n partial records (slots s0 .. s0+n-1) of one head into its
 // output, then clears the head's arrival counter.  n * R <= 1024 (the host
 // bounds the workgroups per head), so each thread holds at most 4 records.
-template <int D>
+template <int D, int ROWS>
 __device__ __forceinline__ void merge_head_records(const SplitKParams& p, int b, int kvh, int head,
                                                    int64_t s0, int n, float* w_s, unsigned* red_m,
                                                    float* red_l, int tid) {
+    constexpr int EPT = ROWS * D / 256;   // output elements per thread (R <= ROWS)
+    constexpr int NPRE = EPT >= 8 ? 2 : 4;  // partials per element loaded up front
     const int NR = n * p.R;
+    const int RD = p.R * D;
+    const float* o_src = p.ws_o + s0 * RD;
+    // Every load is issued before the first barrier: one memory round trip.
+    float pre[EPT][NPRE];
+#pragma unroll
+    for (int j = 0; j < EPT; ++j) {
+        const int e = tid + 256 * j;
+#pragma unroll
+        for (int c = 0; c < NPRE; ++c)
+            pre[j][c] = (e < RD && c < n) ? load_coherent(o_src + (int64_t)c * RD + e) : 0.f;
+    }
     float mv[4], lv[4];
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
@@ -218,21 +231,17 @@ __device__ __forceinline__ void merge_head_records(const SplitKParams& p, int b,
         }
     }
     __syncthreads();
-    const int RD = p.R * D;
-    const float* o_src = p.ws_o + s0 * RD;
-    for (int e = tid; e < RD; e += 256) {
+#pragma unroll
+    for (int j = 0; j < EPT; ++j) {
+        const int e = tid + 256 * j;
+        if (e >= RD) break;
         const int rr = e / D, dd = e % D;
         float acc = 0.f;
-        int c = 0;
-        for (; c + 4 <= n; c += 4) {
-            const float a0 = load_coherent(o_src + (int64_t)(c + 0) * RD + e);
-            const float a1 = load_coherent(o_src + (int64_t)(c + 1) * RD + e);
-            const float a2 = load_coherent(o_src + (int64_t)(c + 2) * RD + e);
-            const float a3 = load_coherent(o_src + (int64_t)(c + 3) * RD + e);
-            acc += w_s[(c + 0) * p.R + rr] * a0 + w_s[(c + 1) * p.R + rr] * a1 +
-                   w_s[(c + 2) * p.R + rr] * a2 + w_s[(c + 3) * p.R + rr] * a3;
-        }
-        for (; c < n; ++c) acc += w_s[c * p.R + rr] * load_coherent(o_src + (int64_t)c * RD + e);
+#pragma unroll
+        for (int c = 0; c < NPRE; ++c)
+            if (c < n) acc += w_s[c * p.R + rr] * pre[j][c];
+        for (int c = NPRE; c < n; ++c)
+            acc += w_s[c * p.R + rr] * load_coherent(o_src + (int64_t)c * RD + e);
         if (dd < p.d) {
             const float den = red_l[rr];
             const int hq = kvh * p.G + rr / p.Tq, t = rr % p.Tq;
@@ -661,7 +670,7 @@ __global__ __launch_bounds__(256, 2) void splitk_kernel(const SplitKParams p) {
         const int n = (h0 + L - 1) / p.chunk - w_first + 1;
         if (tid < 16) { red_m[tid] = float_order(kNegInf); red_l[tid] = 0.f; }
         __syncthreads();
-        merge_head_records<D>(p, bb, kv, bb * p.Hkv + kv, (int64_t)w_first + bb * p.Hkv + kv, n,
+        merge_head_records<D, ROWS>(p, bb, kv, bb * p.Hkv + kv, (int64_t)w_first + bb * p.Hkv + kv, n,
                               lds, red_m, red_l, tid);
         __syncthreads();
     }
