@@ -30,11 +30,12 @@ PEAK_HBM_GBS = 8000.0
 
 # HBM bytes per launch measured with rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE on
 # the `--probe` workload, each scaled by its reading for a plain 1 GiB device copy
-# (FETCH_SIZE x2.00, WRITE_SIZE x1.00).  Config 2 prefill: 215.8 MB read + 134.2 MB
-# written (algorithmic 201.3 + 134.2).  Config 3 decode step (split + combine):
-# 647.4 MB read + 2.4 MB written (algorithmic ~646 + ~1.3).
-TRAFFIC_PREFILL_CONFIG2 = int(215.8e6 + 134.2e6)
-TRAFFIC_DECODE_CONFIG3_STEP = int(647.4e6 + 2.4e6)
+# (FETCH_SIZE x2.00, WRITE_SIZE x1.00).  Config 2 prefill: 203.6 MB read + 134.2 MB
+# written (algorithmic 201.3 + 134.2).  Config 3 decode step (one launch, split
+# heads merged inside it): 648.0 MB read + 3.1 MB written (algorithmic ~646 + 0.8,
+# plus the partial records of split heads).
+TRAFFIC_PREFILL_CONFIG2 = round(203.6e6 + 134.2e6)
+TRAFFIC_DECODE_CONFIG3_STEP = round(648.0e6 + 3.1e6)
 
 
 def load_pkg():
@@ -185,6 +186,14 @@ def probe(nne, torch, dev):
     del q, k, v, out
     bench_decode(nne, torch, dev, steps=8, warmup=1)
     torch.cuda.synchronize()
+    g = torch.Generator(device=dev).manual_seed(0x5EED0005)
+    qx = torch.randn(8, 20, 8, 64, generator=g, device=dev)
+    ox = torch.empty_like(qx)
+    kvs = [(torch.randn(8, 20, 1500, 64, generator=g, device=dev),
+            torch.randn(8, 20, 1500, 64, generator=g, device=dev)) for _ in range(3)]
+    for i in range(6):                        # config 5b, K/V sets rotated past the MALL
+        nne.attention_forward(qx, kvs[i % 3][0], kvs[i % 3][1], False, out=ox)
+    torch.cuda.synchronize()
     print("probe done", file=sys.stderr, flush=True)
 
 
@@ -198,7 +207,8 @@ def main():
     ap.add_argument("--all", action="store_true", help="also print lines for configs 1, 4, 5")
     ap.add_argument("--probe", action="store_true",
                     help="counter-collection run: a 1 GiB device copy (calibrates FETCH_SIZE/"
-                         "WRITE_SIZE), 3 config-2 prefills and 8 config-3 decode steps")
+                         "WRITE_SIZE), 3 config-2 prefills, 8 config-3 decode steps and 6 "
+                         "config-5b cross-attention calls")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
