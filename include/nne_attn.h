@@ -106,8 +106,12 @@ uint64_t nne_decode_workspace_bytes(int64_t B, int64_t Hq, int64_t Hkv, int64_t 
 /* Single-token decode attention over the cache: q [B, Hq, 1, d] attends to
  * the first lens[b] rows of its sequence, no mask (llama.rs:239-296 with
  * t = 1).  Ragged lengths are allowed; Hq / Hkv <= 16.  workspace may be NULL
- * (the library then allocates stream-ordered scratch) or a device buffer of
- * at least nne_decode_workspace_bytes(B, Hq, Hkv, d, max(lens_host)) bytes. */
+ * (the library then uses its own per-stream workspace, allocated in stream
+ * order on first use and kept until the process ends) or a device buffer of
+ * at least nne_decode_workspace_bytes(B, Hq, Hkv, d, max(lens_host)) bytes.
+ * The library also keeps, per (device, stream), a small zeroed array of
+ * arrival counters that launches on that stream share; launches on
+ * different streams never share it. */
 int nne_decode_attention(const float *q, const int64_t q_strides[4], const float *k_cache,
                          const float *v_cache, const int32_t *lens_dev, const int32_t *lens_host,
                          float *o, const int64_t o_strides[4], int64_t B, int64_t Hq, int64_t Hkv,
