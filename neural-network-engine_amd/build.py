@@ -2,7 +2,9 @@
 
     python neural-network-engine_amd/build.py
 
-produces neural-network-engine_amd/lib/libnne_attn.so (HIP kernels + C ABI).
+produces neural-network-engine_amd/lib/libnne_attn.so (HIP kernels + C ABI) and
+neural-network-engine_amd/lib/libnne_host.so (the C++ host API of host/nne.hpp,
+on top of the C ABI and rocBLAS).
 Every build recompiles; nothing is cached outside the repository, so the
 built file travels with the tree to the GPU machine.
 """
@@ -15,6 +17,7 @@ ROOT = os.path.dirname(PKG)
 CSRC = os.path.join(PKG, "csrc")
 LIB_DIR = os.path.join(PKG, "lib")
 LIB = os.path.join(LIB_DIR, "libnne_attn.so")
+HOST_LIB = os.path.join(LIB_DIR, "libnne_host.so")
 
 SOURCES = ["prefill.hip", "splitk.hip", "abi.cpp"]
 
@@ -35,14 +38,9 @@ def hipcc():
     return os.path.join(rocm, "bin", "hipcc")
 
 
-def build_library(verbose=False):
-    os.makedirs(LIB_DIR, exist_ok=True)
-    tmp = LIB + ".tmp"
-    cmd = [hipcc()] + HIPCC_FLAGS + [
-        "-I" + os.path.join(ROOT, "include"),
-        "-I" + CSRC,
-        "-o", tmp,
-    ] + [os.path.join(CSRC, s) for s in SOURCES]
+def _run(cmd, out, verbose):
+    tmp = out + ".tmp"
+    cmd = cmd + ["-o", tmp]
     if verbose:
         print(" ".join(cmd), flush=True)
     res = subprocess.run(cmd, capture_output=True, text=True)
@@ -52,9 +50,36 @@ def build_library(verbose=False):
         raise RuntimeError("hipcc failed:\n" + err)
     if verbose and err.strip():
         print(err, file=sys.stderr)
-    os.replace(tmp, LIB)
-    return LIB
+    os.replace(tmp, out)
+    return out
+
+
+def build_library(verbose=False):
+    os.makedirs(LIB_DIR, exist_ok=True)
+    cmd = [hipcc()] + HIPCC_FLAGS + [
+        "-I" + os.path.join(ROOT, "include"),
+        "-I" + CSRC,
+    ] + [os.path.join(CSRC, s) for s in SOURCES]
+    return _run(cmd, LIB, verbose)
+
+
+def build_host_library(verbose=False):
+    """The C++ host API; links libnne_attn.so from the same directory."""
+    cmd = [hipcc()] + HIPCC_FLAGS + [
+        "-I" + os.path.join(ROOT, "include"),
+        "-I" + os.path.join(PKG, "host"),
+        os.path.join(PKG, "host", "nne_host.hip"),
+        "-L" + LIB_DIR, "-lnne_attn",
+        "-L" + os.path.join(os.environ.get("ROCM_PATH", "/opt/rocm"), "lib"), "-lrocblas",
+        "-Wl,-rpath,$ORIGIN",
+    ]
+    return _run(cmd, HOST_LIB, verbose)
+
+
+def build_all(verbose=False):
+    return [build_library(verbose), build_host_library(verbose)]
 
 
 if __name__ == "__main__":
-    print(build_library(verbose=True))
+    for path in build_all(verbose=True):
+        print(path)

@@ -1,0 +1,216 @@
+// nne.hpp -- C++ host API of the MI355X attention path, mirroring the
+// reference engine's Rust API for this path so that a caller (or a test) reads
+// the same way as against the reference:
+//
+//   flash_attention_forward(q, k, v, is_causal, scale, block_size_r,
+//                           block_size_c) -> Result<RawTensor>
+//                                      src/nn/flash_attention.rs:19-199
+//   FlashAttention{q_proj, k_proj, v_proj, out_proj, num_heads, d_model,
+//                  head_dim, is_causal, block_size}, new / forward_flash /
+//                  forward                src/nn/flash_attention.rs:202-292
+//   Linear{weight, bias, in_features, out_features}, new / forward
+//                                      src/nn/linear.rs:9-60
+//   KVCache new / reset / num_layers / current_seq_len / update
+//                                      src/nn/kv_cache.rs:11-74
+//   EngineError / Result<T>            src/error.rs:6-58
+//
+// Differences that come from the hardware, not from taste:
+//   * RawTensor data live in device memory (HBM); to_vec() copies to the host.
+//     Views (transpose, slice, reshape of contiguous data) share storage, as the
+//     reference's strided RawTensor does (src/tensor/mod.rs:20-27).
+//   * KVCache is device-resident with a capacity fixed at creation and rows
+//     appended in place (the reference concatenates, kv_cache.rs:63-72); it
+//     adds decode_step / attend for single-token decode (llama.rs:239-296,
+//     t = 1) and accepts ragged per-sequence lengths.
+//   * attention_forward is the grouped-query entry (Hkv divides Hq, query head
+//     hq reads KV head hq / (Hq / Hkv), llama.rs:256-266; causal key c visible
+//     to row r iff c <= r + q_offset) that the reference spreads over its
+//     model code.
+//   * randn / uniform draw from a seeded generator (manual_seed); the
+//     reference's thread_rng is unseeded.
+// Everything runs on the HIP default stream; every call that returns data to
+// the host synchronises it.  All compute goes through include/nne_attn.h.
+#pragma once
+
+#include <cstddef>
+#include <cstdint>
+#include <memory>
+#include <optional>
+#include <stdexcept>
+#include <string>
+#include <utility>
+#include <variant>
+#include <vector>
+
+namespace nne {
+
+// src/error.rs:8-52: the variants this path produces, with the same messages.
+struct EngineError {
+    enum class Kind { ShapeMismatch, IncompatibleShapes, InvalidArgument, GpuError, NonContiguousTensor };
+    Kind kind = Kind::InvalidArgument;
+    std::vector<size_t> expected, actual;        // ShapeMismatch
+    std::string op;                              // IncompatibleShapes
+    std::vector<std::vector<size_t>> shapes;     // IncompatibleShapes
+    std::string message;                         // InvalidArgument / GpuError payload
+
+    static EngineError shape_mismatch(std::vector<size_t> expected, std::vector<size_t> actual);
+    static EngineError incompatible_shapes(std::string op, std::vector<std::vector<size_t>> shapes);
+    static EngineError invalid_argument(std::string message);
+    static EngineError gpu_error(std::string message);
+    static EngineError non_contiguous_tensor();
+
+    std::string to_string() const;               // the #[error(...)] text of the variant
+    bool operator==(const EngineError& o) const;
+};
+
+// Result<T> = std::result::Result<T, EngineError> (src/error.rs:6).
+template <class T>
+class Result {
+  public:
+    Result(T value) : v_(std::move(value)) {}
+    Result(EngineError error) : v_(std::move(error)) {}
+    bool is_ok() const { return v_.index() == 0; }
+    bool is_err() const { return v_.index() == 1; }
+    const T& value() const { return check(), std::get<0>(v_); }
+    T& value() { return check(), std::get<0>(v_); }
+    const EngineError& error() const {
+        if (is_ok()) throw std::logic_error("called error() on an Ok Result");
+        return std::get<1>(v_);
+    }
+    // Rust's unwrap(): the value, or a std::runtime_error carrying the error text.
+    T unwrap() { return check(), std::move(std::get<0>(v_)); }
+
+  private:
+    void check() const {
+        if (is_err()) throw std::runtime_error(std::get<1>(v_).to_string());
+    }
+    std::variant<T, EngineError> v_;
+};
+
+// Seeds the generator behind RawTensor::randn / uniform and the layer inits.
+void manual_seed(uint64_t seed);
+
+// Strided f32 tensor in device memory (src/tensor/mod.rs:20-27).
+class RawTensor {
+  public:
+    RawTensor() = default;                               // no storage, shape []
+
+    // src/tensor/mod.rs:60-77; throws std::invalid_argument if data.size() != numel(shape).
+    static RawTensor from_vec(const std::vector<float>& data, std::vector<size_t> shape);
+    static RawTensor zeros(const std::vector<size_t>& shape);
+    static RawTensor randn(const std::vector<size_t>& shape, float mean, float std);
+    static RawTensor uniform(const std::vector<size_t>& shape, float low, float high);
+    static RawTensor kaiming_uniform(const std::vector<size_t>& shape, size_t fan_in);
+
+    const std::vector<size_t>& shape() const { return shape_; }
+    const std::vector<size_t>& strides() const { return strides_; }  // in elements
+    size_t ndim() const { return shape_.size(); }
+    size_t numel() const;
+    bool is_contiguous() const;
+
+    float* data() const;                                 // device pointer of element 0
+    std::vector<float> to_vec() const;                   // row-major copy on the host
+    RawTensor to_contiguous() const;                     // device copy when strided
+
+    Result<RawTensor> transpose(size_t a, size_t b) const;          // view
+    Result<RawTensor> reshape(const std::vector<size_t>& shape) const;
+    Result<RawTensor> slice(size_t axis, size_t start, size_t end) const;  // view
+
+    // Wraps device memory owned elsewhere (kept alive by `owner`).
+    static RawTensor view(std::shared_ptr<float> owner, size_t offset, std::vector<size_t> shape,
+                          std::vector<size_t> strides);
+
+  private:
+    std::shared_ptr<float> storage_;
+    size_t offset_ = 0;
+    std::vector<size_t> shape_, strides_;
+};
+
+// src/nn/flash_attention.rs:19-199.  Output: a new contiguous [B, H, Tq, d].
+Result<RawTensor> flash_attention_forward(const RawTensor& q, const RawTensor& k, const RawTensor& v,
+                                          bool is_causal, std::optional<float> scale,
+                                          size_t block_size_r, size_t block_size_c);
+
+// Grouped-query attention core (llama.rs:253-296; attention.rs:93-122, 193-203):
+// q [B, Hq, Tq, d], k/v [B, Hkv, Tk, d], Hkv | Hq.  Output: new contiguous [B, Hq, Tq, d].
+Result<RawTensor> attention_forward(const RawTensor& q, const RawTensor& k, const RawTensor& v,
+                                    bool is_causal, int64_t q_offset = 0,
+                                    std::optional<float> scale = std::nullopt);
+
+// src/nn/linear.rs:9-60: y = x W^T + b on the last axis (rocBLAS SGEMM).
+class Linear {
+  public:
+    Linear(size_t in_features, size_t out_features);     // bias, Kaiming-uniform weight
+    static Linear with_bias(size_t in_features, size_t out_features, bool has_bias);
+    static Linear without_bias(size_t in_features, size_t out_features);
+    Result<RawTensor> forward(const RawTensor& input) const;
+
+    RawTensor weight;                                    // [out_features, in_features]
+    std::optional<RawTensor> bias;                       // [out_features]
+    size_t in_features = 0, out_features = 0;
+
+  private:
+    Linear() = default;
+};
+
+// src/nn/flash_attention.rs:202-292 (forward only: the reference's output is a leaf, :273).
+class FlashAttention {
+  public:
+    // Throws std::invalid_argument unless num_heads divides d_model (the reference asserts).
+    FlashAttention(size_t d_model, size_t num_heads, bool is_causal);
+    // x [B, T, C] -> [B, T, C].  The projections are read as [B, H, T, d] views
+    // and the attention output is written straight into [B, T, H, d], so the
+    // reference's transpose/reshape copies (:259-275) disappear.
+    Result<RawTensor> forward_flash(const RawTensor& x) const;
+    Result<RawTensor> forward(const RawTensor& x) const { return forward_flash(x); }
+
+    Linear q_proj, k_proj, v_proj, out_proj;
+    size_t num_heads, d_model, head_dim;
+    bool is_causal;
+    size_t block_size = 64;
+};
+
+// src/nn/kv_cache.rs:11-74 on a device-resident, fixed-capacity layout:
+// per layer K and V [B, Hkv, capacity, d] and per-sequence lengths.
+class KVCache {
+  public:
+    KVCache(size_t num_layers, size_t batch, size_t num_kv_heads, size_t capacity, size_t head_dim);
+
+    void reset();                                        // kv_cache.rs:25-29
+    size_t num_layers() const;                           // kv_cache.rs:32-34
+    size_t current_seq_len(size_t layer_idx) const;      // kv_cache.rs:37-44 (longest sequence)
+
+    // kv_cache.rs:49-74: appends k_new / v_new [B, Hkv, t, d] to every sequence
+    // and returns views [B, Hkv, L, d] of the filled rows (L = longest sequence).
+    Result<std::pair<RawTensor, RawTensor>> update(size_t layer_idx, const RawTensor& k_new,
+                                                   const RawTensor& v_new);
+    // Single-token decode: q [B, Hq, 1, d] attends to the cached rows of its sequence.
+    Result<RawTensor> attend(size_t layer_idx, const RawTensor& q,
+                             std::optional<float> scale = std::nullopt);
+    // Append one row per sequence, then attend (llama.rs:239-296 with t = 1).
+    Result<RawTensor> decode_step(size_t layer_idx, const RawTensor& q, const RawTensor& k_new,
+                                  const RawTensor& v_new, std::optional<float> scale = std::nullopt);
+    // Declares rows [0, lens[b]) of each sequence filled (ragged batches).
+    Result<bool> set_lengths(size_t layer_idx, const std::vector<int32_t>& lens);
+
+    RawTensor k(size_t layer_idx) const;                 // full [B, Hkv, capacity, d]
+    RawTensor v(size_t layer_idx) const;
+    const std::vector<int32_t>& lengths(size_t layer_idx) const;
+
+    size_t batch, num_kv_heads, capacity, head_dim;
+
+  private:
+    Result<bool> check_layer(size_t layer_idx) const;
+    void* workspace(size_t num_heads);
+
+    struct Layer {
+        std::shared_ptr<float> k, v;
+        std::shared_ptr<int32_t> lens_dev;
+        std::vector<int32_t> lens_host;
+    };
+    std::vector<Layer> layers_;
+    std::shared_ptr<void> ws_;
+    uint64_t ws_bytes_ = 0;
+};
+
+}  // namespace nne

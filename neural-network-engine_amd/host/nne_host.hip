@@ -1,0 +1,580 @@
+// C++ host API of the attention path (declared in nne.hpp): tensors in device
+// memory, the reference's function / layer / cache API, and error mapping
+// from the C ABI's status codes onto EngineError.  Attention itself always
+// runs through include/nne_attn.h; the two small kernels here only gather a
+// strided tensor and add a bias row.
+#include <hip/hip_runtime.h>
+#include <rocblas/rocblas.h>
+
+#include <algorithm>
+#include <cmath>
+#include <cstring>
+#include <mutex>
+#include <random>
+#include <sstream>
+
+#include "nne.hpp"
+#include "nne_attn.h"
+
+namespace nne {
+
+namespace {
+
+constexpr int kMaxDims = 8;
+
+struct GatherArgs {
+    const float* src;
+    float* dst;
+    int64_t n;
+    int nd;
+    int64_t shape[kMaxDims];
+    int64_t stride[kMaxDims];
+};
+
+__global__ void gather_kernel(GatherArgs a) {
+    for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < a.n;
+         i += (int64_t)gridDim.x * blockDim.x) {
+        int64_t idx = i, off = 0;
+        for (int d = a.nd - 1; d >= 0; --d) {
+            const int64_t c = idx % a.shape[d];
+            idx /= a.shape[d];
+            off += c * a.stride[d];
+        }
+        a.dst[i] = a.src[off];
+    }
+}
+
+__global__ void bias_add_kernel(float* y, const float* bias, int64_t rows, int64_t cols) {
+    const int64_t n = rows * cols;
+    for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n;
+         i += (int64_t)gridDim.x * blockDim.x)
+        y[i] += bias[i % cols];
+}
+
+unsigned grid_for(int64_t n) {
+    int64_t blocks = (n + 255) / 256;
+    return (unsigned)std::max<int64_t>(1, std::min<int64_t>(blocks, 4096));
+}
+
+std::string dims(const std::vector<size_t>& v) {      // Rust {:?} of a Vec<usize>
+    std::ostringstream s;
+    s << "[";
+    for (size_t i = 0; i < v.size(); ++i) s << (i ? ", " : "") << v[i];
+    s << "]";
+    return s.str();
+}
+
+std::mutex g_rng_mu;
+std::mt19937_64 g_rng(0x5EED);
+
+std::vector<size_t> contiguous_strides(const std::vector<size_t>& shape) {
+    std::vector<size_t> st(shape.size());
+    size_t acc = 1;
+    for (size_t i = shape.size(); i-- > 0;) {
+        st[i] = acc;
+        acc *= shape[i];
+    }
+    return st;
+}
+
+size_t count(const std::vector<size_t>& shape) {
+    size_t n = 1;
+    for (size_t s : shape) n *= s;
+    return n;
+}
+
+// Strips the Display prefix the C ABI puts in front of its messages, so that
+// EngineError::to_string() does not repeat it.
+std::string payload(const char* msg, const char* prefix) {
+    std::string m = msg ? msg : "";
+    const size_t n = std::strlen(prefix);
+    return m.compare(0, n, prefix) == 0 ? m.substr(n) : m;
+}
+
+EngineError from_status(int rc) {
+    const char* msg = nne_last_error();
+    if (rc == NNE_EINVAL) return EngineError::invalid_argument(payload(msg, "Invalid configuration or argument: "));
+    return EngineError::gpu_error(payload(msg, "GPU compute error: "));
+}
+
+// Device allocation through the C ABI; zero bytes gives an empty pointer.
+template <class T>
+std::shared_ptr<T> device_alloc(size_t n) {
+    void* p = nullptr;
+    if (nne_dev_alloc(&p, (uint64_t)n * sizeof(T)) != NNE_OK)
+        throw std::runtime_error(from_status(NNE_EHIP).to_string());
+    return std::shared_ptr<T>(static_cast<T*>(p), [](T* q) { nne_dev_free(q); });
+}
+
+void hip_check(hipError_t e, const char* what) {
+    if (e != hipSuccess)
+        throw std::runtime_error(EngineError::gpu_error(std::string(what) + ": " + hipGetErrorString(e)).to_string());
+}
+
+std::vector<int64_t> as_i64(const std::vector<size_t>& v) { return std::vector<int64_t>(v.begin(), v.end()); }
+
+}  // namespace
+
+// ---- EngineError ------------------------------------------------------------
+
+EngineError EngineError::shape_mismatch(std::vector<size_t> expected, std::vector<size_t> actual) {
+    EngineError e;
+    e.kind = Kind::ShapeMismatch;
+    e.expected = std::move(expected);
+    e.actual = std::move(actual);
+    return e;
+}
+EngineError EngineError::incompatible_shapes(std::string op, std::vector<std::vector<size_t>> shapes) {
+    EngineError e;
+    e.kind = Kind::IncompatibleShapes;
+    e.op = std::move(op);
+    e.shapes = std::move(shapes);
+    return e;
+}
+EngineError EngineError::invalid_argument(std::string message) {
+    EngineError e;
+    e.kind = Kind::InvalidArgument;
+    e.message = std::move(message);
+    return e;
+}
+EngineError EngineError::gpu_error(std::string message) {
+    EngineError e;
+    e.kind = Kind::GpuError;
+    e.message = std::move(message);
+    return e;
+}
+EngineError EngineError::non_contiguous_tensor() {
+    EngineError e;
+    e.kind = Kind::NonContiguousTensor;
+    return e;
+}
+
+std::string EngineError::to_string() const {
+    switch (kind) {
+        case Kind::ShapeMismatch:
+            return "Shape mismatch error: expected shape " + dims(expected) + ", got " + dims(actual);
+        case Kind::IncompatibleShapes: {
+            std::string s = "Incompatible shapes for operation " + op + ": [";
+            for (size_t i = 0; i < shapes.size(); ++i) s += (i ? ", " : "") + dims(shapes[i]);
+            return s + "]";
+        }
+        case Kind::InvalidArgument: return "Invalid configuration or argument: " + message;
+        case Kind::GpuError: return "GPU compute error: " + message;
+        case Kind::NonContiguousTensor: return "Tensor is not contiguous in memory";
+    }
+    return "";
+}
+
+bool EngineError::operator==(const EngineError& o) const {
+    return kind == o.kind && expected == o.expected && actual == o.actual && op == o.op &&
+           shapes == o.shapes && message == o.message;
+}
+
+// ---- RawTensor ---------------------------------------------------------------
+
+void manual_seed(uint64_t seed) {
+    std::lock_guard<std::mutex> lock(g_rng_mu);
+    g_rng.seed(seed);
+}
+
+RawTensor RawTensor::view(std::shared_ptr<float> owner, size_t offset, std::vector<size_t> shape,
+                          std::vector<size_t> strides) {
+    RawTensor t;
+    t.storage_ = std::move(owner);
+    t.offset_ = offset;
+    t.shape_ = std::move(shape);
+    t.strides_ = std::move(strides);
+    return t;
+}
+
+RawTensor RawTensor::from_vec(const std::vector<float>& data, std::vector<size_t> shape) {
+    const size_t n = count(shape);
+    if (data.size() != n)
+        throw std::invalid_argument("Data length " + std::to_string(data.size()) + " does not match shape " +
+                                    dims(shape) + " (expected " + std::to_string(n) + ")");
+    auto buf = device_alloc<float>(n);
+    if (n && nne_memcpy_h2d(buf.get(), data.data(), n * 4, nullptr) != NNE_OK)
+        throw std::runtime_error(from_status(NNE_EHIP).to_string());
+    auto st = contiguous_strides(shape);
+    return view(std::move(buf), 0, std::move(shape), std::move(st));
+}
+
+RawTensor RawTensor::zeros(const std::vector<size_t>& shape) {
+    const size_t n = count(shape);
+    auto buf = device_alloc<float>(n);
+    if (n) hip_check(hipMemset(buf.get(), 0, n * 4), "hipMemset");
+    return view(std::move(buf), 0, shape, contiguous_strides(shape));
+}
+
+RawTensor RawTensor::randn(const std::vector<size_t>& shape, float mean, float std) {
+    std::vector<float> data(count(shape));
+    {
+        std::lock_guard<std::mutex> lock(g_rng_mu);
+        std::normal_distribution<float> dist(mean, std);
+        for (float& x : data) x = dist(g_rng);
+    }
+    return from_vec(data, shape);
+}
+
+RawTensor RawTensor::uniform(const std::vector<size_t>& shape, float low, float high) {
+    std::vector<float> data(count(shape));
+    {
+        std::lock_guard<std::mutex> lock(g_rng_mu);
+        std::uniform_real_distribution<float> dist(low, high);
+        for (float& x : data) x = dist(g_rng);
+    }
+    return from_vec(data, shape);
+}
+
+RawTensor RawTensor::kaiming_uniform(const std::vector<size_t>& shape, size_t fan_in) {
+    const float bound = std::sqrt(6.0f / (float)std::max<size_t>(fan_in, 1));   // tensor/mod.rs:128-131
+    return uniform(shape, -bound, bound);
+}
+
+size_t RawTensor::numel() const { return count(shape_); }
+
+bool RawTensor::is_contiguous() const { return strides_ == contiguous_strides(shape_); }
+
+float* RawTensor::data() const { return storage_ ? storage_.get() + offset_ : nullptr; }
+
+RawTensor RawTensor::to_contiguous() const {
+    if (is_contiguous() || numel() == 0) return *this;
+    if (ndim() > (size_t)kMaxDims) throw std::invalid_argument("to_contiguous: more than 8 dimensions");
+    auto buf = device_alloc<float>(numel());
+    GatherArgs a{};
+    a.src = data();
+    a.dst = buf.get();
+    a.n = (int64_t)numel();
+    a.nd = (int)ndim();
+    for (size_t i = 0; i < ndim(); ++i) {
+        a.shape[i] = (int64_t)shape_[i];
+        a.stride[i] = (int64_t)strides_[i];
+    }
+    hipLaunchKernelGGL(gather_kernel, dim3(grid_for(a.n)), dim3(256), 0, nullptr, a);
+    hip_check(hipGetLastError(), "gather_kernel");
+    return view(std::move(buf), 0, shape_, contiguous_strides(shape_));
+}
+
+std::vector<float> RawTensor::to_vec() const {
+    RawTensor c = to_contiguous();
+    std::vector<float> out(c.numel());
+    if (!out.empty() && nne_memcpy_d2h(out.data(), c.data(), out.size() * 4, nullptr) != NNE_OK)
+        throw std::runtime_error(from_status(NNE_EHIP).to_string());
+    return out;
+}
+
+Result<RawTensor> RawTensor::transpose(size_t a, size_t b) const {
+    if (a >= ndim() || b >= ndim())
+        return EngineError::invalid_argument("transpose axes (" + std::to_string(a) + ", " +
+                                             std::to_string(b) + ") out of range for " + dims(shape_));
+    RawTensor t = *this;
+    std::swap(t.shape_[a], t.shape_[b]);
+    std::swap(t.strides_[a], t.strides_[b]);
+    return t;
+}
+
+Result<RawTensor> RawTensor::reshape(const std::vector<size_t>& shape) const {
+    if (count(shape) != numel())
+        return EngineError::shape_mismatch(shape, shape_);
+    RawTensor c = to_contiguous();
+    return view(c.storage_, c.offset_, shape, contiguous_strides(shape));
+}
+
+Result<RawTensor> RawTensor::slice(size_t axis, size_t start, size_t end) const {
+    if (axis >= ndim() || start > end || end > shape_[axis])
+        return EngineError::invalid_argument("slice [" + std::to_string(start) + ", " + std::to_string(end) +
+                                             ") of axis " + std::to_string(axis) + " out of range for " +
+                                             dims(shape_));
+    RawTensor t = *this;
+    t.offset_ += start * strides_[axis];
+    t.shape_[axis] = end - start;
+    return t;
+}
+
+// ---- attention -----------------------------------------------------------
+
+Result<RawTensor> flash_attention_forward(const RawTensor& q, const RawTensor& k, const RawTensor& v,
+                                          bool is_causal, std::optional<float> scale,
+                                          size_t block_size_r, size_t block_size_c) {
+    if (q.ndim() != 4 || k.ndim() != 4 || v.ndim() != 4)          // flash_attention.rs:32-37
+        return EngineError::invalid_argument(
+            "FlashAttention expects 4D tensors [Batch, Heads, SeqLen, Dim], got Q:" + dims(q.shape()) +
+            ", K:" + dims(k.shape()) + ", V:" + dims(v.shape()));
+    const auto &qs = q.shape(), &ks = k.shape(), &vs = v.shape();
+    if (qs[0] != ks[0] || qs[0] != vs[0] || qs[1] != ks[1] || qs[1] != vs[1] || qs[3] != ks[3] ||
+        qs[3] != vs[3] || ks[2] != vs[2])                         // flash_attention.rs:43-48
+        return EngineError::shape_mismatch({qs[0], qs[1], ks[2], qs[3]}, {ks[0], ks[1], ks[2], ks[3]});
+    RawTensor out = RawTensor::zeros(qs);
+    const auto q_shape = as_i64(qs), k_shape = as_i64(ks), v_shape = as_i64(vs);
+    const auto q_st = as_i64(q.strides()), k_st = as_i64(k.strides()), v_st = as_i64(v.strides());
+    const auto o_st = as_i64(out.strides());
+    const int rc = nne_flash_attention_forward(
+        q.data(), q_shape.data(), q_st.data(), k.data(), k_shape.data(), k_st.data(), v.data(),
+        v_shape.data(), v_st.data(), out.data(), o_st.data(), is_causal ? 1 : 0, scale ? 1 : 0,
+        scale.value_or(0.f), (int64_t)block_size_r, (int64_t)block_size_c, nullptr);
+    if (rc != NNE_OK) return from_status(rc);
+    return out;
+}
+
+Result<RawTensor> attention_forward(const RawTensor& q, const RawTensor& k, const RawTensor& v,
+                                    bool is_causal, int64_t q_offset, std::optional<float> scale) {
+    if (q.ndim() != 4 || k.ndim() != 4 || v.ndim() != 4)
+        return EngineError::invalid_argument("attention expects 4D tensors [Batch, Heads, SeqLen, Dim], got Q:" +
+                                             dims(q.shape()) + ", K:" + dims(k.shape()) + ", V:" +
+                                             dims(v.shape()));
+    const auto &qs = q.shape(), &ks = k.shape(), &vs = v.shape();
+    const size_t hkv = ks[1];
+    if (qs[0] != ks[0] || qs[0] != vs[0] || hkv != vs[1] || qs[3] != ks[3] || qs[3] != vs[3] ||
+        ks[2] != vs[2] || hkv == 0 || qs[1] % hkv != 0)
+        return EngineError::shape_mismatch({qs[0], hkv > 0 && qs[1] % hkv == 0 ? hkv : qs[1], ks[2], qs[3]},
+                                           {ks[0], hkv, ks[2], ks[3]});
+    RawTensor out = RawTensor::zeros(qs);
+    const auto q_shape = as_i64(qs), k_shape = as_i64(ks), v_shape = as_i64(vs);
+    const auto q_st = as_i64(q.strides()), k_st = as_i64(k.strides()), v_st = as_i64(v.strides());
+    const auto o_st = as_i64(out.strides());
+    const int rc = nne_attention_forward(q.data(), q_shape.data(), q_st.data(), k.data(), k_shape.data(),
+                                         k_st.data(), v.data(), v_shape.data(), v_st.data(), out.data(),
+                                         o_st.data(), is_causal ? 1 : 0, q_offset, scale ? 1 : 0,
+                                         scale.value_or(0.f), nullptr);
+    if (rc != NNE_OK) return from_status(rc);
+    return out;
+}
+
+// ---- Linear ------------------------------------------------------------------
+
+namespace {
+
+rocblas_handle blas() {
+    thread_local rocblas_handle h = nullptr;
+    if (!h && rocblas_create_handle(&h) != rocblas_status_success)
+        throw std::runtime_error(EngineError::gpu_error("rocblas_create_handle failed").to_string());
+    return h;
+}
+
+}  // namespace
+
+Linear::Linear(size_t in, size_t out) { *this = with_bias(in, out, true); }
+
+Linear Linear::with_bias(size_t in, size_t out, bool has_bias) {   // linear.rs:28-42
+    Linear l;
+    l.in_features = in;
+    l.out_features = out;
+    l.weight = RawTensor::kaiming_uniform({out, in}, in);
+    if (has_bias) {
+        const float bound = 1.0f / std::sqrt((float)in);
+        l.bias = RawTensor::uniform({out}, -bound, bound);
+    }
+    return l;
+}
+
+Linear Linear::without_bias(size_t in, size_t out) { return with_bias(in, out, false); }
+
+Result<RawTensor> Linear::forward(const RawTensor& input) const {   // linear.rs:45-56
+    if (input.ndim() == 0 || input.shape().back() != in_features)
+        return EngineError::incompatible_shapes("matmul_transposed_b", {input.shape(), weight.shape()});
+    RawTensor x = input.to_contiguous();
+    const size_t rows = x.numel() / std::max<size_t>(in_features, 1);
+    std::vector<size_t> out_shape = x.shape();
+    out_shape.back() = out_features;
+    RawTensor y = RawTensor::zeros(out_shape);
+    if (rows && out_features) {
+        // Row-major Y[rows, out] = X[rows, in] W^T is column-major
+        // Y^T[out, rows] = W[out, in] (stored as W^T, transposed) x X^T[in, rows].
+        const float one = 1.f, zero = 0.f;
+        if (rocblas_sgemm(blas(), rocblas_operation_transpose, rocblas_operation_none, (rocblas_int)out_features,
+                          (rocblas_int)rows, (rocblas_int)in_features, &one, weight.data(),
+                          (rocblas_int)in_features, x.data(), (rocblas_int)in_features, &zero, y.data(),
+                          (rocblas_int)out_features) != rocblas_status_success)
+            return EngineError::gpu_error("rocblas_sgemm failed");
+        if (bias) {
+            hipLaunchKernelGGL(bias_add_kernel, dim3(grid_for((int64_t)(rows * out_features))), dim3(256), 0,
+                               nullptr, y.data(), bias->data(), (int64_t)rows, (int64_t)out_features);
+            if (hipGetLastError() != hipSuccess) return EngineError::gpu_error("bias_add_kernel launch failed");
+        }
+    }
+    return y;
+}
+
+// ---- FlashAttention layer ----------------------------------------------------
+
+namespace {
+
+// flash_attention.rs:217-223, checked before any projection is allocated.
+size_t divisible_d_model(size_t d_model, size_t num_heads) {
+    if (num_heads == 0 || d_model % num_heads != 0)
+        throw std::invalid_argument("d_model (" + std::to_string(d_model) + ") must be divisible by num_heads (" +
+                                    std::to_string(num_heads) + ")");
+    return d_model;
+}
+
+}  // namespace
+
+FlashAttention::FlashAttention(size_t d_model_, size_t num_heads_, bool is_causal_)
+    : q_proj(divisible_d_model(d_model_, num_heads_), d_model_), k_proj(d_model_, d_model_),
+      v_proj(d_model_, d_model_), out_proj(d_model_, d_model_), num_heads(num_heads_), d_model(d_model_),
+      head_dim(d_model_ / num_heads_), is_causal(is_causal_) {}
+
+Result<RawTensor> FlashAttention::forward_flash(const RawTensor& x) const {
+    if (x.ndim() != 3)                                               // flash_attention.rs:240-246
+        return EngineError::incompatible_shapes("FlashAttention forward (expected 3D input [B, T, C])", {x.shape()});
+    const size_t b = x.shape()[0], t = x.shape()[1], h = num_heads, d = head_dim;
+    auto q = q_proj.forward(x);
+    if (q.is_err()) return q.error();
+    auto k = k_proj.forward(x);
+    if (k.is_err()) return k.error();
+    auto v = v_proj.forward(x);
+    if (v.is_err()) return v.error();
+    // [B, T, C] read as [B, H, T, d]: strides (T*C, d, C, 1); the output is written
+    // the same way, i.e. directly in [B, T, C].
+    const std::vector<size_t> hs{b, h, t, d}, st{t * d_model, d, d_model, 1};
+    RawTensor merged = RawTensor::zeros({b, t, d_model});
+    const auto shape = as_i64(hs), strides = as_i64(st);
+    const int rc = nne_flash_attention_forward(
+        q.value().data(), shape.data(), strides.data(), k.value().data(), shape.data(), strides.data(),
+        v.value().data(), shape.data(), strides.data(), merged.data(), strides.data(), is_causal ? 1 : 0, 0, 0.f,
+        (int64_t)block_size, (int64_t)block_size, nullptr);
+    if (rc != NNE_OK) return from_status(rc);
+    return out_proj.forward(merged);
+}
+
+// ---- KVCache -----------------------------------------------------------------
+
+KVCache::KVCache(size_t num_layers, size_t batch_, size_t num_kv_heads_, size_t capacity_, size_t head_dim_)
+    : batch(batch_), num_kv_heads(num_kv_heads_), capacity(capacity_), head_dim(head_dim_) {
+    const size_t n = batch * num_kv_heads * capacity * head_dim;
+    for (size_t i = 0; i < num_layers; ++i) {
+        Layer l;
+        l.k = device_alloc<float>(n);
+        l.v = device_alloc<float>(n);
+        l.lens_dev = device_alloc<int32_t>(batch);
+        if (n) {
+            hip_check(hipMemset(l.k.get(), 0, n * 4), "hipMemset");
+            hip_check(hipMemset(l.v.get(), 0, n * 4), "hipMemset");
+        }
+        if (batch) hip_check(hipMemset(l.lens_dev.get(), 0, batch * 4), "hipMemset");
+        l.lens_host.assign(batch, 0);
+        layers_.push_back(std::move(l));
+    }
+}
+
+void KVCache::reset() {
+    for (auto& l : layers_) {
+        std::fill(l.lens_host.begin(), l.lens_host.end(), 0);
+        if (batch) hip_check(hipMemset(l.lens_dev.get(), 0, batch * 4), "hipMemset");
+    }
+}
+
+size_t KVCache::num_layers() const { return layers_.size(); }
+
+size_t KVCache::current_seq_len(size_t layer_idx) const {
+    if (layer_idx >= layers_.size() || batch == 0) return 0;
+    const auto& l = layers_[layer_idx].lens_host;
+    return (size_t)*std::max_element(l.begin(), l.end());
+}
+
+Result<bool> KVCache::check_layer(size_t layer_idx) const {
+    if (layer_idx >= layers_.size())                                 // kv_cache.rs:55-61
+        return EngineError::invalid_argument("KVCache layer index " + std::to_string(layer_idx) +
+                                             " out of range (total layers: " + std::to_string(layers_.size()) +
+                                             ")");
+    return true;
+}
+
+RawTensor KVCache::k(size_t layer_idx) const {
+    const std::vector<size_t> s{batch, num_kv_heads, capacity, head_dim};
+    return RawTensor::view(layers_.at(layer_idx).k, 0, s, contiguous_strides(s));
+}
+
+RawTensor KVCache::v(size_t layer_idx) const {
+    const std::vector<size_t> s{batch, num_kv_heads, capacity, head_dim};
+    return RawTensor::view(layers_.at(layer_idx).v, 0, s, contiguous_strides(s));
+}
+
+const std::vector<int32_t>& KVCache::lengths(size_t layer_idx) const { return layers_.at(layer_idx).lens_host; }
+
+Result<std::pair<RawTensor, RawTensor>> KVCache::update(size_t layer_idx, const RawTensor& k_new,
+                                                       const RawTensor& v_new) {
+    auto ok = check_layer(layer_idx);
+    if (ok.is_err()) return ok.error();
+    const std::vector<size_t> want{batch, num_kv_heads, k_new.ndim() == 4 ? k_new.shape()[2] : 0, head_dim};
+    if (k_new.shape() != want) return EngineError::shape_mismatch(want, k_new.shape());
+    if (v_new.shape() != want) return EngineError::shape_mismatch(want, v_new.shape());
+    Layer& l = layers_[layer_idx];
+    const auto kst = as_i64(k_new.strides()), vst = as_i64(v_new.strides());
+    const int rc = nne_kv_append(l.k.get(), l.v.get(), l.lens_dev.get(), l.lens_host.data(), k_new.data(), kst.data(),
+                                 v_new.data(), vst.data(), (int64_t)batch, (int64_t)num_kv_heads,
+                                 (int64_t)capacity, (int64_t)head_dim, (int64_t)want[2], nullptr);
+    if (rc != NNE_OK) return from_status(rc);
+    const size_t L = current_seq_len(layer_idx);
+    auto kv = k(layer_idx).slice(2, 0, L), vv = v(layer_idx).slice(2, 0, L);
+    return std::make_pair(kv.value(), vv.value());
+}
+
+void* KVCache::workspace(size_t num_heads) {
+    const uint64_t need = nne_decode_workspace_bytes((int64_t)batch, (int64_t)num_heads, (int64_t)num_kv_heads,
+                                                     (int64_t)head_dim, (int64_t)capacity);
+    if (need > ws_bytes_) {
+        auto buf = device_alloc<char>(need);
+        ws_ = std::shared_ptr<void>(buf, buf.get());
+        ws_bytes_ = need;
+    }
+    return ws_.get();
+}
+
+Result<RawTensor> KVCache::attend(size_t layer_idx, const RawTensor& q, std::optional<float> scale) {
+    auto ok = check_layer(layer_idx);
+    if (ok.is_err()) return ok.error();
+    if (q.ndim() != 4 || q.shape()[0] != batch || q.shape()[2] != 1 || q.shape()[3] != head_dim)
+        return EngineError::shape_mismatch({batch, q.ndim() == 4 ? q.shape()[1] : 0, 1, head_dim}, q.shape());
+    Layer& l = layers_[layer_idx];
+    RawTensor out = RawTensor::zeros(q.shape());
+    const auto qst = as_i64(q.strides()), ost = as_i64(out.strides());
+    void* ws = workspace(q.shape()[1]);
+    const int rc = nne_decode_attention(q.data(), qst.data(), l.k.get(), l.v.get(), l.lens_dev.get(),
+                                        l.lens_host.data(), out.data(), ost.data(), (int64_t)batch,
+                                        (int64_t)q.shape()[1], (int64_t)num_kv_heads, (int64_t)capacity,
+                                        (int64_t)head_dim, scale ? 1 : 0, scale.value_or(0.f), ws, ws_bytes_,
+                                        nullptr);
+    if (rc != NNE_OK) return from_status(rc);
+    return out;
+}
+
+Result<RawTensor> KVCache::decode_step(size_t layer_idx, const RawTensor& q, const RawTensor& k_new,
+                                       const RawTensor& v_new, std::optional<float> scale) {
+    auto ok = check_layer(layer_idx);
+    if (ok.is_err()) return ok.error();
+    if (q.ndim() != 4 || q.shape()[0] != batch || q.shape()[2] != 1 || q.shape()[3] != head_dim)
+        return EngineError::shape_mismatch({batch, q.ndim() == 4 ? q.shape()[1] : 0, 1, head_dim}, q.shape());
+    const std::vector<size_t> want{batch, num_kv_heads, 1, head_dim};
+    if (k_new.shape() != want) return EngineError::shape_mismatch(want, k_new.shape());
+    if (v_new.shape() != want) return EngineError::shape_mismatch(want, v_new.shape());
+    Layer& l = layers_[layer_idx];
+    RawTensor out = RawTensor::zeros(q.shape());
+    const auto qst = as_i64(q.strides()), ost = as_i64(out.strides());
+    const auto kst = as_i64(k_new.strides()), vst = as_i64(v_new.strides());
+    void* ws = workspace(q.shape()[1]);
+    const int rc = nne_decode_step(q.data(), qst.data(), l.k.get(), l.v.get(), l.lens_dev.get(),
+                                   l.lens_host.data(), k_new.data(), kst.data(), v_new.data(), vst.data(),
+                                   out.data(), ost.data(), (int64_t)batch, (int64_t)q.shape()[1],
+                                   (int64_t)num_kv_heads, (int64_t)capacity, (int64_t)head_dim, scale ? 1 : 0,
+                                   scale.value_or(0.f), ws, ws_bytes_, nullptr);
+    if (rc != NNE_OK) return from_status(rc);
+    return out;
+}
+
+Result<bool> KVCache::set_lengths(size_t layer_idx, const std::vector<int32_t>& lens) {
+    auto ok = check_layer(layer_idx);
+    if (ok.is_err()) return ok.error();
+    if (lens.size() != batch) return EngineError::shape_mismatch({batch}, {lens.size()});
+    for (int32_t L : lens)
+        if (L < 0 || (size_t)L > capacity)
+            return EngineError::invalid_argument("sequence length " + std::to_string(L) + " outside [0, " +
+                                                 std::to_string(capacity) + "]");
+    Layer& l = layers_[layer_idx];
+    l.lens_host = lens;
+    if (batch && nne_memcpy_h2d(l.lens_dev.get(), lens.data(), batch * 4, nullptr) != NNE_OK)
+        return from_status(NNE_EHIP);
+    return true;
+}
+
+}  // namespace nne

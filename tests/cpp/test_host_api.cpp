@@ -1,0 +1,321 @@
+// Tests of the C++ host API (neural-network-engine_amd/host/nne.hpp), written
+// after the reference's own tests of this path:
+//   tests/nn/flash_attention_tests.rs  (parity with standard attention by cosine
+//                                       similarity > 0.9999, shapes, the layer)
+//   tests/nn/kv_cache_tests.rs         (cache bookkeeping; cached decode equals
+//                                       the full-sequence result within 1e-4)
+// plus this build's element-wise bar |gpu - ref| <= 1e-4 + 1e-3 |ref| against the
+// CPU oracle (oracle/oracle.c, test infrastructure) and the error variants of
+// src/error.rs that the path returns.
+//
+//   test_host_api            run every test (needs a GPU)
+//   test_host_api --cpu      run only the tests that touch no device
+// Prints "ok <name>" / "FAIL <name>: <why>" per test; exit status = failures.
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+#include <functional>
+#include <stdexcept>
+#include <string>
+#include <vector>
+
+#include "nne.hpp"
+
+extern "C" {
+void oracle_flash_forward(const float* q, const float* k, const float* v, float* out, int64_t b, int64_t h,
+                          int64_t tq, int64_t tk, int64_t d, int is_causal, int has_scale, float scale,
+                          int64_t block_r, int64_t block_c, int n_threads);
+void oracle_standard_attention(const float* q, const float* k, const float* v, float* out, int64_t b,
+                               int64_t hq, int64_t hkv, int64_t tq, int64_t tk, int64_t d, int masked,
+                               int64_t start_pos, int has_scale, float scale, int n_threads);
+}
+
+using namespace nne;
+
+namespace {
+
+struct Failure : std::runtime_error {
+    using std::runtime_error::runtime_error;
+};
+
+#define CHECK(cond)                                                                          \
+    do {                                                                                     \
+        if (!(cond)) throw Failure(std::string(#cond) + " (line " + std::to_string(__LINE__) + ")"); \
+    } while (0)
+
+struct Test {
+    const char* name;
+    bool needs_gpu;
+    std::function<void()> fn;
+};
+std::vector<Test>& registry() {
+    static std::vector<Test> r;
+    return r;
+}
+struct Register {
+    Register(const char* n, bool gpu, std::function<void()> f) { registry().push_back({n, gpu, std::move(f)}); }
+};
+#define TEST_GPU(name) static void name(); static Register reg_##name(#name, true, name); static void name()
+#define TEST_CPU(name) static void name(); static Register reg_##name(#name, false, name); static void name()
+
+// Element-wise bar of this build and the reference's cosine-similarity bar.
+void check_close(const std::vector<float>& got, const std::vector<float>& ref, const char* what) {
+    CHECK(got.size() == ref.size());
+    double dot = 0, ng = 0, nr = 0;
+    for (size_t i = 0; i < got.size(); ++i) {
+        const double tol = 1e-4 + 1e-3 * std::fabs(ref[i]);
+        if (!(std::fabs((double)got[i] - ref[i]) <= tol))
+            throw Failure(std::string(what) + ": element " + std::to_string(i) + " got " + std::to_string(got[i]) +
+                          " want " + std::to_string(ref[i]));
+        dot += (double)got[i] * ref[i];
+        ng += (double)got[i] * got[i];
+        nr += (double)ref[i] * ref[i];
+    }
+    if (ng > 0 || nr > 0) CHECK(dot / std::sqrt(ng * nr) > 0.9999);
+}
+
+std::vector<float> standard_attention(const RawTensor& q, const RawTensor& k, const RawTensor& v, bool causal,
+                                      int64_t start_pos = 0) {
+    const auto qs = q.shape(), ks = k.shape();
+    std::vector<float> out(q.numel());
+    const auto qh = q.to_vec(), kh = k.to_vec(), vh = v.to_vec();
+    oracle_standard_attention(qh.data(), kh.data(), vh.data(), out.data(), qs[0], qs[1], ks[1], qs[2], ks[2], qs[3],
+                              causal ? 1 : 0, start_pos, 0, 0.f, 8);
+    return out;
+}
+
+// x [rows, in] W^T + b on the host, for the layer check.
+std::vector<float> host_linear(const std::vector<float>& x, size_t rows, const Linear& l) {
+    const auto w = l.weight.to_vec();
+    const auto b = l.bias ? l.bias->to_vec() : std::vector<float>(l.out_features, 0.f);
+    std::vector<float> y(rows * l.out_features);
+    for (size_t r = 0; r < rows; ++r)
+        for (size_t o = 0; o < l.out_features; ++o) {
+            double acc = b[o];
+            for (size_t i = 0; i < l.in_features; ++i) acc += (double)x[r * l.in_features + i] * w[o * l.in_features + i];
+            y[r * l.out_features + o] = (float)acc;
+        }
+    return y;
+}
+
+// ---- flash_attention_tests.rs ----------------------------------------------
+
+TEST_GPU(test_flash_attention_parity_with_standard_attention_causal) {   // :4-59
+    const size_t b = 2, h = 4, t = 16, d = 32;
+    manual_seed(1);
+    RawTensor q = RawTensor::randn({b, h, t, d}, 0.f, 1.f);
+    RawTensor k = RawTensor::randn({b, h, t, d}, 0.f, 1.f);
+    RawTensor v = RawTensor::randn({b, h, t, d}, 0.f, 1.f);
+    RawTensor flash_out = flash_attention_forward(q, k, v, true, std::nullopt, 8, 8).unwrap();
+    CHECK(flash_out.shape() == (std::vector<size_t>{b, h, t, d}));
+    check_close(flash_out.to_vec(), standard_attention(q, k, v, true), "causal flash vs standard");
+}
+
+TEST_GPU(test_flash_attention_non_causal) {                              // :61-74
+    const size_t b = 1, h = 2, t = 32, d = 16;
+    manual_seed(2);
+    RawTensor q = RawTensor::randn({b, h, t, d}, 0.f, 1.f);
+    RawTensor k = RawTensor::randn({b, h, t, d}, 0.f, 1.f);
+    RawTensor v = RawTensor::randn({b, h, t, d}, 0.f, 1.f);
+    RawTensor out = flash_attention_forward(q, k, v, false, std::nullopt, 16, 16).unwrap();
+    CHECK(out.shape() == (std::vector<size_t>{b, h, t, d}));
+    std::vector<float> ref(out.numel());
+    const auto qh = q.to_vec(), kh = k.to_vec(), vh = v.to_vec();
+    oracle_flash_forward(qh.data(), kh.data(), vh.data(), ref.data(), b, h, t, t, d, 0, 0, 0.f, 16, 16, 4);
+    check_close(out.to_vec(), ref, "non-causal flash vs oracle flash");
+}
+
+TEST_GPU(test_flash_attention_strided_views_and_scale) {
+    // [B, T, H, d] projections read in place as [B, H, T, d] views; explicit scale.
+    manual_seed(3);
+    RawTensor base = RawTensor::randn({2, 40, 3, 64}, 0.f, 1.f);
+    RawTensor q = base.transpose(1, 2).unwrap();
+    RawTensor k = RawTensor::randn({2, 40, 3, 64}, 0.f, 1.f).transpose(1, 2).unwrap();
+    RawTensor v = RawTensor::randn({2, 40, 3, 64}, 0.f, 1.f).transpose(1, 2).unwrap();
+    CHECK(!q.is_contiguous());
+    RawTensor out = flash_attention_forward(q, k, v, true, 0.3f, 64, 64).unwrap();
+    std::vector<float> ref(out.numel());
+    const auto qh = q.to_vec(), kh = k.to_vec(), vh = v.to_vec();
+    oracle_flash_forward(qh.data(), kh.data(), vh.data(), ref.data(), 2, 3, 40, 40, 64, 1, 1, 0.3f, 64, 64, 4);
+    check_close(out.to_vec(), ref, "strided views, scale 0.3");
+}
+
+TEST_GPU(test_flash_attention_layer_forward) {                           // :76-83
+    manual_seed(4);
+    FlashAttention layer(64, 4, true);
+    RawTensor x = RawTensor::randn({2, 16, 64}, 0.f, 1.f);
+    RawTensor out = layer.forward(x).unwrap();
+    CHECK(out.shape() == (std::vector<size_t>{2, 16, 64}));
+    // The same composition on the host: projections, per-head oracle, out_proj.
+    const size_t b = 2, t = 16, c = 64, h = 4, d = 16;
+    const auto xh = x.to_vec();
+    const auto qp = host_linear(xh, b * t, layer.q_proj), kp = host_linear(xh, b * t, layer.k_proj),
+               vp = host_linear(xh, b * t, layer.v_proj);
+    auto heads = [&](const std::vector<float>& p) {       // [B, T, H, d] -> [B, H, T, d]
+        std::vector<float> r(p.size());
+        for (size_t bi = 0; bi < b; ++bi)
+            for (size_t ti = 0; ti < t; ++ti)
+                for (size_t hi = 0; hi < h; ++hi)
+                    for (size_t di = 0; di < d; ++di)
+                        r[((bi * h + hi) * t + ti) * d + di] = p[(bi * t + ti) * c + hi * d + di];
+        return r;
+    };
+    const auto q4 = heads(qp), k4 = heads(kp), v4 = heads(vp);
+    std::vector<float> o4(q4.size()), merged(q4.size());
+    oracle_flash_forward(q4.data(), k4.data(), v4.data(), o4.data(), b, h, t, t, d, 1, 0, 0.f, 64, 64, 4);
+    for (size_t bi = 0; bi < b; ++bi)
+        for (size_t hi = 0; hi < h; ++hi)
+            for (size_t ti = 0; ti < t; ++ti)
+                for (size_t di = 0; di < d; ++di)
+                    merged[(bi * t + ti) * c + hi * d + di] = o4[((bi * h + hi) * t + ti) * d + di];
+    check_close(out.to_vec(), host_linear(merged, b * t, layer.out_proj), "layer vs host composition");
+}
+
+// ---- kv_cache_tests.rs -------------------------------------------------------
+
+TEST_GPU(test_kv_cache_basic_operations) {                               // :4-27
+    KVCache cache(4, 2, 4, 16, 16);
+    CHECK(cache.num_layers() == 4);
+    CHECK(cache.current_seq_len(0) == 0);
+    manual_seed(5);
+    RawTensor k1 = RawTensor::randn({2, 4, 3, 16}, 0.f, 1.f);   // [B=2, H=4, T=3, D=16]
+    RawTensor v1 = RawTensor::randn({2, 4, 3, 16}, 0.f, 1.f);
+    auto [k_all, v_all] = cache.update(0, k1, v1).unwrap();
+    CHECK(k_all.shape() == (std::vector<size_t>{2, 4, 3, 16}));
+    CHECK(v_all.shape() == (std::vector<size_t>{2, 4, 3, 16}));
+    CHECK(cache.current_seq_len(0) == 3);
+    RawTensor k2 = RawTensor::randn({2, 4, 1, 16}, 0.f, 1.f);
+    RawTensor v2 = RawTensor::randn({2, 4, 1, 16}, 0.f, 1.f);
+    auto [k_all2, v_all2] = cache.update(0, k2, v2).unwrap();
+    CHECK(k_all2.shape() == (std::vector<size_t>{2, 4, 4, 16}));
+    CHECK(v_all2.shape() == (std::vector<size_t>{2, 4, 4, 16}));
+    CHECK(cache.current_seq_len(0) == 4);
+    // In-place append == concatenation along axis 2, bit for bit.
+    const auto a = k_all2.to_vec(), p1 = k1.to_vec(), p2 = k2.to_vec();
+    for (size_t bh = 0; bh < 8; ++bh)
+        for (size_t r = 0; r < 4; ++r)
+            for (size_t dd = 0; dd < 16; ++dd) {
+                const float want = r < 3 ? p1[(bh * 3 + r) * 16 + dd] : p2[bh * 16 + dd];
+                CHECK(a[(bh * 4 + r) * 16 + dd] == want);
+            }
+    cache.reset();
+    CHECK(cache.current_seq_len(0) == 0);
+}
+
+TEST_GPU(test_gqa_cached_parity) {                                       // :65-103 pattern
+    // Step-by-step decode through the cache equals the causal full-sequence result.
+    const size_t b = 1, hq = 8, hkv = 2, t = 6, d = 32;
+    manual_seed(6);
+    RawTensor q = RawTensor::randn({b, hq, t, d}, 0.f, 1.f);
+    RawTensor k = RawTensor::randn({b, hkv, t, d}, 0.f, 1.f);
+    RawTensor v = RawTensor::randn({b, hkv, t, d}, 0.f, 1.f);
+    const auto full = attention_forward(q, k, v, true).unwrap().to_vec();
+    KVCache cache(1, b, hkv, 32, d);
+    for (size_t s = 0; s < t; ++s) {
+        RawTensor qs = q.slice(2, s, s + 1).unwrap(), ks = k.slice(2, s, s + 1).unwrap(),
+                  vs = v.slice(2, s, s + 1).unwrap();
+        const auto step = cache.decode_step(0, qs, ks, vs).unwrap().to_vec();
+        for (size_t h = 0; h < hq; ++h)
+            for (size_t dd = 0; dd < d; ++dd) {
+                const float a = full[(h * t + s) * d + dd], c = step[h * d + dd];
+                if (!(std::fabs(a - c) < 1e-4f))
+                    throw Failure("GQA cached parity mismatch at step " + std::to_string(s) + ": " +
+                                  std::to_string(a) + " vs " + std::to_string(c));
+            }
+    }
+    CHECK(cache.current_seq_len(0) == t);
+}
+
+TEST_GPU(test_gqa_attention_matches_standard) {
+    manual_seed(7);
+    RawTensor q = RawTensor::randn({2, 12, 50, 64}, 0.f, 1.f);
+    RawTensor k = RawTensor::randn({2, 3, 70, 64}, 0.f, 1.f);
+    RawTensor v = RawTensor::randn({2, 3, 70, 64}, 0.f, 1.f);
+    check_close(attention_forward(q, k, v, true, 20).unwrap().to_vec(), standard_attention(q, k, v, true, 20),
+                "GQA causal, q_offset 20");
+    check_close(attention_forward(q, k, v, false).unwrap().to_vec(), standard_attention(q, k, v, false),
+                "GQA non-causal");
+}
+
+// ---- errors (src/error.rs) ---------------------------------------------------
+
+TEST_GPU(test_shape_errors_match_reference) {
+    manual_seed(8);
+    RawTensor q = RawTensor::randn({2, 4, 16, 32}, 0.f, 1.f);
+    RawTensor k = RawTensor::randn({2, 2, 16, 32}, 0.f, 1.f);
+    RawTensor three = RawTensor::randn({2, 16, 32}, 0.f, 1.f);
+    auto r = flash_attention_forward(q, k, k, true, std::nullopt, 64, 64);   // flash_attention.rs:43-48
+    CHECK(r.is_err());
+    CHECK(r.error() == EngineError::shape_mismatch({2, 4, 16, 32}, {2, 2, 16, 32}));
+    auto r2 = flash_attention_forward(three, q, q, true, std::nullopt, 64, 64);  // :32-37
+    CHECK(r2.is_err() && r2.error().kind == EngineError::Kind::InvalidArgument);
+    CHECK(r2.error().to_string() ==
+          "Invalid configuration or argument: FlashAttention expects 4D tensors [Batch, Heads, SeqLen, Dim], "
+          "got Q:[2, 16, 32], K:[2, 4, 16, 32], V:[2, 4, 16, 32]");
+    FlashAttention layer(32, 2, false);
+    auto r3 = layer.forward(q);                                              // :240-246
+    CHECK(r3.is_err() && r3.error().kind == EngineError::Kind::IncompatibleShapes);
+    KVCache cache(4, 2, 2, 8, 32);
+    auto r4 = cache.update(9, k, k);                                          // kv_cache.rs:55-61
+    CHECK(r4.is_err() && r4.error().to_string() ==
+                             "Invalid configuration or argument: KVCache layer index 9 out of range (total layers: 4)");
+    RawTensor big = RawTensor::randn({2, 2, 9, 32}, 0.f, 1.f);
+    auto r5 = cache.update(0, big, big);                                      // past capacity: nothing written
+    CHECK(r5.is_err() && r5.error().kind == EngineError::Kind::GpuError);
+    CHECK(cache.current_seq_len(0) == 0);
+    CHECK(cache.current_seq_len(99) == 0);                                    // kv_cache.rs:37-44
+}
+
+TEST_CPU(test_error_messages_and_result) {
+    CHECK(EngineError::shape_mismatch({2, 4, 16, 32}, {2, 2, 16, 32}).to_string() ==
+          "Shape mismatch error: expected shape [2, 4, 16, 32], got [2, 2, 16, 32]");
+    CHECK(EngineError::incompatible_shapes("FlashAttention forward (expected 3D input [B, T, C])", {{2, 3}})
+              .to_string() ==
+          "Incompatible shapes for operation FlashAttention forward (expected 3D input [B, T, C]): [[2, 3]]");
+    CHECK(EngineError::gpu_error("x").to_string() == "GPU compute error: x");
+    CHECK(EngineError::non_contiguous_tensor().to_string() == "Tensor is not contiguous in memory");
+    Result<int> ok(3);
+    CHECK(ok.is_ok() && ok.value() == 3 && ok.unwrap() == 3);
+    Result<int> err(EngineError::invalid_argument("bad"));
+    CHECK(err.is_err());
+    bool threw = false;
+    try {
+        err.unwrap();
+    } catch (const std::runtime_error& e) {
+        threw = std::string(e.what()) == "Invalid configuration or argument: bad";
+    }
+    CHECK(threw);
+}
+
+TEST_CPU(test_layer_rejects_indivisible_heads) {                         // flash_attention.rs:217-223
+    bool threw = false;
+    try {
+        FlashAttention layer(30, 4, true);
+    } catch (const std::invalid_argument&) {
+        threw = true;
+    }
+    CHECK(threw);
+}
+
+}  // namespace
+
+int main(int argc, char** argv) {
+    const bool cpu_only = argc > 1 && std::strcmp(argv[1], "--cpu") == 0;
+    int failures = 0, ran = 0;
+    for (const Test& t : registry()) {
+        if (cpu_only && t.needs_gpu) continue;
+        ++ran;
+        std::printf("run %s\n", t.name);
+        std::fflush(stdout);
+        try {
+            t.fn();
+            std::printf("ok %s\n", t.name);
+        } catch (const std::exception& e) {
+            ++failures;
+            std::printf("FAIL %s: %s\n", t.name, e.what());
+        }
+        std::fflush(stdout);
+    }
+    std::printf("%d of %d tests failed\n", failures, ran);
+    return failures;
+}
