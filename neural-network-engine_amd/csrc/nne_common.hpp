@@ -48,8 +48,16 @@ struct PrefillParams {
     float qscale;   // softmax scale * log2(e), folded into Q
     int n_rb;       // ceil(Tq / 32)
     int n_units;    // G * n_rb
-    int n_wg;       // ceil(n_units / 4) workgroups per KV head
-    int total;      // B * Hkv * n_wg
+    int n_wg;       // ceil(n_units / 4) work items (4 units each) per KV head
+    int total;      // B * Hkv * n_wg work items
+    // Persistent schedule: a work item is the 4 units of one workgroup-sized
+    // step of a KV head.  With `pairing`, items of ranks r and n_wg-1-r of a
+    // head form one super-item (equal causal work); n_pairs super-items per
+    // head, n_super in all, per_xcd of them per XCD.
+    int pairing;
+    int n_pairs;
+    int n_super;
+    int per_xcd;
 };
 
 // Split-K few-query kernel parameters (decode and cross-attention).  Each KV

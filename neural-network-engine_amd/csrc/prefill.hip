@@ -30,6 +30,8 @@
 // the same staged tiles.  Workgroups are numbered so that each XCD works on a
 // contiguous range of KV heads (its own L2) and, within a head, the longest
 // causal row blocks start first.
+#include <utility>
+
 #include "nne_common.hpp"
 #include "nne_launch.hpp"
 
@@ -92,6 +94,29 @@ __device__ __forceinline__ int last_visible_key(const PrefillParams& p, int rb, 
     return lk < p.Tk - 1 ? lk : p.Tk - 1;
 }
 
+// The j-th work item of the workgroup in slot q of XCD x (S slots per XCD):
+// super-items x*per_xcd + q + k*S, k = 0, 1, ..., each one item (rank pr) or,
+// with pairing, two (ranks pr and n_wg-1-pr).  Rank r is wgi = n_wg-1-r, so
+// rank 0 holds the longest causal rows.  Returns 0 past the end, 2 for the
+// missing partner of an odd middle rank, 1 with (head, wgi) otherwise.
+__device__ __forceinline__ int item_at(const PrefillParams& p, int j, int x, int q, int S, int& head,
+                                       int& wgi) {
+    const int k = p.pairing ? j >> 1 : j;
+    const int s = x * p.per_xcd + q + k * S;
+    int s_end = (x + 1) * p.per_xcd;
+    if (s_end > p.n_super) s_end = p.n_super;
+    if (s >= s_end) return 0;
+    head = s / p.n_pairs;
+    const int pr = s % p.n_pairs;
+    int rank = pr;
+    if (p.pairing && (j & 1)) {
+        rank = p.n_wg - 1 - pr;
+        if (rank == pr) return 2;
+    }
+    wgi = p.n_wg - 1 - rank;
+    return 1;
+}
+
 template <int D, bool CAUSAL, bool VEC>
 __global__ __launch_bounds__(256, 2) void prefill_mfma_kernel(const PrefillParams p) {
     constexpr int KS = D + 4;          // K row stride in LDS (16-byte reads conflict-free)
@@ -100,18 +125,26 @@ __global__ __launch_bounds__(256, 2) void prefill_mfma_kernel(const PrefillParam
     constexpr int NB = D / 32;         // 32-wide output column blocks
     __shared__ __attribute__((aligned(16))) float lds[2 * STAGE];
 
-    // ---- workgroup -> (KV head, workgroup-in-head) --------------------------
+    // ---- persistent workgroup: slot q of XCD x -------------------------------
     // Hardware dispatches consecutive workgroup ids round-robin over the 8
-    // XCDs; remap so XCD c gets the contiguous logical range [c*per, (c+1)*per).
-    const int per = gridDim.x >> 3;
-    const int logical = (blockIdx.x & 7) * per + (blockIdx.x >> 3);
-    if (logical >= p.total) return;
-    const int head = logical / p.n_wg;
-    const int wgi = p.n_wg - 1 - (logical % p.n_wg);   // longest causal work first
-    const int bi = head / p.Hkv, kvh = head % p.Hkv;
+    // XCDs, so x = id & 7; each XCD owns a contiguous range of super-items
+    // (whole KV heads, its own L2).  The workgroup runs its items one after the
+    // other: no dispatch gaps, and the static schedule is balanced.
+    const int x = blockIdx.x & 7, q = blockIdx.x >> 3, S = gridDim.x >> 3;
 
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+#pragma nounroll
+    for (int j = 0;; ++j) {
+    int head = 0, wgi = 0;
+    const int st = item_at(p, j, x, q, S, head, wgi);
+    if (st == 0) break;
+    if (st == 2) continue;
+    // Lane-derived addressing is recomputed for every item rather than held
+    // live across the whole persistent loop.
+    int tid = threadIdx.x;
+    asm volatile("" : "+v"(tid));
+    const int lane = tid & 63, wave = tid >> 6;
     const int l32 = lane & 31, half = lane >> 5;
+    const int bi = head / p.Hkv, kvh = head % p.Hkv;
 
     const int unit = wgi * 4 + wave;
     const bool active = unit < p.n_units;
@@ -172,14 +205,12 @@ __global__ __launch_bounds__(256, 2) void prefill_mfma_kernel(const PrefillParam
 
     for (int kt = 0; kt < n_tiles; ++kt) {
         const bool has_next = kt + 1 < n_tiles;
-        if (has_next) ld.load(p, kb, vb, (kt + 1) * 32, tid);
-
-        if (kt < wave_tiles) {
-            const float* Ks = lds + (kt & 1) * STAGE;
-            const float* Vs = Ks + 32 * KS;
-
+        const bool mine = kt < wave_tiles;
+        const float* Ks = lds + (kt & 1) * STAGE;
+        const float* Vs = Ks + 32 * KS;
+        floatx16 s;
+        if (mine) {
             // S^T = K Q^T  (32 keys x 32 rows), log2 domain.
-            floatx16 s;
 #pragma unroll
             for (int r = 0; r < 16; ++r) s[r] = 0.f;
             const float* krow = Ks + l32 * KS + half * (D / 2);
@@ -194,8 +225,23 @@ __global__ __launch_bounds__(256, 2) void prefill_mfma_kernel(const PrefillParam
                 s = __builtin_amdgcn_mfma_f32_32x32x2f32(kq.z, qf[4 * t + 2], s, 0, 0, 0);
                 s = __builtin_amdgcn_mfma_f32_32x32x2f32(kq.w, qf[4 * t + 3], s, 0, 0, 0);
             }
+            // Schedule: the first 4 K reads, then one read per 4 MFMAs, so
+            // reads run 4 chunks (16 MFMAs) ahead of their use.
+#pragma unroll
+            for (int i = 0; i < 4; ++i) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+#pragma unroll
+            for (int i = 0; i < D / 8 - 4; ++i) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
+                __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+            }
+            __builtin_amdgcn_sched_group_barrier(0x008, 16, 0);
 
             __builtin_amdgcn_s_setprio(0);
+        }
+        // The next tile's loads are issued after the QK^T MFMAs, so their
+        // registers and the K operands are never live at the same time.
+        if (has_next) ld.load(p, kb, vb, (kt + 1) * 32, tid);
+        if (mine) {
             // Mask keys past T_k and (causal) keys after row + q_offset.
             const int key0 = kt * 32;
             const bool need_mask = (key0 + 32 > p.Tk) || (CAUSAL && key0 + 31 > row0 + p.q_offset);
@@ -245,6 +291,17 @@ __global__ __launch_bounds__(256, 2) void prefill_mfma_kernel(const PrefillParam
                 for (int b = 0; b < NB; ++b)
                     o[b] = __builtin_amdgcn_mfma_f32_32x32x2f32(vrow[32 * b], s[r], o[b], 0, 0, 0);
             }
+            // Schedule: V operands are read (two per ds_read2) 4 reads ahead of
+            // the MFMAs that use them.
+            constexpr int NVR = 16 * NB / 2;       // ds_read2_b32 per tile
+#pragma unroll
+            for (int i = 0; i < 4; ++i) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+#pragma unroll
+            for (int i = 0; i < NVR - 4; ++i) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+                __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+            }
+            __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);
             __builtin_amdgcn_s_setprio(0);
         }
 
@@ -278,12 +335,58 @@ __global__ __launch_bounds__(256, 2) void prefill_mfma_kernel(const PrefillParam
             }
         }
     }
+    __syncthreads();   // the next item's first tile reuses the LDS stages
+    }
 }
 
+// CUs and resident workgroups per CU of the kernel on the current device.
 template <int D, bool CAUSAL, bool VEC>
-hipError_t launch_t(const PrefillParams& p, hipStream_t stream) {
-    const int grid = ((p.total + 7) / 8) * 8;
-    hipLaunchKernelGGL((prefill_mfma_kernel<D, CAUSAL, VEC>), dim3(grid), dim3(256), 0, stream, p);
+void residency(int& cus, int& per_cu) {
+    static int cached_cus[64] = {0}, cached_per[64] = {0};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
+    if (cached_cus[dev] == 0) {
+        int c = 0, k = 0;
+        if (hipDeviceGetAttribute(&c, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || c < 8) c = 256;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&k, prefill_mfma_kernel<D, CAUSAL, VEC>, 256, 0) !=
+                hipSuccess || k < 1)
+            k = 1;
+        cached_per[dev] = k;
+        cached_cus[dev] = c;
+    }
+    cus = cached_cus[dev];
+    per_cu = cached_per[dev];
+}
+
+// One resident wave of persistent workgroups: k per CU on every CU (an
+// uneven count would leave the CUs that hold more workgroups behind), 8*S in
+// all with S = k * CUs / 8 per XCD, each XCD's super-items dealt round-robin.
+// k minimises rounds * k (the time of a round grows with the workgroups that
+// share a CU; one workgroup per CU leaves its SIMDs a single wave, taken as
+// 30 % slower).  Causal problems with enough work pair ranks r and n_wg-1-r
+// so that every super-item costs the same.
+template <int D, bool CAUSAL, bool VEC>
+hipError_t launch_t(PrefillParams p, hipStream_t stream) {
+    int cus = 0, k_max = 0;
+    residency<D, CAUSAL, VEC>(cus, k_max);
+    const int cu_per_xcd = cus / 8;
+    const int64_t heads = (int64_t)p.B * p.Hkv;
+    p.pairing = (CAUSAL && p.n_wg > 1 && heads * ((p.n_wg + 1) / 2) >= (int64_t)cus * k_max) ? 1 : 0;
+    p.n_pairs = p.pairing ? (p.n_wg + 1) / 2 : p.n_wg;
+    p.n_super = (int)(heads * p.n_pairs);
+    p.per_xcd = (p.n_super + 7) / 8;
+    int S = 1, best_rounds = 1;
+    double best = 1e300;
+    for (int k = 1; k <= k_max; ++k) {
+        const int s = k * cu_per_xcd;
+        const int rounds = (p.per_xcd + s - 1) / s;
+        const double cost = (double)rounds * k * (k == 1 ? 1.3 : 1.0);
+        if (cost < best) { best = cost; S = s; best_rounds = rounds; }
+    }
+    // A partly empty last round costs more than the hardware's own dispatch of
+    // one super-item per workgroup (which also covers small problems).
+    if (S >= p.per_xcd || (double)p.per_xcd / ((double)best_rounds * S) < 0.97) S = p.per_xcd;
+    hipLaunchKernelGGL((prefill_mfma_kernel<D, CAUSAL, VEC>), dim3(8 * S), dim3(256), 0, stream, p);
     return hipGetLastError();
 }
 
