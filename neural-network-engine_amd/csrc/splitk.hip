@@ -409,18 +409,21 @@ __global__ __launch_bounds__(256, 2) void splitk_kernel(const SplitKParams p) {
         // are masked to -inf, so the finite data gets weight 0); columns past d
         // read the row's last 4 floats (their Q columns are zero, their O
         // columns are never stored).  Loads are branch-free, so the next block
-        // stays in flight while the current one computes.
+        // stays in flight while the current one computes.  They are
+        // non-temporal: each K/V byte is read once per launch, and keeping the
+        // stream out of the caches' normal allocation lifts a chunked read of
+        // the cache from ~6.0 to ~6.9 TB/s on MI355X.
         auto load_block = [&](vf4 (&kr)[NK], vf4 (&vr)[4 * NH], int kb0) __attribute__((always_inline)) {
 #pragma unroll
             for (int i = 0; i < NK; ++i) {
                 const int key = min(kb0 + lane / LPR + RPI * i, key_end - 1);
-                kr[i] = *reinterpret_cast<const vf4*>(kb + key * kst + kc_col);
+                kr[i] = __builtin_nontemporal_load(reinterpret_cast<const vf4*>(kb + key * kst + kc_col));
             }
             if constexpr (NARROW) {
 #pragma unroll
                 for (int i = 0; i < NK; ++i) {
                     const int key = min(kb0 + lane / LPR + RPI * i, key_end - 1);
-                    vr[i] = *reinterpret_cast<const vf4*>(vb + key * vst + kc_col);
+                    vr[i] = __builtin_nontemporal_load(reinterpret_cast<const vf4*>(vb + key * vst + kc_col));
                 }
             } else {
 #pragma unroll
@@ -428,7 +431,7 @@ __global__ __launch_bounds__(256, 2) void splitk_kernel(const SplitKParams p) {
                     const int key = min(kb0 + 4 * grp + st, key_end - 1);
 #pragma unroll
                     for (int h = 0; h < NH; ++h)
-                        vr[st * NH + h] = *reinterpret_cast<const vf4*>(vb + key * vst + v_col[h]);
+                        vr[st * NH + h] = __builtin_nontemporal_load(reinterpret_cast<const vf4*>(vb + key * vst + v_col[h]));
                 }
             }
         };
