@@ -30,7 +30,7 @@ enum {
     NNE_EHIP = 4       /* HIP runtime failure            -> EngineError::GpuError (src/error.rs:48) */
 };
 
-#define NNE_ABI_VERSION 1
+#define NNE_ABI_VERSION 2
 
 int nne_abi_version(void);
 
@@ -132,6 +132,65 @@ int nne_decode_step(const float *q, const int64_t q_strides[4], float *k_cache, 
                     int64_t B, int64_t Hq, int64_t Hkv, int64_t capacity, int64_t d,
                     int has_scale, float scale, void *workspace, uint64_t workspace_bytes,
                     void *stream);
+
+/* ---- decode prologue -----------------------------------------------------
+ * The steps of GroupedQueryAttention::forward_gqa_cached before attention
+ * (src/models/llama.rs:226-235): q/k/v projections (Linear::forward,
+ * src/nn/linear.rs:47-57) and rotary position embedding (RotaryEmbedding,
+ * llama.rs:64-158).  Positions are per sequence: the reference's start_pos
+ * (the cache length before the step, llama.rs:525) for each b. */
+
+/* RotaryEmbedding::new (llama.rs:74-107): fills HOST arrays cos_out and
+ * sin_out of max_seq_len * head_dim floats, in f32 exactly as the reference
+ * (inv_freq[i] = 1 / theta^(2i / head_dim); both halves of a row hold
+ * cos / sin(pos * inv_freq[i])).  Copy them to the device once
+ * (nne_memcpy_h2d).  NNE_EINVAL for an odd head_dim (the reference asserts). */
+int nne_rope_tables(float *cos_out, float *sin_out, int64_t max_seq_len, int64_t head_dim,
+                    float theta);
+
+/* RotaryEmbedding::apply (llama.rs:110-157) on a [B, H, T, d] view: row t of
+ * sequence b is rotated with table row start[b] + t (start_dev on the device,
+ * start_host the same values on the host, for validation).  out may be x with
+ * the same strides.  Products and the sum are rounded like the reference's
+ * x * cos + rotate_half(x) * sin, so results are bit-identical to it.
+ * NNE_ESHAPE if d != table_head_dim (:119-124); NNE_EINVAL if a range
+ * [start, start + T) exceeds max_seq_len (:131-139). */
+int nne_rope_apply(const float *x, const int64_t x_shape[4], const int64_t x_strides[4], float *out,
+                   const int64_t out_strides[4], const float *cos_table, const float *sin_table,
+                   int64_t max_seq_len, int64_t table_head_dim, const int32_t *start_dev,
+                   const int32_t *start_host, void *stream);
+
+/* Bytes of the packed q/k/v weights of nne_qkv_pack (0 for unsupported
+ * geometry: d and C must be multiples of 64). */
+uint64_t nne_qkv_packed_bytes(int64_t C, int64_t Hq, int64_t Hkv, int64_t d);
+
+/* Packs the three Linear weights of GroupedQueryAttention (q_proj, k_proj,
+ * v_proj: [H * d, C] row-major, llama.rs:189-192) once, into the order the
+ * fused projection streams them (tiles of 64 output columns holding 32 RoPE
+ * pairs, 64-wide slices of C, MFMA lane order).  The weights are static, so
+ * this runs once per layer; packed must hold nne_qkv_packed_bytes bytes. */
+int nne_qkv_pack(const float *wq, const float *wk, const float *wv, float *packed, int64_t C,
+                 int64_t Hq, int64_t Hkv, int64_t d, void *stream);
+
+/* Fused decode prologue (t = 1): for every sequence b, with x row b at
+ * x + b * x_row_stride ([B, C], d_model C),
+ *   q = RoPE(x Wq^T + bq), k = RoPE(x Wk^T + bk), v = x Wv^T + bv
+ * at position pos[b] (pos_dev on the device, pos_host for validation), split
+ * into heads and written to contiguous q_out [B, Hq, 1, d], k_out and v_out
+ * [B, Hkv, 1, d] -- the q, k_new and v_new of nne_decode_step, which appends
+ * k/v in place and attends.  w_packed comes from nne_qkv_pack; biases are
+ * [H * d] or NULL (llama.rs uses Linear::without_bias).  One launch streams
+ * the weights once; the reduction over C is split across workgroups whose
+ * partial sums are merged inside the launch, in a fixed order, with the
+ * library's per-stream workspace and counters (as nne_decode_attention).
+ * Requires d % 64 == 0, C % 64 == 0, x rows 16-byte aligned with
+ * x_row_stride >= C and a multiple of 4.  NNE_ESHAPE if d != table_head_dim;
+ * NNE_EINVAL if pos[b] >= max_seq_len. */
+int nne_qkv_rope(const float *x, int64_t x_row_stride, const float *w_packed, const float *bq,
+                 const float *bk, const float *bv, const float *cos_table, const float *sin_table,
+                 int64_t max_seq_len, int64_t table_head_dim, const int32_t *pos_dev,
+                 const int32_t *pos_host, float *q_out, float *k_out, float *v_out, int64_t B,
+                 int64_t C, int64_t Hq, int64_t Hkv, int64_t d, void *stream);
 
 #ifdef __cplusplus
 }

@@ -12,6 +12,10 @@ engine's attention API (elvin-mark/neural-network-engine):
 * ``KVCache`` -- src/nn/kv_cache.rs:11-74, stored on the device head-major
   and appended in place
 * ``FlashAttention`` layer -- src/nn/flash_attention.rs:202-292
+* ``RotaryEmbedding`` -- src/models/llama.rs:64-158
+* ``qkv_rope`` -- the fused decode prologue (q/k/v projections + RoPE) of
+  GroupedQueryAttention::forward_gqa_cached (llama.rs:226-235)
+* ``GroupedQueryAttention`` -- src/models/llama.rs:160-300
 
 Tensors are torch tensors on the GPU (torch is used only for device memory and
 streams).  Errors raise the EngineError variant the reference would return.
@@ -88,6 +92,18 @@ SIGNATURES = {
         _vp, _i64p, _vp, _vp, _vp, _i32p, _vp, _i64p, _vp, _i64p, _vp, _i64p,
         ctypes.c_int64, ctypes.c_int64, ctypes.c_int64, ctypes.c_int64, ctypes.c_int64,
         ctypes.c_int, ctypes.c_float, _vp, ctypes.c_uint64, _vp]),
+    "nne_rope_tables": (ctypes.c_int, [_vp, _vp, ctypes.c_int64, ctypes.c_int64, ctypes.c_float]),
+    "nne_rope_apply": (ctypes.c_int, [
+        _vp, _i64p, _i64p, _vp, _i64p, _vp, _vp, ctypes.c_int64, ctypes.c_int64, _vp, _i32p,
+        _vp]),
+    "nne_qkv_packed_bytes": (ctypes.c_uint64, [
+        ctypes.c_int64, ctypes.c_int64, ctypes.c_int64, ctypes.c_int64]),
+    "nne_qkv_pack": (ctypes.c_int, [
+        _vp, _vp, _vp, _vp, ctypes.c_int64, ctypes.c_int64, ctypes.c_int64, ctypes.c_int64, _vp]),
+    "nne_qkv_rope": (ctypes.c_int, [
+        _vp, ctypes.c_int64, _vp, _vp, _vp, _vp, _vp, _vp, ctypes.c_int64,
+        ctypes.c_int64, _vp, _i32p, _vp, _vp, _vp, ctypes.c_int64, ctypes.c_int64,
+        ctypes.c_int64, ctypes.c_int64, ctypes.c_int64, _vp]),
 }
 
 
@@ -339,3 +355,170 @@ class FlashAttention:
         return torch.nn.functional.linear(out.view(b, t, self.d_model), *self.out_proj)
 
     __call__ = forward
+
+
+class RotaryEmbedding:
+    """RotaryEmbedding (src/models/llama.rs:64-158).
+
+    The cos/sin tables are computed on the host in f32 exactly as the
+    reference's ``new`` (:74-107) and kept on the device; ``apply`` rotates a
+    [B, H, T, d] tensor on the GPU with the reference's roundings."""
+
+    def __init__(self, head_dim, max_seq_len, theta=10000.0, device="cuda"):
+        import torch
+        self.head_dim, self.max_seq_len = int(head_dim), int(max_seq_len)
+        cos = np.zeros((max(self.max_seq_len, 0), max(self.head_dim, 0)), np.float32)
+        sin = np.zeros_like(cos)
+        check(lib().nne_rope_tables(cos.ctypes.data, sin.ctypes.data, self.max_seq_len,
+                                    self.head_dim, float(theta)))
+        self.cos_host, self.sin_host = cos, sin
+        self.cos = torch.from_numpy(cos).to(device)
+        self.sin = torch.from_numpy(sin).to(device)
+
+    def _starts(self, start_pos, b, device):
+        import torch
+        sp = np.ascontiguousarray(np.broadcast_to(np.asarray(start_pos, np.int32), (b,)))
+        return sp, torch.from_numpy(sp.copy()).to(device)
+
+    def apply(self, x, start_pos, out=None, stream=None):
+        """x [B, H, T, d] (any strides); row t of sequence b uses position
+        start_pos[b] + t (start_pos: an int or B ints).  Returns ``out``
+        (a new contiguous tensor by default; may be ``x`` itself)."""
+        import torch
+        if x.dim() != 4:
+            raise InvalidArgument(
+                "Invalid configuration or argument: RoPE apply expects 4D tensor [Batch, Heads, "
+                "SeqLen, HeadDim], got rank %d with shape %s" % (x.dim(), list(x.shape)))
+        _require_f32_cuda(x)
+        if out is None:
+            out = torch.empty(tuple(x.shape), dtype=torch.float32, device=x.device)
+        sp_h, sp_d = self._starts(start_pos, x.shape[0], x.device)
+        check(lib().nne_rope_apply(
+            x.data_ptr(), _i64(x.shape), _i64(x.stride()), out.data_ptr(), _i64(out.stride()),
+            self.cos.data_ptr(), self.sin.data_ptr(), self.max_seq_len, self.head_dim,
+            sp_d.data_ptr(), sp_h.ctypes.data_as(_i32p), _stream(stream)))
+        return out
+
+
+def qkv_pack(wq, wk, wv, num_heads, num_kv_heads, stream=None):
+    """Packs q_proj / k_proj / v_proj weights ([H * d, C]) for ``qkv_rope``
+    (once per layer: the weights are static)."""
+    import torch
+    _require_f32_cuda(wq, wk, wv)
+    c = wq.shape[1]
+    d = wq.shape[0] // num_heads
+    nbytes = lib().nne_qkv_packed_bytes(c, num_heads, num_kv_heads, d)
+    if nbytes == 0:
+        raise InvalidArgument("Invalid configuration or argument: the fused projection needs a "
+                              "head dim and a d_model that are multiples of 64")
+    packed = torch.empty(int(nbytes) // 4, dtype=torch.float32, device=wq.device)
+    check(lib().nne_qkv_pack(wq.contiguous().data_ptr(), wk.contiguous().data_ptr(),
+                             wv.contiguous().data_ptr(), packed.data_ptr(), c, num_heads,
+                             num_kv_heads, d, _stream(stream)))
+    return packed
+
+
+def qkv_rope(x, w_packed, bq, bk, bv, rope, pos_dev, pos_host, num_heads, num_kv_heads,
+             q_out=None, k_out=None, v_out=None, stream=None):
+    """Fused decode prologue: x [B, C] (or [B, 1, C]) -> q [B, Hq, 1, d] and
+    k, v [B, Hkv, 1, d] with q = RoPE(x Wq^T + bq), k = RoPE(x Wk^T + bk),
+    v = x Wv^T + bv at positions pos (int32, device and host copies);
+    ``w_packed`` comes from ``qkv_pack``."""
+    import torch
+    x2 = x.reshape(x.shape[0], x.shape[-1]) if x.dim() == 3 else x
+    _require_f32_cuda(x2, w_packed)
+    b, c = x2.shape
+    d = rope.head_dim
+    dev = x2.device
+    if q_out is None:
+        q_out = torch.empty((b, num_heads, 1, d), dtype=torch.float32, device=dev)
+    if k_out is None:
+        k_out = torch.empty((b, num_kv_heads, 1, d), dtype=torch.float32, device=dev)
+    if v_out is None:
+        v_out = torch.empty((b, num_kv_heads, 1, d), dtype=torch.float32, device=dev)
+    pos_host = np.ascontiguousarray(pos_host, dtype=np.int32)
+
+    def ptr(t):
+        return None if t is None else t.data_ptr()
+
+    for t in (q_out, k_out, v_out):
+        if not t.is_contiguous():
+            raise InvalidArgument("Invalid configuration or argument: outputs must be contiguous")
+    check(lib().nne_qkv_rope(
+        x2.data_ptr(), x2.stride(0), w_packed.data_ptr(), ptr(bq), ptr(bk), ptr(bv),
+        rope.cos.data_ptr(), rope.sin.data_ptr(), rope.max_seq_len, rope.head_dim,
+        pos_dev.data_ptr(), pos_host.ctypes.data_as(_i32p), q_out.data_ptr(), k_out.data_ptr(),
+        v_out.data_ptr(), b, c, num_heads, num_kv_heads, d, _stream(stream)))
+    return q_out, k_out, v_out
+
+
+class GroupedQueryAttention:
+    """GroupedQueryAttention (src/models/llama.rs:160-300), forward only.
+
+    Decode steps (T = 1 with a cache) run the fused prologue (projections +
+    RoPE in one launch, on weights packed at construction) and the fused
+    append + attend launch; the output projection is a plain GEMM.  Longer
+    inputs (and head dims or widths that are not multiples of 64) project with
+    GEMMs, rotate with ``RotaryEmbedding.apply``, append to the cache and run
+    the attention kernel with q_offset = start_pos (:277-292)."""
+
+    def __init__(self, d_model, num_heads, num_kv_heads, max_seq_len, rope_theta=10000.0,
+                 device="cuda", seed=0):
+        import torch
+        if d_model % num_heads != 0:
+            raise InvalidArgument("d_model must be divisible by num_heads")
+        if num_heads % num_kv_heads != 0:
+            raise InvalidArgument("num_heads must be divisible by num_kv_heads for GQA")
+        self.num_heads, self.num_kv_heads = num_heads, num_kv_heads
+        self.head_dim = d_model // num_heads
+        self.d_model = d_model
+        kv_dim = num_kv_heads * self.head_dim
+        g = torch.Generator(device="cpu").manual_seed(seed)
+
+        def w(out_f, in_f):   # Linear::without_bias, Kaiming-uniform range
+            bound = math.sqrt(6.0 / in_f)
+            return ((torch.rand(out_f, in_f, generator=g) * 2 - 1) * bound).to(device)
+
+        self.wq, self.wk = w(d_model, d_model), w(kv_dim, d_model)
+        self.wv, self.wo = w(kv_dim, d_model), w(d_model, d_model)
+        self.rope = RotaryEmbedding(self.head_dim, max_seq_len, rope_theta, device)
+        self.w_packed = None
+        if self.head_dim % 64 == 0 and d_model % 64 == 0:
+            self.w_packed = qkv_pack(self.wq, self.wk, self.wv, num_heads, num_kv_heads)
+
+    def forward_gqa_cached(self, x, start_pos, cache=None, layer_idx=0, stream=None):
+        """x [B, T, C].  With a cache, start_pos must be each sequence's cached
+        length (an int for equal lengths, or B ints)."""
+        import torch
+        if x.dim() != 3:
+            raise EngineError("Incompatible shapes for operation GroupedQueryAttention forward "
+                              "(expected 3D input [B, T, C]): %s" % [list(x.shape)])
+        b, t, c = x.shape
+        hq, hkv, d = self.num_heads, self.num_kv_heads, self.head_dim
+        sp = np.ascontiguousarray(np.broadcast_to(np.asarray(start_pos, np.int32), (b,)))
+        if cache is not None:
+            cache._check_layer(layer_idx)
+            if not np.array_equal(sp, cache.lens_host[layer_idx]):
+                raise InvalidArgument("Invalid configuration or argument: start_pos must equal "
+                                      "the cached length of every sequence")
+        if cache is not None and t == 1 and self.w_packed is not None:
+            q, k_new, v_new = qkv_rope(x, self.w_packed, None, None, None, self.rope,
+                                       cache.lens_dev[layer_idx], sp, hq, hkv, stream=stream)
+            ctx = cache.decode_step(layer_idx, q, k_new, v_new, stream=stream)
+            return torch.nn.functional.linear(ctx.view(b, 1, hq * d), self.wo)
+        q = torch.nn.functional.linear(x, self.wq).view(b, t, hq, d).transpose(1, 2)
+        k = torch.nn.functional.linear(x, self.wk).view(b, t, hkv, d).transpose(1, 2)
+        v = torch.nn.functional.linear(x, self.wv).view(b, t, hkv, d).transpose(1, 2)
+        q = self.rope.apply(q, sp, stream=stream)
+        k = self.rope.apply(k, sp, stream=stream)
+        if cache is not None:
+            k_all, v_all = cache.update(layer_idx, k, v, stream=stream)
+            if b > 1 and not (sp == sp[0]).all():
+                raise InvalidArgument("Invalid configuration or argument: multi-token steps need "
+                                      "equal cached lengths")
+        else:
+            k_all, v_all = k, v
+        out = torch.empty((b, t, hq, d), dtype=torch.float32, device=x.device)
+        attention_forward(q, k_all, v_all, t > 1, q_offset=int(sp[0]) if b else 0,
+                          out=out.transpose(1, 2), stream=stream)
+        return torch.nn.functional.linear(out.view(b, t, hq * d), self.wo)

@@ -509,4 +509,168 @@ int nne_decode_step(const float* q, const int64_t q_strides[4], float* k_cache, 
                       has_scale, scale, workspace, workspace_bytes, as_stream(stream));
 }
 
+// ---- decode prologue: projections and rotary position embedding ----------
+
+int nne_rope_tables(float* cos_out, float* sin_out, int64_t max_seq_len, int64_t head_dim,
+                    float theta) {
+    // RotaryEmbedding::new (llama.rs:74-107); the reference asserts an even
+    // head_dim (:75).
+    if (head_dim <= 0 || head_dim % 2 != 0)
+        return fail(NNE_EINVAL, "Invalid configuration or argument: RoPE head_dim (%lld) must be "
+                                "even", (long long)head_dim);
+    if (max_seq_len < 0)
+        return fail(NNE_EINVAL, "Invalid configuration or argument: RoPE max_seq_len %lld",
+                    (long long)max_seq_len);
+    if (max_seq_len > 0 && (!cos_out || !sin_out))
+        return fail(NNE_EINVAL, "Invalid configuration or argument: null table pointer");
+    nne::rope_tables_host(cos_out, sin_out, max_seq_len, head_dim, theta);
+    return NNE_OK;
+}
+
+namespace {
+
+// RotaryEmbedding::apply's checks (llama.rs:115-139) for rows
+// [start, start + t) of every sequence.
+int check_rope_range(const int32_t* start_host, int64_t B, int64_t t, int64_t max_seq_len) {
+    if (B > 0 && !start_host)
+        return fail(NNE_EINVAL, "Invalid configuration or argument: start positions are null");
+    for (int64_t b = 0; b < B; ++b) {
+        const int64_t s = start_host[b];
+        if (s < 0 || s + t > max_seq_len)
+            return fail(NNE_EINVAL, "Invalid configuration or argument: Sequence range [%lld, %lld) "
+                                    "exceeds RoPE max_seq_len %lld",
+                        (long long)s, (long long)(s + t), (long long)max_seq_len);
+    }
+    return NNE_OK;
+}
+
+}  // namespace
+
+int nne_rope_apply(const float* x, const int64_t x_shape[4], const int64_t x_strides[4], float* out,
+                   const int64_t out_strides[4], const float* cos_table, const float* sin_table,
+                   int64_t max_seq_len, int64_t table_head_dim, const int32_t* start_dev,
+                   const int32_t* start_host, void* stream) {
+    if (!x_shape)
+        return fail(NNE_EINVAL, "Invalid configuration or argument: RoPE apply expects 4D tensor "
+                                "[Batch, Heads, SeqLen, HeadDim]");
+    if (!dims_ok(x_shape))
+        return fail(NNE_EINVAL, "Invalid configuration or argument: RoPE dims out of range, got %s",
+                    shape_str(x_shape).c_str());
+    const int64_t B = x_shape[0], H = x_shape[1], T = x_shape[2], d = x_shape[3];
+    if (d != table_head_dim)   // llama.rs:119-124
+        return fail(NNE_ESHAPE, "Shape mismatch error: expected shape [%lld], got [%lld]",
+                    (long long)table_head_dim, (long long)d);
+    if (d % 2 != 0)
+        return fail(NNE_EINVAL, "Invalid configuration or argument: RoPE head_dim (%lld) must be "
+                                "even", (long long)d);
+    int rc = check_rope_range(start_host, B, T, max_seq_len);
+    if (rc) return rc;
+    if (B * H * T * d == 0) return NNE_OK;
+    if (!x || !out || !cos_table || !sin_table || !start_dev)
+        return fail(NNE_EINVAL, "Invalid configuration or argument: null tensor pointer");
+    int64_t c[4];
+    contiguous_strides(x_shape, c);
+    hipError_t e = nne::launch_rope_apply(make_view(x, x_strides ? x_strides : c),
+                                          make_out(out, out_strides ? out_strides : c), (int)B,
+                                          (int)H, (int)T, (int)d, cos_table, sin_table, start_dev,
+                                          as_stream(stream));
+    return e == hipSuccess ? NNE_OK : hip_fail(e, "RoPE launch");
+}
+
+namespace {
+
+// Shared checks of the packed-projection entry points.
+int check_qkv_geometry(int64_t C, int64_t Hq, int64_t Hkv, int64_t d) {
+    if (C <= 0 || Hq <= 0 || Hkv <= 0 || d <= 0 || C > INT32_MAX || Hq > INT32_MAX ||
+        Hkv > INT32_MAX || (Hq + 2 * Hkv) * d > INT32_MAX || (Hq + 2 * Hkv) * d * C > INT64_MAX / 8)
+        return fail(NNE_EINVAL, "Invalid configuration or argument: bad projection geometry "
+                                "C=%lld Hq=%lld Hkv=%lld d=%lld", (long long)C, (long long)Hq,
+                    (long long)Hkv, (long long)d);
+    if (d % 64 != 0 || C % 64 != 0)
+        return fail(NNE_EINVAL, "Invalid configuration or argument: the fused projection needs a "
+                                "head dim (got %lld) and a d_model (got %lld) that are multiples "
+                                "of 64", (long long)d, (long long)C);
+    return NNE_OK;
+}
+
+int device_cus() {
+    static int cached[64] = {0};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
+    if (cached[dev] == 0) {
+        int cus = 0;
+        if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+            cus <= 0)
+            cus = 256;
+        cached[dev] = cus;
+    }
+    return cached[dev];
+}
+
+}  // namespace
+
+uint64_t nne_qkv_packed_bytes(int64_t C, int64_t Hq, int64_t Hkv, int64_t d) {
+    if (check_qkv_geometry(C, Hq, Hkv, d) != NNE_OK) return 0;
+    return 4 * nne::qkv_packed_floats((int)C, (int)Hq, (int)Hkv, (int)d);
+}
+
+int nne_qkv_pack(const float* wq, const float* wk, const float* wv, float* packed, int64_t C,
+                 int64_t Hq, int64_t Hkv, int64_t d, void* stream) {
+    int rc = check_qkv_geometry(C, Hq, Hkv, d);
+    if (rc) return rc;
+    if (!wq || !wk || !wv || !packed)
+        return fail(NNE_EINVAL, "Invalid configuration or argument: null tensor pointer");
+    if (!aligned16(wq) || !aligned16(wk) || !aligned16(wv) || !aligned16(packed))
+        return fail(NNE_EINVAL, "Invalid configuration or argument: weights must be 16-byte aligned");
+    hipError_t e = nne::launch_qkv_pack(wq, wk, wv, packed, (int)C, (int)Hq, (int)Hkv, (int)d,
+                                        as_stream(stream));
+    return e == hipSuccess ? NNE_OK : hip_fail(e, "weight packing launch");
+}
+
+int nne_qkv_rope(const float* x, int64_t x_row_stride, const float* w_packed, const float* bq,
+                 const float* bk, const float* bv, const float* cos_table, const float* sin_table,
+                 int64_t max_seq_len, int64_t table_head_dim, const int32_t* pos_dev,
+                 const int32_t* pos_host, float* q_out, float* k_out, float* v_out, int64_t B,
+                 int64_t C, int64_t Hq, int64_t Hkv, int64_t d, void* stream) {
+    if (B < 0 || B > INT32_MAX)
+        return fail(NNE_EINVAL, "Invalid configuration or argument: batch %lld", (long long)B);
+    if (d != table_head_dim)   // llama.rs:119-124
+        return fail(NNE_ESHAPE, "Shape mismatch error: expected shape [%lld], got [%lld]",
+                    (long long)table_head_dim, (long long)d);
+    int rc = check_qkv_geometry(C, Hq, Hkv, d);
+    if (rc) return rc;
+    rc = check_rope_range(pos_host, B, 1, max_seq_len);
+    if (rc) return rc;
+    if (B == 0) return NNE_OK;
+    if (!x || !w_packed || !cos_table || !sin_table || !pos_dev || !q_out || !k_out || !v_out)
+        return fail(NNE_EINVAL, "Invalid configuration or argument: null tensor pointer");
+    if (x_row_stride < C || x_row_stride % 4 != 0 || !aligned16(x) || !aligned16(w_packed))
+        return fail(NNE_EINVAL, "Invalid configuration or argument: x rows and packed weights "
+                                "must be 16-byte aligned with a row stride >= d_model and a "
+                                "multiple of 4");
+    const nne::QkvWorkspace w = nne::qkv_workspace((int)C, (int)Hq, (int)Hkv, (int)d, device_cus());
+    uint32_t* counters = nullptr;
+    void* ws = nullptr;
+    hipError_t e = stream_resources(w.n_tiles, w.floats * 4, as_stream(stream), &counters, &ws);
+    if (e != hipSuccess) return hip_fail(e, "projection workspace");
+    nne::QkvParams p{};
+    p.x = x;
+    p.x_rs = x_row_stride;
+    p.wp = w_packed;
+    p.bias[0] = bq; p.bias[1] = bk; p.bias[2] = bv;
+    p.cos = cos_table;
+    p.sin = sin_table;
+    p.pos = pos_dev;
+    p.out[0] = q_out; p.out[1] = k_out; p.out[2] = v_out;
+    p.o_sb[0] = Hq * d; p.o_sh[0] = d;
+    p.o_sb[1] = Hkv * d; p.o_sh[1] = d;
+    p.o_sb[2] = Hkv * d; p.o_sh[2] = d;
+    p.M = (int)B; p.C = (int)C; p.Hq = (int)Hq; p.Hkv = (int)Hkv; p.d = (int)d;
+    p.n_tiles = w.n_tiles; p.S = w.S; p.kc_per_slice = w.kc_per_slice;
+    p.ws = static_cast<float*>(ws);
+    p.cnt = counters;
+    e = nne::launch_qkv_rope(p, as_stream(stream));
+    return e == hipSuccess ? NNE_OK : hip_fail(e, "q/k/v projection launch");
+}
+
 }  // extern "C"

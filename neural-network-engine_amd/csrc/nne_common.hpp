@@ -60,6 +60,29 @@ struct PrefillParams {
     int per_xcd;
 };
 
+// Fused decode prologue (qkv.hip): rows m < M of x [M, C] (row stride x_rs,
+// unit column stride) times the packed q/k/v weights (n_tiles tiles of 64
+// output columns, C split into S slices of kc_per_slice 64-wide chunks), plus
+// bias[j] (j = q, k, v; [H_j * d] or null); q and k rotated at position
+// pos[m] with tables cos/sin [max_seq_len, d]; row m, head h, dim i written to
+// out[j] + m * o_sb[j] + h * o_sh[j] + i.  With S > 1, ws holds the partial
+// tiles ([n_tiles][S][64][64]) and cnt[n_tiles] the zeroed arrival counters.
+struct QkvParams {
+    const float* x;
+    int64_t x_rs;
+    const float* wp;
+    const float* bias[3];
+    const float* cos;
+    const float* sin;
+    const int32_t* pos;
+    float* out[3];
+    int64_t o_sb[3], o_sh[3];
+    int M, C, Hq, Hkv, d;
+    int n_tiles, S, kc_per_slice;
+    float* ws;
+    uint32_t* cnt;
+};
+
 // Split-K few-query kernel parameters (decode and cross-attention).  Each KV
 // head serves R = G * Tq query rows; row rr maps to query head kvh*G + rr/Tq
 // and query position rr % Tq.  Every row sees every key of its sequence.
@@ -104,6 +127,27 @@ struct SplitKParams {
 };
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// Partial records cross workgroups without a fence: they are written with
+// agent-scope relaxed atomic stores (global_store sc1, written through to the
+// device coherence point) and read with agent-scope relaxed atomic loads
+// (global_load sc1, never served from a stale per-XCD L2 line).  A writer waits
+// for its stores (vmcnt(0)) before its arrival is counted, and a reader loads
+// only after the count says every writer has arrived.  An agent-scope
+// release/acquire pair would also write back and invalidate the whole L2 of
+// each XCD, which costs tens of microseconds per launch.
+__device__ __forceinline__ void store_coherent(float* p, float x) {
+    __hip_atomic_store(p, x, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float load_coherent(const float* p) {
+    return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void wait_stores_performed() {
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0), expcnt/lgkmcnt unconstrained
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
+
 
 // Swaps lanes 32..63 of `a` with lanes 0..31 of `b` (gfx950 v_permlane32_swap).
 // Called with a == b == x, element 0 of the result holds x from lanes 0..31 in

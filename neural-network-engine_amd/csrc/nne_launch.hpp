@@ -43,4 +43,23 @@ hipError_t zero_counters(uint32_t* counters, int64_t n, hipStream_t stream);
 hipError_t launch_kv_append(float* kc, float* vc, int32_t* lens_dev, View4 kn, View4 vn, int B,
                             int Hkv, int cap, int d, int t_new, hipStream_t stream);
 
+// Decode prologue (qkv.hip).  Requires d % 64 == 0, C % 64 == 0, 16-byte
+// aligned x rows; any M (launched in groups of qkv_max_rows_per_launch()).
+int qkv_max_rows_per_launch();
+uint64_t qkv_packed_floats(int C, int Hq, int Hkv, int d);
+hipError_t launch_qkv_pack(const float* wq, const float* wk, const float* wv, float* packed, int C,
+                           int Hq, int Hkv, int d, hipStream_t stream);
+struct QkvWorkspace {
+    int n_tiles, S, kc_per_slice;
+    uint64_t floats;   // partial tiles (0 when S == 1)
+};
+QkvWorkspace qkv_workspace(int C, int Hq, int Hkv, int d, int cus);
+hipError_t launch_qkv_rope(QkvParams p, hipStream_t stream);
+// RoPE tables of RotaryEmbedding::new, computed on the host ([max_seq_len, d]).
+void rope_tables_host(float* cos_out, float* sin_out, int64_t max_seq_len, int64_t d, float theta);
+// RoPE on a strided [B, H, T, d] view (d even); row t of sequence b at table
+// row pos[b] + t.  o may alias x with the same strides.
+hipError_t launch_rope_apply(View4 x, OutView4 o, int B, int H, int T, int d, const float* cos_t,
+                             const float* sin_t, const int32_t* pos, hipStream_t stream);
+
 }  // namespace nne

@@ -111,25 +111,6 @@ __device__ __forceinline__ floatx4 mfma4(float a, float b, floatx4 c) {
     return __builtin_amdgcn_mfma_f32_4x4x1f32(a, b, c, CB, AB, 0);
 }
 
-// Partial records cross workgroups without a fence: they are written with
-// agent-scope relaxed atomic stores (global_store sc1, written through to the
-// device coherence point) and read with agent-scope relaxed atomic loads
-// (global_load sc1, never served from a stale per-XCD L2 line).  A writer waits
-// for its stores (vmcnt(0)) before its arrival is counted, and a reader loads
-// only after the count says every writer has arrived.  An agent-scope
-// release/acquire pair would also write back and invalidate the whole L2 of
-// each XCD, which costs tens of microseconds per launch.
-__device__ __forceinline__ void store_coherent(float* p, float x) {
-    __hip_atomic_store(p, x, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ float load_coherent(const float* p) {
-    return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ void wait_stores_performed() {
-    __atomic_signal_fence(__ATOMIC_SEQ_CST);
-    __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0), expcnt/lgkmcnt unconstrained
-    __atomic_signal_fence(__ATOMIC_SEQ_CST);
-}
 // Monotonic map of floats (incl. -inf) to unsigned, for LDS atomic max.
 __device__ __forceinline__ unsigned float_order(float x) {
     const unsigned u = __float_as_uint(x);

@@ -29,6 +29,17 @@
  *   oracle_decode_step        equals the matching row of a causal prefill
  *                             (the cached-vs-full pattern of
  *                             tests/nn/kv_cache_tests.rs:30-103).
+ *   oracle_rope_tables        float64 closed form cos/sin(p * theta^(-2i/d))
+ *                             within f32 rounding, the [c, c] / [s, s] halves,
+ *                             position 0 = (1, 0), the llama.rs:74-107 f32
+ *                             steps recomputed in numpy bit for bit.
+ *   oracle_rope_apply         float64 rotation of each (i, i + d/2) pair,
+ *                             norm preservation, identity at position 0,
+ *                             R(a) R(b) = R(a + b), q.k depending only on the
+ *                             position difference.
+ *   oracle_linear             float64 x W^T + b.
+ *   oracle_qkv_rope           composition of the two above with the
+ *                             [B, T, H, d] -> [B, H, T, d] head split.
  */
 #include <math.h>
 #include <pthread.h>
@@ -377,4 +388,104 @@ void oracle_decode_attend(const float *q, const float *k_cache, const float *v_c
     c.hq = hq; c.hkv = hkv; c.cap = cap; c.d = d;
     c.scale = has_scale ? scale : 1.0f / sqrtf((float)d);
     parallel_for(dec_item, &c, b * hq, n_threads);
+}
+
+/* ------------------------------------------------------------------------- */
+/* Decode prologue: Linear projections and rotary position embedding.        */
+/* ------------------------------------------------------------------------- */
+
+/* RotaryEmbedding::new (src/models/llama.rs:74-107): inv_freq[i] =
+ * 1 / theta^((2i) / d) in f32; for every position p < max_seq_len and
+ * i < d/2, cos[p][i] = cos[p][i + d/2] = cosf(p * inv_freq[i]) and the same
+ * for sin.  Tables are [max_seq_len][d]. */
+void oracle_rope_tables(float *cos_out, float *sin_out, int64_t max_seq_len, int64_t d,
+                        float theta) {
+    const int64_t half = d / 2;
+    for (int64_t i = 0; i < half; ++i) {
+        const float exponent = (float)(2 * i) / (float)d;
+        const float inv_freq = 1.0f / powf(theta, exponent);
+        for (int64_t p = 0; p < max_seq_len; ++p) {
+            const float freq = (float)p * inv_freq;
+            const float c = cosf(freq), s = sinf(freq);
+            cos_out[p * d + i] = c;
+            cos_out[p * d + i + half] = c;
+            sin_out[p * d + i] = s;
+            sin_out[p * d + i + half] = s;
+        }
+    }
+}
+
+/* RotaryEmbedding::apply (src/models/llama.rs:110-157) on x [B, H, T, d]:
+ * out = x * cos + rotate_half(x) * sin with rotate_half(x) = [-x2, x1]
+ * (:149-156), row t of sequence b taking table row start_pos[b] + t (the
+ * reference slices rows [start_pos, start_pos + T), :141-142; ragged batches
+ * give each sequence its own start).  Each product and the sum are rounded
+ * to f32 separately, as the reference's three tensor ops are. */
+void oracle_rope_apply(const float *x, float *out, const float *cos_t, const float *sin_t,
+                       int64_t b, int64_t h, int64_t t, int64_t d, const int32_t *start_pos) {
+    const int64_t half = d / 2;
+    for (int64_t bi = 0; bi < b; ++bi)
+        for (int64_t hi = 0; hi < h; ++hi)
+            for (int64_t ti = 0; ti < t; ++ti) {
+                const int64_t pos = (int64_t)start_pos[bi] + ti;
+                const float *c = cos_t + pos * d, *s = sin_t + pos * d;
+                const float *xr = x + ((bi * h + hi) * t + ti) * d;
+                float *o = out + ((bi * h + hi) * t + ti) * d;
+                for (int64_t i = 0; i < d; ++i) {
+                    const float rot = i < half ? -xr[i + half] : xr[i - half];
+                    const float term1 = xr[i] * c[i];
+                    const float term2 = rot * s[i];
+                    o[i] = term1 + term2;
+                }
+            }
+}
+
+/* Linear::forward (src/nn/linear.rs:47-57): y = x W^T (+ b) with x [M, K],
+ * W [N, K] (weight [out_features, in_features]), b [N] or NULL, y [M, N];
+ * each dot product summed in k order in f32, then the bias added. */
+void oracle_linear(const float *x, const float *w, const float *bias, float *y, int64_t m,
+                   int64_t k, int64_t n) {
+    for (int64_t i = 0; i < m; ++i)
+        for (int64_t j = 0; j < n; ++j) {
+            float acc = 0.0f;
+            for (int64_t kk = 0; kk < k; ++kk) acc += x[i * k + kk] * w[j * k + kk];
+            y[i * n + j] = bias ? acc + bias[j] : acc;
+        }
+}
+
+/* Steps 1-2 of GroupedQueryAttention::forward_gqa_cached
+ * (src/models/llama.rs:226-235) for x [B, T, C]: q = x Wq^T (+ bq) reshaped
+ * [B, T, Hq, d] -> [B, Hq, T, d], the same for k and v with Hkv heads, then
+ * RoPE on q and k at positions start_pos[b] + t.  Outputs are contiguous
+ * [B, Hq, T, d] and [B, Hkv, T, d]. */
+void oracle_qkv_rope(const float *x, const float *wq, const float *wk, const float *wv,
+                     const float *bq, const float *bk, const float *bv, const float *cos_t,
+                     const float *sin_t, const int32_t *start_pos, float *q_out, float *k_out,
+                     float *v_out, int64_t b, int64_t t, int64_t c, int64_t hq, int64_t hkv,
+                     int64_t d) {
+    const int64_t m = b * t;
+    float *yq = (float *)malloc(sizeof(float) * (size_t)(m * hq * d));
+    float *yk = (float *)malloc(sizeof(float) * (size_t)(m * hkv * d));
+    float *yv = (float *)malloc(sizeof(float) * (size_t)(m * hkv * d));
+    float *tq = (float *)malloc(sizeof(float) * (size_t)(m * hq * d));
+    float *tk = (float *)malloc(sizeof(float) * (size_t)(m * hkv * d));
+    oracle_linear(x, wq, bq, yq, m, c, hq * d);
+    oracle_linear(x, wk, bk, yk, m, c, hkv * d);
+    oracle_linear(x, wv, bv, yv, m, c, hkv * d);
+    /* [B, T, H, d] -> [B, H, T, d] (llama.rs:231-233) */
+    for (int64_t bi = 0; bi < b; ++bi)
+        for (int64_t ti = 0; ti < t; ++ti) {
+            for (int64_t hi = 0; hi < hq; ++hi)
+                memcpy(tq + ((bi * hq + hi) * t + ti) * d, yq + ((bi * t + ti) * hq + hi) * d,
+                       sizeof(float) * (size_t)d);
+            for (int64_t hi = 0; hi < hkv; ++hi) {
+                memcpy(tk + ((bi * hkv + hi) * t + ti) * d, yk + ((bi * t + ti) * hkv + hi) * d,
+                       sizeof(float) * (size_t)d);
+                memcpy(v_out + ((bi * hkv + hi) * t + ti) * d, yv + ((bi * t + ti) * hkv + hi) * d,
+                       sizeof(float) * (size_t)d);
+            }
+        }
+    oracle_rope_apply(tq, q_out, cos_t, sin_t, b, hq, t, d, start_pos);
+    oracle_rope_apply(tk, k_out, cos_t, sin_t, b, hkv, t, d, start_pos);
+    free(yq); free(yk); free(yv); free(tq); free(tk);
 }

@@ -62,6 +62,15 @@ def oracle():
         o.oracle_decode_attend.argtypes = [_f, _f, _f, _i32, _f, _I, _I, _I, _I, _I,
                                            ctypes.c_int, ctypes.c_float, ctypes.c_int]
         o.oracle_decode_attend.restype = None
+        o.oracle_rope_tables.argtypes = [_f, _f, _I, _I, ctypes.c_float]
+        o.oracle_rope_tables.restype = None
+        o.oracle_rope_apply.argtypes = [_f, _f, _f, _f, _I, _I, _I, _I, _i32]
+        o.oracle_rope_apply.restype = None
+        o.oracle_linear.argtypes = [_f, _f, _f, _f, _I, _I, _I]
+        o.oracle_linear.restype = None
+        o.oracle_qkv_rope.argtypes = [_f, _f, _f, _f, _f, _f, _f, _f, _f, _i32, _f, _f, _f, _I,
+                                      _I, _I, _I, _I, _I]
+        o.oracle_qkv_rope.restype = None
         _oracle = o
     return _oracle
 
@@ -132,6 +141,58 @@ def ref_kv_append(kc, vc, lens, kn, vn):
     rc = oracle().oracle_kv_append(_p(kc), _p(vc), lens.ctypes.data_as(_i32), _p(kn), _p(vn), b,
                                    hkv, cap, d, kn.shape[2])
     return rc, kc, vc, lens
+
+
+def _po(a):
+    return None if a is None else _p(a)
+
+
+def ref_rope_tables(max_seq_len, d, theta=10000.0):
+    cos = np.zeros((max_seq_len, d), np.float32)
+    sin = np.zeros((max_seq_len, d), np.float32)
+    oracle().oracle_rope_tables(_p(cos), _p(sin), max_seq_len, d, float(theta))
+    return cos, sin
+
+
+def ref_rope_apply(x, cos, sin, start_pos):
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    b, h, t, d = x.shape
+    sp = np.ascontiguousarray(np.broadcast_to(np.asarray(start_pos, np.int32), (b,)))
+    assert (sp >= 0).all() and (sp + t <= cos.shape[0]).all()
+    out = np.zeros_like(x)
+    oracle().oracle_rope_apply(_p(x), _p(out), _p(np.ascontiguousarray(cos)),
+                               _p(np.ascontiguousarray(sin)), b, h, t, d,
+                               sp.ctypes.data_as(_i32))
+    return out
+
+
+def ref_linear(x, w, bias=None):
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    w = np.ascontiguousarray(w, dtype=np.float32)
+    m, k = x.shape
+    n = w.shape[0]
+    y = np.zeros((m, n), np.float32)
+    bias = None if bias is None else np.ascontiguousarray(bias, dtype=np.float32)
+    oracle().oracle_linear(_p(x), _p(w), _po(bias), _p(y), m, k, n)
+    return y
+
+
+def ref_qkv_rope(x, wq, wk, wv, bq, bk, bv, cos, sin, start_pos, hq, hkv):
+    """x [B, T, C] -> (q [B, Hq, T, d], k [B, Hkv, T, d], v [B, Hkv, T, d])."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    b, t, c = x.shape
+    d = wq.shape[0] // hq
+    sp = np.ascontiguousarray(np.broadcast_to(np.asarray(start_pos, np.int32), (b,)))
+    q = np.zeros((b, hq, t, d), np.float32)
+    k = np.zeros((b, hkv, t, d), np.float32)
+    v = np.zeros((b, hkv, t, d), np.float32)
+    ws = [np.ascontiguousarray(a, dtype=np.float32) for a in (wq, wk, wv)]
+    bs = [None if a is None else np.ascontiguousarray(a, dtype=np.float32) for a in (bq, bk, bv)]
+    oracle().oracle_qkv_rope(_p(x), _p(ws[0]), _p(ws[1]), _p(ws[2]), _po(bs[0]), _po(bs[1]),
+                             _po(bs[2]), _p(np.ascontiguousarray(cos)),
+                             _p(np.ascontiguousarray(sin)), sp.ctypes.data_as(_i32), _p(q),
+                             _p(k), _p(v), b, t, c, hq, hkv, d)
+    return q, k, v
 
 
 def assert_close(got, ref, atol=ATOL, rtol=RTOL, what=""):

@@ -22,7 +22,7 @@ def test_library_exports_header_symbols(nne):
     for name in declared:
         assert hasattr(lib, name), name
         assert name in nne.SIGNATURES, name
-    assert lib.nne_abi_version() == 1
+    assert lib.nne_abi_version() == 2
 
 
 def test_flash_shape_mismatch_is_shape_error(nne):
@@ -124,3 +124,66 @@ def test_python_mirror_rejects_non_4d(nne):
 def test_layer_divisibility_check(nne):
     with pytest.raises(nne.InvalidArgument):
         nne.FlashAttention(30, 4, True, device="cpu")
+
+
+# ---------------------------------------------------------- decode prologue --
+
+def test_rope_tables_are_the_reference_tables(nne):
+    """nne_rope_tables runs on the host: bit-identical to the oracle's
+    restatement of RotaryEmbedding::new (llama.rs:74-107)."""
+    lib = nne.lib()
+    for d, n, theta in [(64, 300, 10000.0), (128, 4096, 10000.0), (16, 5, 500000.0)]:
+        cos = np.zeros((n, d), np.float32)
+        sin = np.zeros((n, d), np.float32)
+        assert lib.nne_rope_tables(cos.ctypes.data, sin.ctypes.data, n, d, theta) == nne.NNE_OK
+        rc, rs = T.ref_rope_tables(n, d, theta)
+        assert np.array_equal(cos, rc) and np.array_equal(sin, rs)
+
+
+def test_rope_tables_reject_odd_head_dim(nne):
+    lib = nne.lib()
+    cos = np.zeros(16, np.float32)
+    assert lib.nne_rope_tables(cos.ctypes.data, cos.ctypes.data, 2, 7, 10000.0) == nne.NNE_EINVAL
+    assert "RoPE head_dim (7) must be even" in lib.nne_last_error().decode()
+
+
+def test_rope_apply_host_checks(nne):
+    lib = nne.lib()
+    sp = np.array([0, 250], np.int32)
+    # head dim differs from the table's: ShapeMismatch {expected [64], actual [32]} (:119-124)
+    rc = lib.nne_rope_apply(FAKE, i64(2, 4, 8, 32), None, FAKE, None, FAKE, FAKE, 256, 64, FAKE,
+                            sp.ctypes.data_as(ctypes.POINTER(ctypes.c_int32)), None)
+    assert rc == nne.NNE_ESHAPE
+    assert "expected shape [64], got [32]" in lib.nne_last_error().decode()
+    # [250, 258) runs past max_seq_len 256 (:131-139)
+    rc = lib.nne_rope_apply(FAKE, i64(2, 4, 8, 64), None, FAKE, None, FAKE, FAKE, 256, 64, FAKE,
+                            sp.ctypes.data_as(ctypes.POINTER(ctypes.c_int32)), None)
+    assert rc == nne.NNE_EINVAL
+    assert "Sequence range [250, 258) exceeds RoPE max_seq_len 256" in lib.nne_last_error().decode()
+
+
+def test_qkv_rope_host_checks(nne):
+    lib = nne.lib()
+    pos = np.array([3, 7], np.int32)
+    pp = pos.ctypes.data_as(ctypes.POINTER(ctypes.c_int32))
+
+    def call(C=256, Hq=4, Hkv=2, d=64, table_d=64, max_len=8, x=FAKE, stride=256):
+        return lib.nne_qkv_rope(x, stride, FAKE, None, None, None, FAKE, FAKE, max_len, table_d,
+                                FAKE, pp, FAKE, FAKE, FAKE, 2, C, Hq, Hkv, d, None)
+
+    assert call(table_d=128) == nne.NNE_ESHAPE
+    assert call(d=48, table_d=48) == nne.NNE_EINVAL            # d % 64
+    assert call(C=200, stride=200) == nne.NNE_EINVAL           # C % 64
+    assert call(max_len=7) == nne.NNE_EINVAL                   # position 7 needs 8 rows
+    assert "Sequence range [7, 8) exceeds RoPE max_seq_len 7" in lib.nne_last_error().decode()
+    assert call(x=ctypes.c_void_p(4100)) == nne.NNE_EINVAL     # x rows not 16-byte aligned
+    assert call(stride=200) == nne.NNE_EINVAL                  # row stride < d_model
+
+
+def test_qkv_packed_bytes(nne):
+    lib = nne.lib()
+    assert lib.nne_qkv_packed_bytes(4096, 32, 8, 128) == 4 * 4096 * 48 * 128
+    assert lib.nne_qkv_packed_bytes(768, 12, 12, 64) == 4 * 768 * 36 * 64
+    assert lib.nne_qkv_packed_bytes(100, 4, 2, 64) == 0        # C % 64
+    assert lib.nne_qkv_packed_bytes(256, 4, 2, 32) == 0        # d % 64
+    assert lib.nne_qkv_pack(FAKE, FAKE, FAKE, FAKE, 256, 4, 2, 32, None) == nne.NNE_EINVAL
