@@ -169,6 +169,65 @@ def cpu_baseline(target_seconds=15.0):
                       "(unmasked pairs only)" % (heads, el)}
 
 
+def bench_decode_layer(nne, torch, dev, steps=32, seed=0x5EED0013):
+    """Config 3 as a GQA decode layer step (llama.rs:205-300, t = 1) minus
+    the output GEMM: the fused projection + RoPE launch on packed weights
+    (d_model 4096 = Hq * d), then the append + attend launch.  Three layers'
+    weights (3 x 100.7 MB) rotate so no step finds its weights in the 256 MB
+    MALL, as in a model whose layers run in turn."""
+    import numpy as np
+    b, hq, hkv, d = 32, 32, 8, 128
+    c = hq * d
+    rng = np.random.default_rng(seed)
+    lens0 = rng.integers(512, 4097, size=b).astype(np.int32)
+    cap = 4096 + 2 * steps + 8
+    g = torch.Generator(device=dev).manual_seed(seed)
+    bound = (1.0 / c) ** 0.5
+    packed = []
+    for _ in range(3):
+        w = [(torch.rand(n * d, c, generator=g, device=dev) * 2 - 1) * bound
+             for n in (hq, hkv, hkv)]
+        packed.append(nne.qkv_pack(w[0], w[1], w[2], hq, hkv))
+        del w
+    rope = nne.RotaryEmbedding(d, cap, device=dev)
+    cache = nne.KVCache(1, b, hkv, cap, d, device=dev)
+    cache.k[0].normal_(generator=g)
+    cache.v[0].normal_(generator=g)
+    xs = torch.randn(steps, b, c, generator=g, device=dev)
+    q = torch.empty(b, hq, 1, d, device=dev)
+    kn = torch.empty(b, hkv, 1, d, device=dev)
+    vn = torch.empty(b, hkv, 1, d, device=dev)
+    out = torch.empty(b, hq, 1, d, device=dev)
+    cache.set_lengths(0, lens0)
+    lens_dev = cache.lens_dev[0]
+    lens_host = cache.lens_host[0]
+
+    def prologue(i):
+        nne.qkv_rope(xs[i % steps], packed[i % 3], None, None, None, rope, lens_dev, lens_host,
+                     hq, hkv, q, kn, vn)
+
+    def layer_step(i):
+        prologue(i)
+        cache.decode_step(0, q, kn, vn, out=out)
+
+    for i in range(3):
+        prologue(i)
+    pro_ms = gpu_ms_per_call(torch, prologue, steps, queued=True)
+    layer_step(0)
+    cache.set_lengths(0, lens0)
+    step_ms = gpu_ms_per_call(torch, layer_step, steps, queued=True)
+    wbytes = (hq + 2 * hkv) * d * c * 4
+    pbytes = wbytes + b * c * 4 + b * (hq + 2 * hkv) * d * 4
+    gbs = pbytes / (pro_ms / 1e3) / 1e9
+    flops = 2.0 * b * c * (hq + 2 * hkv) * d
+    return {"workload": "config3 decode layer step: fused q/k/v projection + RoPE (d_model "
+                        "4096, packed weights, 3 layers rotated) + append/attend",
+            "prologue_ms": round(pro_ms, 4), "prologue_GB/s": round(gbs, 1),
+            "prologue_TFLOP/s": round(flops / (pro_ms / 1e3) / 1e12, 2),
+            "prologue_frac_hbm": round(gbs / PEAK_HBM_GBS, 4),
+            "prologue_bytes": pbytes, "layer_step_ms": round(step_ms, 4)}
+
+
 def probe(nne, torch, dev):
     """Fixed, short workload for rocprofv3 --pmc runs (one counter set per run)."""
     x = torch.empty(1 << 28, dtype=torch.float32, device=dev)     # 1 GiB
@@ -194,6 +253,8 @@ def probe(nne, torch, dev):
     for i in range(6):                        # config 5b, K/V sets rotated past the MALL
         nne.attention_forward(qx, kvs[i % 3][0], kvs[i % 3][1], False, out=ox)
     torch.cuda.synchronize()
+    bench_decode_layer(nne, torch, dev, steps=6)
+    torch.cuda.synchronize()
     print("probe done", file=sys.stderr, flush=True)
 
 
@@ -207,8 +268,8 @@ def main():
     ap.add_argument("--all", action="store_true", help="also print lines for configs 1, 4, 5")
     ap.add_argument("--probe", action="store_true",
                     help="counter-collection run: a 1 GiB device copy (calibrates FETCH_SIZE/"
-                         "WRITE_SIZE), 3 config-2 prefills, 8 config-3 decode steps and 6 "
-                         "config-5b cross-attention calls")
+                         "WRITE_SIZE), 3 config-2 prefills, 8 config-3 decode steps, 6 "
+                         "config-5b cross-attention calls and 6 decode layer steps")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
@@ -291,6 +352,8 @@ def main():
                                       "host_paced = issued from Python one by one"})
                 del kvs
             del q, k, v, o
+        print("bench: config3 decode layer step", file=sys.stderr, flush=True)
+        extra.append(bench_decode_layer(nne, torch, dev))
         line["other_configs"] = extra
     if not args.no_cpu:
         print("bench: cpu baseline", file=sys.stderr, flush=True)
