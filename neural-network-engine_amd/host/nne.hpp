@@ -13,6 +13,9 @@
 //   KVCache new / reset / num_layers / current_seq_len / update
 //                                      src/nn/kv_cache.rs:11-74
 //   EngineError / Result<T>            src/error.rs:6-58
+//   RotaryEmbedding new / apply        src/models/llama.rs:64-158
+//   GroupedQueryAttention new / forward_gqa_cached / forward_gqa
+//                                      src/models/llama.rs:160-301
 //
 // Differences that come from the hardware, not from taste:
 //   * RawTensor data live in device memory (HBM); to_vec() copies to the host.
@@ -196,6 +199,7 @@ class KVCache {
     RawTensor k(size_t layer_idx) const;                 // full [B, Hkv, capacity, d]
     RawTensor v(size_t layer_idx) const;
     const std::vector<int32_t>& lengths(size_t layer_idx) const;
+    const int32_t* lengths_device(size_t layer_idx) const;   // the same lengths on the device
 
     size_t batch, num_kv_heads, capacity, head_dim;
 
@@ -211,6 +215,52 @@ class KVCache {
     std::vector<Layer> layers_;
     std::shared_ptr<void> ws_;
     uint64_t ws_bytes_ = 0;
+};
+
+// src/models/llama.rs:64-158.  Tables are built on the host in f32 exactly as
+// the reference builds them and kept on the device.
+class RotaryEmbedding {
+  public:
+    // Throws std::invalid_argument for an odd head_dim (the reference asserts, :75).
+    RotaryEmbedding(size_t head_dim, size_t max_seq_len, float theta);
+    // :110-157: x [B, H, T, D] (any strides) -> new contiguous tensor, row t of
+    // every sequence rotated at position start_pos + t.
+    Result<RawTensor> apply(const RawTensor& x, size_t start_pos) const;
+    // Per-sequence start positions (ragged caches).
+    Result<RawTensor> apply(const RawTensor& x, const std::vector<int32_t>& start_pos) const;
+
+    RawTensor cos_cached, sin_cached;                    // [1, 1, max_seq_len, head_dim]
+    size_t head_dim, max_seq_len;
+};
+
+// src/models/llama.rs:160-300, forward only.  Decode steps (t = 1 with a cache)
+// run the fused projection + RoPE launch on weights packed at construction and
+// the append + attend launch; other inputs project with GEMMs, rotate, append
+// and run the attention kernel with q_offset = start_pos.
+class GroupedQueryAttention {
+  public:
+    // Throws std::invalid_argument unless num_heads divides d_model and
+    // num_kv_heads divides num_heads (the reference asserts, :174-183).
+    GroupedQueryAttention(size_t d_model, size_t num_heads, size_t num_kv_heads, size_t max_seq_len,
+                          float rope_theta = 10000.f);
+    // :205-296.  x [B, T, C].  With a cache, start_pos must equal the cached
+    // length of every sequence of the layer (the reference's start_pos is the
+    // cache length, :525).
+    Result<RawTensor> forward_gqa_cached(const RawTensor& x, size_t start_pos, KVCache* cache = nullptr,
+                                         size_t layer_idx = 0);
+    Result<RawTensor> forward_gqa(const RawTensor& x, size_t start_pos) {   // :298-301
+        return forward_gqa_cached(x, start_pos, nullptr);
+    }
+    // Re-packs q/k/v_proj weights for the fused decode projection; call after
+    // changing them.
+    void repack();
+
+    Linear q_proj, k_proj, v_proj, o_proj;
+    RotaryEmbedding rope;
+    size_t num_heads, num_kv_heads, head_dim, num_queries_per_kv;
+
+  private:
+    std::shared_ptr<float> w_packed_;                    // null when d or d_model is not a multiple of 64
 };
 
 }  // namespace nne

@@ -492,6 +492,8 @@ RawTensor KVCache::v(size_t layer_idx) const {
 
 const std::vector<int32_t>& KVCache::lengths(size_t layer_idx) const { return layers_.at(layer_idx).lens_host; }
 
+const int32_t* KVCache::lengths_device(size_t layer_idx) const { return layers_.at(layer_idx).lens_dev.get(); }
+
 Result<std::pair<RawTensor, RawTensor>> KVCache::update(size_t layer_idx, const RawTensor& k_new,
                                                        const RawTensor& v_new) {
     auto ok = check_layer(layer_idx);
@@ -575,6 +577,168 @@ Result<bool> KVCache::set_lengths(size_t layer_idx, const std::vector<int32_t>& 
     if (batch && nne_memcpy_h2d(l.lens_dev.get(), lens.data(), batch * 4, nullptr) != NNE_OK)
         return from_status(NNE_EHIP);
     return true;
+}
+
+// ---- RotaryEmbedding ------------------------------------------------------------
+
+namespace {
+
+size_t even_head_dim(size_t head_dim) {   // llama.rs:75
+    if (head_dim % 2 != 0)
+        throw std::invalid_argument("RoPE head_dim (" + std::to_string(head_dim) + ") must be even");
+    return head_dim;
+}
+
+}  // namespace
+
+RotaryEmbedding::RotaryEmbedding(size_t head_dim_, size_t max_seq_len_, float theta)
+    : head_dim(even_head_dim(head_dim_)), max_seq_len(max_seq_len_) {
+    std::vector<float> c(max_seq_len * head_dim), s(max_seq_len * head_dim);
+    const int rc = nne_rope_tables(c.data(), s.data(), (int64_t)max_seq_len, (int64_t)head_dim, theta);
+    if (rc != NNE_OK) throw std::invalid_argument(from_status(rc).to_string());
+    cos_cached = RawTensor::from_vec(c, {1, 1, max_seq_len, head_dim});
+    sin_cached = RawTensor::from_vec(s, {1, 1, max_seq_len, head_dim});
+}
+
+Result<RawTensor> RotaryEmbedding::apply(const RawTensor& x, size_t start_pos) const {
+    const size_t b = x.ndim() == 4 ? x.shape()[0] : 0;
+    return apply(x, std::vector<int32_t>(b, (int32_t)std::min<size_t>(start_pos, INT32_MAX)));
+}
+
+Result<RawTensor> RotaryEmbedding::apply(const RawTensor& x, const std::vector<int32_t>& start_pos) const {
+    if (x.ndim() != 4)                                               // llama.rs:111-118
+        return EngineError::invalid_argument("RoPE apply expects 4D tensor [Batch, Heads, SeqLen, HeadDim], got "
+                                             "rank " + std::to_string(x.ndim()) + " with shape " + dims(x.shape()));
+    if (x.shape()[3] != head_dim) return EngineError::shape_mismatch({head_dim}, {x.shape()[3]});   // :119-124
+    if (start_pos.size() != x.shape()[0]) return EngineError::shape_mismatch({x.shape()[0]}, {start_pos.size()});
+    RawTensor out = RawTensor::zeros(x.shape());
+    auto pos_dev = device_alloc<int32_t>(start_pos.size());
+    if (!start_pos.empty() && nne_memcpy_h2d(pos_dev.get(), start_pos.data(), start_pos.size() * 4, nullptr) != NNE_OK)
+        return from_status(NNE_EHIP);
+    const auto shape = as_i64(x.shape()), xst = as_i64(x.strides()), ost = as_i64(out.strides());
+    const int rc = nne_rope_apply(x.data(), shape.data(), xst.data(), out.data(), ost.data(), cos_cached.data(),
+                                  sin_cached.data(), (int64_t)max_seq_len, (int64_t)head_dim, pos_dev.get(),
+                                  start_pos.data(), nullptr);
+    if (rc != NNE_OK) return from_status(rc);
+    if (nne_stream_sync(nullptr) != NNE_OK) return from_status(NNE_EHIP);   // pos_dev is freed on return
+    return out;
+}
+
+// ---- GroupedQueryAttention --------------------------------------------------------
+
+namespace {
+
+size_t gqa_head_dim(size_t d_model, size_t num_heads, size_t num_kv_heads) {   // llama.rs:174-183
+    if (num_heads == 0 || d_model % num_heads != 0)
+        throw std::invalid_argument("d_model must be divisible by num_heads");
+    if (num_kv_heads == 0 || num_heads % num_kv_heads != 0)
+        throw std::invalid_argument("num_heads must be divisible by num_kv_heads for GQA");
+    return d_model / num_heads;
+}
+
+}  // namespace
+
+GroupedQueryAttention::GroupedQueryAttention(size_t d_model, size_t num_heads_, size_t num_kv_heads_,
+                                             size_t max_seq_len, float rope_theta)
+    : q_proj(Linear::without_bias(d_model, gqa_head_dim(d_model, num_heads_, num_kv_heads_) * num_heads_)),
+      k_proj(Linear::without_bias(d_model, num_kv_heads_ * (d_model / num_heads_))),
+      v_proj(Linear::without_bias(d_model, num_kv_heads_ * (d_model / num_heads_))),
+      o_proj(Linear::without_bias(d_model, d_model)),
+      rope(d_model / num_heads_, max_seq_len, rope_theta),
+      num_heads(num_heads_), num_kv_heads(num_kv_heads_), head_dim(d_model / num_heads_),
+      num_queries_per_kv(num_heads_ / num_kv_heads_) {
+    repack();
+}
+
+void GroupedQueryAttention::repack() {
+    const int64_t c = (int64_t)q_proj.in_features;
+    const uint64_t bytes = nne_qkv_packed_bytes(c, (int64_t)num_heads, (int64_t)num_kv_heads, (int64_t)head_dim);
+    if (bytes == 0) {
+        w_packed_.reset();
+        return;
+    }
+    w_packed_ = device_alloc<float>(bytes / 4);
+    const int rc = nne_qkv_pack(q_proj.weight.data(), k_proj.weight.data(), v_proj.weight.data(), w_packed_.get(), c,
+                                (int64_t)num_heads, (int64_t)num_kv_heads, (int64_t)head_dim, nullptr);
+    if (rc != NNE_OK) throw std::runtime_error(from_status(rc).to_string());
+}
+
+Result<RawTensor> GroupedQueryAttention::forward_gqa_cached(const RawTensor& x, size_t start_pos, KVCache* cache,
+                                                            size_t layer_idx) {
+    if (x.ndim() != 3)                                               // llama.rs:211-217
+        return EngineError::incompatible_shapes("GroupedQueryAttention forward (expected 3D input [B, T, C])",
+                                                {x.shape()});
+    const size_t b = x.shape()[0], t = x.shape()[1], c = x.shape()[2];
+    const size_t hq = num_heads, hkv = num_kv_heads, d = head_dim;
+    if (c != q_proj.in_features)
+        return EngineError::incompatible_shapes("matmul_transposed_b", {x.shape(), q_proj.weight.shape()});
+    if (cache) {
+        if (layer_idx >= cache->num_layers())
+            return EngineError::invalid_argument("KVCache layer index " + std::to_string(layer_idx) +
+                                                 " out of range (total layers: " +
+                                                 std::to_string(cache->num_layers()) + ")");
+        if (cache->batch != b || cache->num_kv_heads != hkv || cache->head_dim != d)
+            return EngineError::shape_mismatch({b, hkv, cache->capacity, d},
+                                               {cache->batch, cache->num_kv_heads, cache->capacity, cache->head_dim});
+        for (int32_t L : cache->lengths(layer_idx))
+            if ((size_t)L != start_pos)
+                return EngineError::invalid_argument("start_pos " + std::to_string(start_pos) +
+                                                     " differs from a cached length " + std::to_string(L));
+    }
+    if (cache && t == 1 && w_packed_) {
+        // Decode step: fused projection + RoPE, then append + attend (llama.rs:226-296, t = 1).
+        RawTensor xc = x.to_contiguous();
+        RawTensor q = RawTensor::zeros({b, hq, 1, d}), k_new = RawTensor::zeros({b, hkv, 1, d}),
+                  v_new = RawTensor::zeros({b, hkv, 1, d});
+        const int rc = nne_qkv_rope(xc.data(), (int64_t)c, w_packed_.get(), nullptr, nullptr, nullptr,
+                                    rope.cos_cached.data(), rope.sin_cached.data(), (int64_t)rope.max_seq_len,
+                                    (int64_t)rope.head_dim, cache->lengths_device(layer_idx),
+                                    cache->lengths(layer_idx).data(), q.data(), k_new.data(), v_new.data(),
+                                    (int64_t)b, (int64_t)c, (int64_t)hq, (int64_t)hkv, (int64_t)d, nullptr);
+        if (rc != NNE_OK) return from_status(rc);
+        auto ctx = cache->decode_step(layer_idx, q, k_new, v_new);
+        if (ctx.is_err()) return ctx.error();
+        auto merged = ctx.value().reshape({b, 1, hq * d});          // [B, Hq, 1, d] is [B, 1, Hq * d]
+        if (merged.is_err()) return merged.error();
+        return o_proj.forward(merged.value());
+    }
+    // 1. projections, [B, T, H, d] -> [B, H, T, d] views (llama.rs:222-233)
+    auto qp = q_proj.forward(x);
+    if (qp.is_err()) return qp.error();
+    auto kp = k_proj.forward(x);
+    if (kp.is_err()) return kp.error();
+    auto vp = v_proj.forward(x);
+    if (vp.is_err()) return vp.error();
+    auto heads = [&](const RawTensor& y, size_t h) {
+        return y.reshape({b, t, h, d}).value().transpose(1, 2).value();
+    };
+    // 2. RoPE (:235-236)
+    auto q = rope.apply(heads(qp.value(), hq), start_pos);
+    if (q.is_err()) return q.error();
+    auto k = rope.apply(heads(kp.value(), hkv), start_pos);
+    if (k.is_err()) return k.error();
+    RawTensor v = heads(vp.value(), hkv);
+    // 3. cache append (:238-251)
+    RawTensor k_all = k.value(), v_all = v;
+    if (cache) {
+        auto kv = cache->update(layer_idx, k.value(), v);
+        if (kv.is_err()) return kv.error();
+        k_all = kv.value().first;
+        v_all = kv.value().second;
+    }
+    // 4-7. attention with the causal mask of :277-292 for t > 1, written
+    // straight into [B, T, H, d] = [B, T, C]
+    RawTensor merged = RawTensor::zeros({b, t, hq * d});
+    const std::vector<int64_t> qs = as_i64(q.value().shape()), qst = as_i64(q.value().strides());
+    const std::vector<int64_t> ks = as_i64(k_all.shape()), kst = as_i64(k_all.strides());
+    const std::vector<int64_t> vs = as_i64(v_all.shape()), vst = as_i64(v_all.strides());
+    const std::vector<int64_t> ost{(int64_t)(t * hq * d), (int64_t)d, (int64_t)(hq * d), 1};
+    const int rc = nne_attention_forward(q.value().data(), qs.data(), qst.data(), k_all.data(), ks.data(),
+                                         kst.data(), v_all.data(), vs.data(), vst.data(), merged.data(), ost.data(),
+                                         t > 1 ? 1 : 0, (int64_t)start_pos, 0, 0.f, nullptr);
+    if (rc != NNE_OK) return from_status(rc);
+    // 8. output projection (:298)
+    return o_proj.forward(merged);
 }
 
 }  // namespace nne

@@ -28,6 +28,14 @@ void oracle_flash_forward(const float* q, const float* k, const float* v, float*
 void oracle_standard_attention(const float* q, const float* k, const float* v, float* out, int64_t b,
                                int64_t hq, int64_t hkv, int64_t tq, int64_t tk, int64_t d, int masked,
                                int64_t start_pos, int has_scale, float scale, int n_threads);
+void oracle_rope_tables(float* cos_out, float* sin_out, int64_t max_seq_len, int64_t d, float theta);
+void oracle_rope_apply(const float* x, float* out, const float* cos_t, const float* sin_t, int64_t b, int64_t h,
+                       int64_t t, int64_t d, const int32_t* start_pos);
+void oracle_linear(const float* x, const float* w, const float* bias, float* y, int64_t m, int64_t k, int64_t n);
+void oracle_qkv_rope(const float* x, const float* wq, const float* wk, const float* wv, const float* bq,
+                     const float* bk, const float* bv, const float* cos_t, const float* sin_t,
+                     const int32_t* start_pos, float* q_out, float* k_out, float* v_out, int64_t b, int64_t t,
+                     int64_t c, int64_t hq, int64_t hkv, int64_t d);
 }
 
 using namespace nne;
@@ -235,6 +243,108 @@ TEST_GPU(test_gqa_attention_matches_standard) {
                 "GQA causal, q_offset 20");
     check_close(attention_forward(q, k, v, false).unwrap().to_vec(), standard_attention(q, k, v, false),
                 "GQA non-causal");
+}
+
+// ---- RoPE and GroupedQueryAttention (src/models/llama.rs:64-301) -------------
+
+TEST_GPU(test_rope_matches_reference_tables_and_rotation) {
+    const size_t d = 64, n = 128;
+    RotaryEmbedding rope(d, n, 10000.f);
+    std::vector<float> c(n * d), s(n * d);
+    oracle_rope_tables(c.data(), s.data(), n, d, 10000.f);
+    CHECK(rope.cos_cached.to_vec() == c && rope.sin_cached.to_vec() == s);   // bit-identical tables
+    CHECK(rope.cos_cached.shape() == std::vector<size_t>({1, 1, n, d}));
+    manual_seed(11);
+    RawTensor x = RawTensor::randn({2, 5, 9, 64}, 0.f, 1.f);
+    auto y = rope.apply(x.transpose(1, 2).unwrap(), 17).unwrap();             // strided [B, H, T, D] view
+    const auto xt = x.transpose(1, 2).unwrap().to_contiguous().to_vec();
+    std::vector<float> ref(xt.size());
+    const std::vector<int32_t> sp{17, 17};
+    oracle_rope_apply(xt.data(), ref.data(), c.data(), s.data(), 2, 9, 5, 64, sp.data());
+    CHECK(y.to_vec() == ref);                                                 // bit-identical rotation
+    auto bad = rope.apply(x, 125);                                            // [125, 134) > 128 (:131-139)
+    CHECK(bad.is_err() && bad.error().to_string() ==
+                              "Invalid configuration or argument: Sequence range [125, 134) exceeds RoPE "
+                              "max_seq_len 128");
+    RotaryEmbedding small(32, 8, 10000.f);
+    auto mism = small.apply(x, 0);                                            // :119-124
+    CHECK(mism.is_err() && mism.error() == EngineError::shape_mismatch({32}, {64}));
+}
+
+TEST_GPU(test_gqa_layer_decode_matches_oracle) {
+    // forward_gqa_cached: prefill of t tokens, then decode steps through the
+    // fused projection + RoPE launch; every output equals the oracle's layer.
+    const size_t b = 2, c = 256, hq = 4, hkv = 2, d = 64, t = 7, steps = 3;
+    manual_seed(12);
+    GroupedQueryAttention layer(c, hq, hkv, 64);
+    const auto wq = layer.q_proj.weight.to_vec(), wk = layer.k_proj.weight.to_vec(),
+               wv = layer.v_proj.weight.to_vec(), wo = layer.o_proj.weight.to_vec();
+    const auto cs = layer.rope.cos_cached.to_vec(), sn = layer.rope.sin_cached.to_vec();
+    RawTensor x = RawTensor::randn({b, t + steps, c}, 0.f, 1.f);
+    const auto xh = x.to_vec();
+    KVCache cache(1, b, hkv, 64, d);
+    // oracle cache (contiguous [B, Hkv, L, d] rebuilt per step)
+    std::vector<float> kall, vall;
+    for (size_t s = 0; s <= steps; ++s) {
+        const size_t start = s == 0 ? 0 : t + s - 1, tt = s == 0 ? t : 1;
+        RawTensor xs = x.slice(1, start, start + tt).unwrap();
+        const auto y = layer.forward_gqa_cached(xs, start, &cache, 0).unwrap().to_vec();
+        // oracle
+        const auto xsv = xs.to_contiguous().to_vec();
+        std::vector<float> q(b * hq * tt * d), k(b * hkv * tt * d), v(b * hkv * tt * d);
+        const std::vector<int32_t> sp(b, (int32_t)start);
+        oracle_qkv_rope(xsv.data(), wq.data(), wk.data(), wv.data(), nullptr, nullptr, nullptr, cs.data(), sn.data(),
+                        sp.data(), q.data(), k.data(), v.data(), b, tt, c, hq, hkv, d);
+        const size_t L = start + tt;
+        std::vector<float> kn(b * hkv * L * d), vn(b * hkv * L * d);
+        for (size_t bi = 0; bi < b; ++bi)
+            for (size_t h = 0; h < hkv; ++h)
+                for (size_t r = 0; r < L; ++r)
+                    for (size_t e = 0; e < d; ++e) {
+                        const size_t dst = ((bi * hkv + h) * L + r) * d + e;
+                        if (r < start) {
+                            kn[dst] = kall[((bi * hkv + h) * start + r) * d + e];
+                            vn[dst] = vall[((bi * hkv + h) * start + r) * d + e];
+                        } else {
+                            kn[dst] = k[((bi * hkv + h) * tt + (r - start)) * d + e];
+                            vn[dst] = v[((bi * hkv + h) * tt + (r - start)) * d + e];
+                        }
+                    }
+        kall = kn;
+        vall = vn;
+        std::vector<float> ctx(b * hq * tt * d);
+        oracle_standard_attention(q.data(), kall.data(), vall.data(), ctx.data(), b, hq, hkv, tt, L, d, tt > 1 ? 1 : 0,
+                                  (int64_t)start, 0, 0.f, 8);
+        std::vector<float> merged(b * tt * hq * d);                          // [B, H, T, d] -> [B, T, H*d]
+        for (size_t bi = 0; bi < b; ++bi)
+            for (size_t h = 0; h < hq; ++h)
+                for (size_t r = 0; r < tt; ++r)
+                    for (size_t e = 0; e < d; ++e)
+                        merged[((bi * tt + r) * hq + h) * d + e] = ctx[((bi * hq + h) * tt + r) * d + e];
+        std::vector<float> ref(b * tt * c);
+        oracle_linear(merged.data(), wo.data(), nullptr, ref.data(), b * tt, c, c);
+        check_close(y, ref, s == 0 ? "gqa prefill" : "gqa decode step");
+    }
+    CHECK(cache.current_seq_len(0) == t + steps);
+    auto r = layer.forward_gqa_cached(x.slice(1, 0, 1).unwrap(), 3, &cache, 0);   // start_pos != cached length
+    CHECK(r.is_err() && r.error().kind == EngineError::Kind::InvalidArgument);
+}
+
+TEST_CPU(test_gqa_rejects_bad_head_counts) {                             // llama.rs:174-183
+    bool threw = false;
+    try {
+        GroupedQueryAttention layer(64, 4, 3, 16);
+    } catch (const std::invalid_argument& e) {
+        threw = std::string(e.what()) == "num_heads must be divisible by num_kv_heads for GQA";
+    }
+    CHECK(threw);
+    threw = false;
+    try {
+        RotaryEmbedding rope(7, 16, 10000.f);
+    } catch (const std::invalid_argument& e) {
+        threw = std::string(e.what()) == "RoPE head_dim (7) must be even";
+    }
+    CHECK(threw);
 }
 
 // ---- errors (src/error.rs) ---------------------------------------------------
