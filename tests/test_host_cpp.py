@@ -23,10 +23,11 @@ def run(args, timeout):
 
 
 def test_host_api_cpu_only_parts():
-    """Error variants and messages (src/error.rs), Result, layer argument checks."""
+    """Error variants and messages (src/error.rs), Result, layer and RoPE
+    argument checks."""
     res = run(["--cpu"], 60)
     assert res.returncode == 0, res.stdout
-    assert re.search(r"^0 of 2 tests failed$", res.stdout, re.M)
+    assert re.search(r"^0 of 3 tests failed$", res.stdout, re.M)
 
 
 @pytest.mark.gpu
