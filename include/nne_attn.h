@@ -185,7 +185,10 @@ int nne_qkv_pack(const float *wq, const float *wk, const float *wv, float *packe
  * library's per-stream workspace and counters (as nne_decode_attention).
  * Requires d % 64 == 0, C % 64 == 0, x rows 16-byte aligned with
  * x_row_stride >= C and a multiple of 4.  NNE_ESHAPE if d != table_head_dim;
- * NNE_EINVAL if pos[b] >= max_seq_len. */
+ * NNE_EINVAL if pos[b] >= max_seq_len.  With cos_table = sin_table = NULL
+ * nothing is rotated and positions are not read: the q/k/v projections of
+ * MultiHeadAttention::forward_attention_cached (src/nn/attention.rs:66-75,
+ * with biases, as GPT-2 and Whisper use it). */
 int nne_qkv_rope(const float *x, int64_t x_row_stride, const float *w_packed, const float *bq,
                  const float *bk, const float *bv, const float *cos_table, const float *sin_table,
                  int64_t max_seq_len, int64_t table_head_dim, const int32_t *pos_dev,

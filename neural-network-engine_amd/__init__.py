@@ -16,6 +16,8 @@ engine's attention API (elvin-mark/neural-network-engine):
 * ``qkv_rope`` -- the fused decode prologue (q/k/v projections + RoPE) of
   GroupedQueryAttention::forward_gqa_cached (llama.rs:226-235)
 * ``GroupedQueryAttention`` -- src/models/llama.rs:160-300
+* ``MultiHeadAttention`` -- src/nn/attention.rs:9-210 (GPT-2 / Whisper self- and
+  cross-attention) and ``WhisperKVCache`` -- src/models/whisper.rs:325-350
 
 Tensors are torch tensors on the GPU (torch is used only for device memory and
 streams).  Errors raise the EngineError variant the reference would return.
@@ -419,16 +421,17 @@ def qkv_pack(wq, wk, wv, num_heads, num_kv_heads, stream=None):
 
 
 def qkv_rope(x, w_packed, bq, bk, bv, rope, pos_dev, pos_host, num_heads, num_kv_heads,
-             q_out=None, k_out=None, v_out=None, stream=None):
+             q_out=None, k_out=None, v_out=None, stream=None, head_dim=None):
     """Fused decode prologue: x [B, C] (or [B, 1, C]) -> q [B, Hq, 1, d] and
     k, v [B, Hkv, 1, d] with q = RoPE(x Wq^T + bq), k = RoPE(x Wk^T + bk),
     v = x Wv^T + bv at positions pos (int32, device and host copies);
-    ``w_packed`` comes from ``qkv_pack``."""
+    ``w_packed`` comes from ``qkv_pack``.  With rope=None nothing is rotated
+    (the MultiHeadAttention projections) and ``head_dim`` gives d."""
     import torch
     x2 = x.reshape(x.shape[0], x.shape[-1]) if x.dim() == 3 else x
     _require_f32_cuda(x2, w_packed)
     b, c = x2.shape
-    d = rope.head_dim
+    d = rope.head_dim if rope is not None else int(head_dim)
     dev = x2.device
     if q_out is None:
         q_out = torch.empty((b, num_heads, 1, d), dtype=torch.float32, device=dev)
@@ -436,19 +439,22 @@ def qkv_rope(x, w_packed, bq, bk, bv, rope, pos_dev, pos_host, num_heads, num_kv
         k_out = torch.empty((b, num_kv_heads, 1, d), dtype=torch.float32, device=dev)
     if v_out is None:
         v_out = torch.empty((b, num_kv_heads, 1, d), dtype=torch.float32, device=dev)
-    pos_host = np.ascontiguousarray(pos_host, dtype=np.int32)
-
     def ptr(t):
         return None if t is None else t.data_ptr()
 
     for t in (q_out, k_out, v_out):
         if not t.is_contiguous():
             raise InvalidArgument("Invalid configuration or argument: outputs must be contiguous")
+    if rope is not None:
+        pos_host = np.ascontiguousarray(pos_host, dtype=np.int32)
+        tables = (rope.cos.data_ptr(), rope.sin.data_ptr(), rope.max_seq_len, rope.head_dim,
+                  pos_dev.data_ptr(), pos_host.ctypes.data_as(_i32p))
+    else:
+        tables = (None, None, 0, d, None, None)
     check(lib().nne_qkv_rope(
-        x2.data_ptr(), x2.stride(0), w_packed.data_ptr(), ptr(bq), ptr(bk), ptr(bv),
-        rope.cos.data_ptr(), rope.sin.data_ptr(), rope.max_seq_len, rope.head_dim,
-        pos_dev.data_ptr(), pos_host.ctypes.data_as(_i32p), q_out.data_ptr(), k_out.data_ptr(),
-        v_out.data_ptr(), b, c, num_heads, num_kv_heads, d, _stream(stream)))
+        x2.data_ptr(), x2.stride(0), w_packed.data_ptr(), ptr(bq), ptr(bk), ptr(bv), *tables,
+        q_out.data_ptr(), k_out.data_ptr(), v_out.data_ptr(), b, c, num_heads, num_kv_heads, d,
+        _stream(stream)))
     return q_out, k_out, v_out
 
 
@@ -522,3 +528,122 @@ class GroupedQueryAttention:
         attention_forward(q, k_all, v_all, t > 1, q_offset=int(sp[0]) if b else 0,
                           out=out.transpose(1, 2), stream=stream)
         return torch.nn.functional.linear(out.view(b, t, hq * d), self.wo)
+
+
+class MultiHeadAttention:
+    """MultiHeadAttention (src/nn/attention.rs:9-210), forward only: biased
+    q/k/v/out projections (Linear::new), causal self-attention with an
+    optional KV cache and cross-attention whose projected memory K/V are
+    cached once.
+
+    Self-attention decode steps (T = 1 with a cache, head dim and d_model
+    multiples of 64) run the fused projection launch (no RoPE) and the fused
+    append + attend launch; other inputs project with GEMMs, append, and run
+    the attention kernel with the reference's bottom-right mask
+    (q_offset = L - T, attention.rs:101-108)."""
+
+    def __init__(self, d_model, num_heads, is_causal, device="cuda", seed=0):
+        import torch
+        if d_model % num_heads != 0:
+            raise InvalidArgument("d_model (%d) must be divisible by num_heads (%d)"
+                                  % (d_model, num_heads))
+        self.d_model, self.num_heads = d_model, num_heads
+        self.head_dim = d_model // num_heads
+        self.is_causal = is_causal
+        g = torch.Generator(device="cpu").manual_seed(seed)
+
+        def lin():   # Linear::new: Kaiming-uniform weight, U(-1/sqrt(in), 1/sqrt(in)) bias
+            w = (torch.rand(d_model, d_model, generator=g) * 2 - 1) * math.sqrt(6.0 / d_model)
+            bb = (torch.rand(d_model, generator=g) * 2 - 1) / math.sqrt(d_model)
+            return w.to(device), bb.to(device)
+
+        self.q_proj, self.k_proj, self.v_proj, self.out_proj = lin(), lin(), lin(), lin()
+        self.w_packed = None
+        if self.head_dim % 64 == 0 and d_model % 64 == 0:
+            self.w_packed = qkv_pack(self.q_proj[0], self.k_proj[0], self.v_proj[0], num_heads,
+                                     num_heads)
+
+    def _heads(self, y, b, t):
+        return y.view(b, t, self.num_heads, self.head_dim).transpose(1, 2)
+
+    def forward_attention(self, x, stream=None):
+        return self.forward_attention_cached(x, None, stream=stream)
+
+    def forward_attention_cached(self, x, cache=None, layer_idx=0, stream=None):
+        """x [B, T, C]; cache a KVCache whose layer ``layer_idx`` holds this
+        layer's self-attention rows (attention.rs:78-91)."""
+        import torch
+        if x.dim() != 3:
+            raise EngineError("Incompatible shapes for operation MultiHeadAttention forward "
+                              "(expected 3D input [B, T, C]): %s" % [list(x.shape)])
+        b, t, c = x.shape
+        h, d = self.num_heads, self.head_dim
+        if cache is not None:
+            cache._check_layer(layer_idx)
+        if cache is not None and t == 1 and self.w_packed is not None:
+            q, k_new, v_new = qkv_rope(x, self.w_packed, self.q_proj[1], self.k_proj[1],
+                                       self.v_proj[1], None, None, None, h, h, stream=stream,
+                                       head_dim=d)
+            ctx = cache.decode_step(layer_idx, q, k_new, v_new, stream=stream)
+            return torch.nn.functional.linear(ctx.view(b, 1, c), *self.out_proj)
+        q = self._heads(torch.nn.functional.linear(x, *self.q_proj), b, t)
+        k = self._heads(torch.nn.functional.linear(x, *self.k_proj), b, t)
+        v = self._heads(torch.nn.functional.linear(x, *self.v_proj), b, t)
+        if cache is not None:
+            lens = cache.lens_host[layer_idx]
+            if t > 1 and b > 1 and not (lens == lens[0]).all():
+                raise InvalidArgument("Invalid configuration or argument: multi-token steps need "
+                                      "equal cached lengths")
+            k_all, v_all = cache.update(layer_idx, k.contiguous(), v.contiguous(), stream=stream)
+            total = int(cache.lens_host[layer_idx][0]) if b else 0
+        else:
+            k_all, v_all, total = k, v, t
+        out = torch.empty((b, t, h, d), dtype=torch.float32, device=x.device)
+        attention_forward(q, k_all, v_all, self.is_causal and t > 1, q_offset=max(total - t, 0),
+                          out=out.transpose(1, 2), stream=stream)
+        return torch.nn.functional.linear(out.view(b, t, c), *self.out_proj)
+
+    def forward_cross_attention(self, x, memory, stream=None):
+        return self.forward_cross_attention_cached(x, memory, None, stream=stream)
+
+    def forward_cross_attention_cached(self, x, memory, slots=None, layer_idx=0, stream=None):
+        """Queries from x [B, T_q, C], keys/values from memory [B, T_kv, C];
+        with ``slots`` (e.g. WhisperKVCache.cross_attn) the projected memory
+        K/V [B, H, T_kv, d] are computed once and reused (attention.rs:139-191)."""
+        import torch
+        if x.dim() != 3 or memory.dim() != 3:
+            raise EngineError("Incompatible shapes for operation MultiHeadAttention cross-attention "
+                              "(expected 3D query [B, T_q, C] and 3D memory [B, T_kv, C]): %s"
+                              % [list(x.shape), list(memory.shape)])
+        if x.shape[0] != memory.shape[0] or x.shape[2] != memory.shape[2]:
+            raise EngineError("Incompatible shapes for operation MultiHeadAttention cross-attention "
+                              "(batch size and channel dim must match): %s"
+                              % [list(x.shape), list(memory.shape)])
+        b, tq, c = x.shape
+        tkv = memory.shape[1]
+        h, d = self.num_heads, self.head_dim
+        q = self._heads(torch.nn.functional.linear(x, *self.q_proj), b, tq)
+        kv = slots[layer_idx] if slots is not None else None
+        if kv is None:
+            k = self._heads(torch.nn.functional.linear(memory, *self.k_proj), b, tkv).contiguous()
+            v = self._heads(torch.nn.functional.linear(memory, *self.v_proj), b, tkv).contiguous()
+            kv = (k, v)
+            if slots is not None:
+                slots[layer_idx] = kv
+        out = torch.empty((b, tq, h, d), dtype=torch.float32, device=x.device)
+        attention_forward(q, kv[0], kv[1], False, out=out.transpose(1, 2), stream=stream)
+        return torch.nn.functional.linear(out.view(b, tq, c), *self.out_proj)
+
+
+class WhisperKVCache:
+    """WhisperKVCache (src/models/whisper.rs:325-350): per decoder layer a
+    self-attention cache (a device KVCache layer) and a cross-attention slot
+    holding the projected encoder memory K/V (None until the first step)."""
+
+    def __init__(self, num_layers, batch, num_heads, capacity, head_dim, device="cuda"):
+        self.self_attn = KVCache(num_layers, batch, num_heads, capacity, head_dim, device=device)
+        self.cross_attn = [None] * num_layers
+
+    def reset(self):
+        self.self_attn.reset()
+        self.cross_attn = [None] * len(self.cross_attn)

@@ -634,15 +634,18 @@ int nne_qkv_rope(const float* x, int64_t x_row_stride, const float* w_packed, co
                  int64_t C, int64_t Hq, int64_t Hkv, int64_t d, void* stream) {
     if (B < 0 || B > INT32_MAX)
         return fail(NNE_EINVAL, "Invalid configuration or argument: batch %lld", (long long)B);
-    if (d != table_head_dim)   // llama.rs:119-124
+    const bool rope = cos_table || sin_table;
+    if (rope && d != table_head_dim)   // llama.rs:119-124
         return fail(NNE_ESHAPE, "Shape mismatch error: expected shape [%lld], got [%lld]",
                     (long long)table_head_dim, (long long)d);
     int rc = check_qkv_geometry(C, Hq, Hkv, d);
     if (rc) return rc;
-    rc = check_rope_range(pos_host, B, 1, max_seq_len);
-    if (rc) return rc;
+    if (rope) {
+        rc = check_rope_range(pos_host, B, 1, max_seq_len);
+        if (rc) return rc;
+    }
     if (B == 0) return NNE_OK;
-    if (!x || !w_packed || !cos_table || !sin_table || !pos_dev || !q_out || !k_out || !v_out)
+    if (!x || !w_packed || !q_out || !k_out || !v_out || (rope && (!cos_table || !sin_table || !pos_dev)))
         return fail(NNE_EINVAL, "Invalid configuration or argument: null tensor pointer");
     if (x_row_stride < C || x_row_stride % 4 != 0 || !aligned16(x) || !aligned16(w_packed))
         return fail(NNE_EINVAL, "Invalid configuration or argument: x rows and packed weights "
@@ -658,9 +661,9 @@ int nne_qkv_rope(const float* x, int64_t x_row_stride, const float* w_packed, co
     p.x_rs = x_row_stride;
     p.wp = w_packed;
     p.bias[0] = bq; p.bias[1] = bk; p.bias[2] = bv;
-    p.cos = cos_table;
-    p.sin = sin_table;
-    p.pos = pos_dev;
+    p.cos = rope ? cos_table : nullptr;
+    p.sin = rope ? sin_table : nullptr;
+    p.pos = rope ? pos_dev : nullptr;
     p.out[0] = q_out; p.out[1] = k_out; p.out[2] = v_out;
     p.o_sb[0] = Hq * d; p.o_sh[0] = d;
     p.o_sb[1] = Hkv * d; p.o_sh[1] = d;

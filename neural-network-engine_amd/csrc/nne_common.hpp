@@ -64,7 +64,8 @@ struct PrefillParams {
 // unit column stride) times the packed q/k/v weights (n_tiles tiles of 64
 // output columns, C split into S slices of kc_per_slice 64-wide chunks), plus
 // bias[j] (j = q, k, v; [H_j * d] or null); q and k rotated at position
-// pos[m] with tables cos/sin [max_seq_len, d]; row m, head h, dim i written to
+// pos[m] with tables cos/sin [max_seq_len, d] (no rotation when cos is null);
+// row m, head h, dim i written to
 // out[j] + m * o_sb[j] + h * o_sh[j] + i.  With S > 1, ws holds the partial
 // tiles ([n_tiles][S][64][64]) and cnt[n_tiles] the zeroed arrival counters.
 struct QkvParams {

@@ -258,7 +258,7 @@ __global__ __launch_bounds__(256, 2) void qkv_rope_kernel(const QkvParams p) {
         const int dim = tile_dim(col, u, half);
         float val = fin[col][m];
         if (bias) val = val + bias[head * p.d + dim];
-        if (which < 2) {
+        if (which < 2 && p.cos) {
             // rotate_half(x) = [-x2, x1] (llama.rs:149-152): columns col and
             // col ^ 32 hold dims i and i + d/2 of one pair.
             const int pc = col ^ 32;
@@ -360,7 +360,7 @@ hipError_t launch_qkv_rope(QkvParams p, hipStream_t stream) {
         QkvParams q = p;
         q.M = std::min(16 * QKV_MAX_MT, M - m0);
         q.x = p.x + (int64_t)m0 * p.x_rs;
-        q.pos = p.pos + m0;
+        q.pos = p.pos ? p.pos + m0 : nullptr;
         for (int j = 0; j < 3; ++j) q.out[j] = p.out[j] + (int64_t)m0 * p.o_sb[j];
         const int mt = (q.M + 15) / 16;
         hipError_t e = mt == 1 ? launch_qkv_mt<1>(q, stream)
