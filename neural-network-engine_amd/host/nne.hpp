@@ -16,6 +16,9 @@
 //   RotaryEmbedding new / apply        src/models/llama.rs:64-158
 //   GroupedQueryAttention new / forward_gqa_cached / forward_gqa
 //                                      src/models/llama.rs:160-301
+//   MultiHeadAttention new / forward_attention(_cached) /
+//     forward_cross_attention(_cached) src/nn/attention.rs:9-210
+//   WhisperKVCache                     src/models/whisper.rs:325-350
 //
 // Differences that come from the hardware, not from taste:
 //   * RawTensor data live in device memory (HBM); to_vec() copies to the host.
@@ -261,6 +264,47 @@ class GroupedQueryAttention {
 
   private:
     std::shared_ptr<float> w_packed_;                    // null when d or d_model is not a multiple of 64
+};
+
+// src/nn/attention.rs:9-210, forward only: biased projections (Linear::new),
+// causal or full self-attention with an optional KV cache (bottom-right mask
+// q_offset = L - T for multi-token steps, :101-108), and cross-attention whose
+// projected memory K/V are computed once into a slot (:139-191).
+class MultiHeadAttention {
+  public:
+    // Throws std::invalid_argument unless num_heads divides d_model (:23-30).
+    MultiHeadAttention(size_t d_model, size_t num_heads, bool is_causal);
+    Result<RawTensor> forward_attention(const RawTensor& x) { return forward_attention_cached(x, nullptr); }
+    // :51-129.  x [B, T, C]; cache layer layer_idx holds this layer's rows.
+    Result<RawTensor> forward_attention_cached(const RawTensor& x, KVCache* cache, size_t layer_idx = 0);
+    // :132-210.  x [B, T_q, C], memory [B, T_kv, C]; slot (if given) caches the
+    // projected memory K/V [B, H, T_kv, d] on its first use.
+    Result<RawTensor> forward_cross_attention(const RawTensor& x, const RawTensor& memory) {
+        return forward_cross_attention_cached(x, memory, nullptr);
+    }
+    Result<RawTensor> forward_cross_attention_cached(const RawTensor& x, const RawTensor& memory,
+                                                     std::optional<std::pair<RawTensor, RawTensor>>* slot);
+    void repack();   // after changing q/k/v_proj weights
+
+    Linear q_proj, k_proj, v_proj, out_proj;
+    size_t num_heads, d_model, head_dim;
+    bool is_causal;
+
+  private:
+    std::shared_ptr<float> w_packed_;
+};
+
+// src/models/whisper.rs:325-350: per decoder layer a self-attention cache and a
+// cross-attention slot (empty until the first decoding step projects memory).
+struct WhisperKVCache {
+    WhisperKVCache(size_t num_layers, size_t batch, size_t num_heads, size_t capacity, size_t head_dim)
+        : self_attn(num_layers, batch, num_heads, capacity, head_dim), cross_attn(num_layers) {}
+    void reset() {                                       // whisper.rs:342-350
+        self_attn.reset();
+        for (auto& s : cross_attn) s.reset();
+    }
+    KVCache self_attn;
+    std::vector<std::optional<std::pair<RawTensor, RawTensor>>> cross_attn;
 };
 
 }  // namespace nne

@@ -741,4 +741,134 @@ Result<RawTensor> GroupedQueryAttention::forward_gqa_cached(const RawTensor& x, 
     return o_proj.forward(merged);
 }
 
+// ---- MultiHeadAttention -----------------------------------------------------------
+
+MultiHeadAttention::MultiHeadAttention(size_t d_model_, size_t num_heads_, bool is_causal_)
+    : q_proj(divisible_d_model(d_model_, num_heads_), d_model_), k_proj(d_model_, d_model_),
+      v_proj(d_model_, d_model_), out_proj(d_model_, d_model_), num_heads(num_heads_), d_model(d_model_),
+      head_dim(d_model_ / num_heads_), is_causal(is_causal_) {
+    repack();
+}
+
+void MultiHeadAttention::repack() {
+    const int64_t c = (int64_t)d_model, h = (int64_t)num_heads;
+    const uint64_t bytes = nne_qkv_packed_bytes(c, h, h, (int64_t)head_dim);
+    if (bytes == 0) {
+        w_packed_.reset();
+        return;
+    }
+    w_packed_ = device_alloc<float>(bytes / 4);
+    const int rc = nne_qkv_pack(q_proj.weight.data(), k_proj.weight.data(), v_proj.weight.data(), w_packed_.get(), c,
+                                h, h, (int64_t)head_dim, nullptr);
+    if (rc != NNE_OK) throw std::runtime_error(from_status(rc).to_string());
+}
+
+namespace {
+
+// Attention of q [B, H, Tq, d] over k/v [B, H, Tk, d] written into [B, Tq, C].
+Result<RawTensor> attend_merged(const RawTensor& q, const RawTensor& k, const RawTensor& v, bool causal,
+                                int64_t q_offset) {
+    const size_t b = q.shape()[0], h = q.shape()[1], t = q.shape()[2], d = q.shape()[3];
+    RawTensor merged = RawTensor::zeros({b, t, h * d});
+    const std::vector<int64_t> qs = as_i64(q.shape()), qst = as_i64(q.strides());
+    const std::vector<int64_t> ks = as_i64(k.shape()), kst = as_i64(k.strides());
+    const std::vector<int64_t> vs = as_i64(v.shape()), vst = as_i64(v.strides());
+    const std::vector<int64_t> ost{(int64_t)(t * h * d), (int64_t)d, (int64_t)(h * d), 1};
+    const int rc = nne_attention_forward(q.data(), qs.data(), qst.data(), k.data(), ks.data(), kst.data(), v.data(),
+                                         vs.data(), vst.data(), merged.data(), ost.data(), causal ? 1 : 0, q_offset,
+                                         0, 0.f, nullptr);
+    if (rc != NNE_OK) return from_status(rc);
+    return merged;
+}
+
+}  // namespace
+
+Result<RawTensor> MultiHeadAttention::forward_attention_cached(const RawTensor& x, KVCache* cache,
+                                                               size_t layer_idx) {
+    if (x.ndim() != 3)                                               // attention.rs:56-62
+        return EngineError::incompatible_shapes("MultiHeadAttention forward (expected 3D input [B, T, C])",
+                                                {x.shape()});
+    const size_t b = x.shape()[0], t = x.shape()[1], c = x.shape()[2], h = num_heads, d = head_dim;
+    if (c != d_model) return EngineError::incompatible_shapes("matmul_transposed_b", {x.shape(), q_proj.weight.shape()});
+    if (cache) {
+        if (layer_idx >= cache->num_layers())
+            return EngineError::invalid_argument("KVCache layer index " + std::to_string(layer_idx) +
+                                                 " out of range (total layers: " +
+                                                 std::to_string(cache->num_layers()) + ")");
+        if (cache->batch != b || cache->num_kv_heads != h || cache->head_dim != d)
+            return EngineError::shape_mismatch({b, h, cache->capacity, d},
+                                               {cache->batch, cache->num_kv_heads, cache->capacity, cache->head_dim});
+    }
+    if (cache && t == 1 && w_packed_) {
+        // Decode step: fused biased projections (no rotation), then append + attend.
+        RawTensor xc = x.to_contiguous();
+        RawTensor q = RawTensor::zeros({b, h, 1, d}), k_new = RawTensor::zeros({b, h, 1, d}),
+                  v_new = RawTensor::zeros({b, h, 1, d});
+        const int rc = nne_qkv_rope(xc.data(), (int64_t)c, w_packed_.get(), q_proj.bias->data(), k_proj.bias->data(),
+                                    v_proj.bias->data(), nullptr, nullptr, 0, (int64_t)d, nullptr, nullptr, q.data(),
+                                    k_new.data(), v_new.data(), (int64_t)b, (int64_t)c, (int64_t)h, (int64_t)h,
+                                    (int64_t)d, nullptr);
+        if (rc != NNE_OK) return from_status(rc);
+        auto ctx = cache->decode_step(layer_idx, q, k_new, v_new);
+        if (ctx.is_err()) return ctx.error();
+        auto merged = ctx.value().reshape({b, 1, c});
+        if (merged.is_err()) return merged.error();
+        return out_proj.forward(merged.value());
+    }
+    auto qp = q_proj.forward(x);                                     // :66-75
+    if (qp.is_err()) return qp.error();
+    auto kp = k_proj.forward(x);
+    if (kp.is_err()) return kp.error();
+    auto vp = v_proj.forward(x);
+    if (vp.is_err()) return vp.error();
+    auto heads = [&](const RawTensor& y) { return y.reshape({b, t, h, d}).value().transpose(1, 2).value(); };
+    RawTensor q = heads(qp.value()), k_all = heads(kp.value()), v_all = heads(vp.value());
+    size_t total = t;
+    if (cache) {                                                     // :78-91
+        const auto& lens = cache->lengths(layer_idx);
+        for (int32_t L : lens)
+            if (t > 1 && L != lens[0])
+                return EngineError::invalid_argument("multi-token steps need equal cached lengths");
+        auto kv = cache->update(layer_idx, k_all, v_all);
+        if (kv.is_err()) return kv.error();
+        k_all = kv.value().first;
+        v_all = kv.value().second;
+        total = b ? (size_t)cache->lengths(layer_idx)[0] : 0;
+    }
+    // :93-122: mask c > (L - T) + r only for causal multi-token steps
+    auto merged = attend_merged(q, k_all, v_all, is_causal && t > 1, (int64_t)(total - t));
+    if (merged.is_err()) return merged.error();
+    return out_proj.forward(merged.value());                         // :124-128
+}
+
+Result<RawTensor> MultiHeadAttention::forward_cross_attention_cached(
+    const RawTensor& x, const RawTensor& memory, std::optional<std::pair<RawTensor, RawTensor>>* slot) {
+    if (x.ndim() != 3 || memory.ndim() != 3)                         // attention.rs:148-153
+        return EngineError::incompatible_shapes("MultiHeadAttention cross-attention (expected 3D query [B, T_q, C] "
+                                                "and 3D memory [B, T_kv, C])",
+                                                {x.shape(), memory.shape()});
+    if (x.shape()[0] != memory.shape()[0] || x.shape()[2] != memory.shape()[2])   // :155-160
+        return EngineError::incompatible_shapes(
+            "MultiHeadAttention cross-attention (batch size and channel dim must match)", {x.shape(), memory.shape()});
+    const size_t b = x.shape()[0], tq = x.shape()[1], tkv = memory.shape()[1], h = num_heads, d = head_dim;
+    auto qp = q_proj.forward(x);
+    if (qp.is_err()) return qp.error();
+    RawTensor q = qp.value().reshape({b, tq, h, d}).value().transpose(1, 2).value();
+    std::pair<RawTensor, RawTensor> kv;
+    if (slot && slot->has_value()) {
+        kv = slot->value();
+    } else {
+        auto kp = k_proj.forward(memory);
+        if (kp.is_err()) return kp.error();
+        auto vp = v_proj.forward(memory);
+        if (vp.is_err()) return vp.error();
+        kv = {kp.value().reshape({b, tkv, h, d}).value().transpose(1, 2).value(),
+              vp.value().reshape({b, tkv, h, d}).value().transpose(1, 2).value()};
+        if (slot) *slot = kv;
+    }
+    auto merged = attend_merged(q, kv.first, kv.second, false, 0);
+    if (merged.is_err()) return merged.error();
+    return out_proj.forward(merged.value());
+}
+
 }  // namespace nne

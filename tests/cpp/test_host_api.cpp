@@ -330,6 +330,92 @@ TEST_GPU(test_gqa_layer_decode_matches_oracle) {
     CHECK(r.is_err() && r.error().kind == EngineError::Kind::InvalidArgument);
 }
 
+// Oracle of attention.rs:51-210 for one call: projections with bias, optional
+// cached rows, -1e4 mask with start = L - T for causal multi-token steps.
+std::vector<float> oracle_mha(const MultiHeadAttention& m, const std::vector<float>& xq, size_t b, size_t tq,
+                              const std::vector<float>& kall, const std::vector<float>& vall, size_t L, bool causal) {
+    const size_t c = m.d_model, h = m.num_heads, d = m.head_dim;
+    const auto wq = m.q_proj.weight.to_vec(), bq = m.q_proj.bias->to_vec();
+    const auto wo = m.out_proj.weight.to_vec(), bo = m.out_proj.bias->to_vec();
+    std::vector<float> qy(b * tq * c), q(b * h * tq * d), ctx(b * h * tq * d), merged(b * tq * c), y(b * tq * c);
+    oracle_linear(xq.data(), wq.data(), bq.data(), qy.data(), b * tq, c, c);
+    for (size_t bi = 0; bi < b; ++bi)
+        for (size_t r = 0; r < tq; ++r)
+            for (size_t hh = 0; hh < h; ++hh)
+                for (size_t e = 0; e < d; ++e) q[((bi * h + hh) * tq + r) * d + e] = qy[(bi * tq + r) * c + hh * d + e];
+    oracle_standard_attention(q.data(), kall.data(), vall.data(), ctx.data(), b, h, h, tq, L, d,
+                              causal && tq > 1 ? 1 : 0, (int64_t)(L - tq), 0, 0.f, 8);
+    for (size_t bi = 0; bi < b; ++bi)
+        for (size_t hh = 0; hh < h; ++hh)
+            for (size_t r = 0; r < tq; ++r)
+                for (size_t e = 0; e < d; ++e)
+                    merged[(bi * tq + r) * c + hh * d + e] = ctx[((bi * h + hh) * tq + r) * d + e];
+    oracle_linear(merged.data(), wo.data(), bo.data(), y.data(), b * tq, c, c);
+    return y;
+}
+
+// [B, T, C] projection -> [B, H, T, d] with bias, appended after `prev` rows.
+std::vector<float> project_heads(const Linear& l, const std::vector<float>& x, size_t b, size_t t, size_t h,
+                                 const std::vector<float>& prev, size_t L_prev) {
+    const size_t c = l.in_features, d = c / h;
+    const auto w = l.weight.to_vec(), bias = l.bias->to_vec();
+    std::vector<float> y(b * t * c), out(b * h * (L_prev + t) * d);
+    oracle_linear(x.data(), w.data(), bias.data(), y.data(), b * t, c, c);
+    for (size_t bi = 0; bi < b; ++bi)
+        for (size_t hh = 0; hh < h; ++hh)
+            for (size_t r = 0; r < L_prev + t; ++r)
+                for (size_t e = 0; e < d; ++e)
+                    out[((bi * h + hh) * (L_prev + t) + r) * d + e] =
+                        r < L_prev ? prev[((bi * h + hh) * L_prev + r) * d + e]
+                                   : y[(bi * t + (r - L_prev)) * c + hh * d + e];
+    return out;
+}
+
+TEST_GPU(test_mha_cached_self_attention_matches_oracle) {                 // attention.rs:51-129
+    const size_t b = 2, c = 128, h = 2, t0 = 5, steps = 3;
+    manual_seed(13);
+    MultiHeadAttention m(c, h, true);
+    RawTensor x = RawTensor::randn({b, t0 + steps, c}, 0.f, 1.f);
+    WhisperKVCache cache(1, b, h, 16, c / h);
+    std::vector<float> kall, vall;
+    size_t L = 0;
+    for (size_t s = 0; s <= steps; ++s) {
+        const size_t lo = s == 0 ? 0 : t0 + s - 1, tt = s == 0 ? t0 : 1;
+        RawTensor xs = x.slice(1, lo, lo + tt).unwrap();
+        const auto y = m.forward_attention_cached(xs, &cache.self_attn, 0).unwrap().to_vec();
+        const auto xv = xs.to_contiguous().to_vec();
+        kall = project_heads(m.k_proj, xv, b, tt, h, kall, L);
+        vall = project_heads(m.v_proj, xv, b, tt, h, vall, L);
+        L += tt;
+        check_close(y, oracle_mha(m, xv, b, tt, kall, vall, L, true), s == 0 ? "mha prefill" : "mha decode");
+    }
+    CHECK(cache.self_attn.current_seq_len(0) == t0 + steps);
+    auto r = m.forward_attention(RawTensor::randn({b, c}, 0.f, 1.f));    // :56-62
+    CHECK(r.is_err() && r.error().kind == EngineError::Kind::IncompatibleShapes);
+}
+
+TEST_GPU(test_cross_attention_cached_slot) {                              // attention.rs:139-210
+    const size_t b = 2, c = 128, h = 2, tkv = 70;
+    manual_seed(14);
+    MultiHeadAttention m(c, h, false);
+    RawTensor mem = RawTensor::randn({b, tkv, c}, 0.f, 1.f);
+    WhisperKVCache cache(2, b, h, 16, c / h);
+    const auto memv = mem.to_vec();
+    const auto kall = project_heads(m.k_proj, memv, b, tkv, h, {}, 0);
+    const auto vall = project_heads(m.v_proj, memv, b, tkv, h, {}, 0);
+    for (int step = 0; step < 3; ++step) {
+        RawTensor x = RawTensor::randn({b, 1, c}, 0.f, 1.f);
+        const auto y = m.forward_cross_attention_cached(x, mem, &cache.cross_attn[1]).unwrap().to_vec();
+        CHECK(cache.cross_attn[1].has_value() && !cache.cross_attn[0].has_value());
+        check_close(y, oracle_mha(m, x.to_vec(), b, 1, kall, vall, tkv, false), "cross attention");
+    }
+    RawTensor bad = RawTensor::randn({3, tkv, c}, 0.f, 1.f);
+    auto r = m.forward_cross_attention(RawTensor::randn({b, 1, c}, 0.f, 1.f), bad);   // :155-160
+    CHECK(r.is_err() && r.error().to_string().find("batch size and channel dim must match") != std::string::npos);
+    cache.reset();
+    CHECK(!cache.cross_attn[1].has_value());
+}
+
 TEST_CPU(test_gqa_rejects_bad_head_counts) {                             // llama.rs:174-183
     bool threw = false;
     try {
