@@ -169,6 +169,42 @@ def cpu_baseline(target_seconds=15.0):
                       "(unmasked pairs only)" % (heads, el)}
 
 
+def decode_cpu_baseline(seed=0x5EED0003, n_seq=8, steps=16):
+    """Oracle decode step (append, then attend, llama.rs:239-296 with t = 1)
+    on the first n_seq sequences of config 3, timed on the host cores."""
+    import numpy as np
+    sys.path.insert(0, os.path.join(ROOT, "tests"))
+    import nne_testlib as T
+    threads = min(16, os.cpu_count() or 1)
+    b, hq, hkv, d = 32, 32, 8, 128
+    rng = np.random.default_rng(seed)
+    lens = rng.integers(512, 4097, size=b).astype(np.int32)[:n_seq].copy()
+    cap = int(lens.max()) + steps
+    kc = rng.standard_normal((n_seq, hkv, cap, d), dtype=np.float32)
+    vc = rng.standard_normal((n_seq, hkv, cap, d), dtype=np.float32)
+    o = T.oracle()
+    total = 0.0
+    el = 0.0
+    for i in range(steps):
+        q = rng.standard_normal((n_seq, hq, 1, d), dtype=np.float32)
+        kn = rng.standard_normal((n_seq, hkv, 1, d), dtype=np.float32)
+        vn = rng.standard_normal((n_seq, hkv, 1, d), dtype=np.float32)
+        out = np.zeros((n_seq, hq, 1, d), np.float32)
+        t0 = time.perf_counter()
+        rc = o.oracle_decode_step(T._p(q), T._p(kc), T._p(vc), lens.ctypes.data_as(T._i32),
+                                  T._p(kn), T._p(vn), T._p(out), n_seq, hq, hkv, cap, d, 0, 0.0,
+                                  threads)
+        el += time.perf_counter() - t0
+        assert rc == 0
+        total += float(lens.sum()) * hkv * d * 4 * 2 + 2 * n_seq * hq * d * 4 + n_seq * hkv * d * 8
+    return {"value": round(total / el / 1e9, 2), "unit": "GB/s", "cores": threads, "kind": "port",
+            "sample": "config 3 decode step restated from llama.rs:239-296 (append in place, "
+                      "repeat-KV head mapping, softmax, PV; f32), the first %d sequences "
+                      "(lengths %d-%d), %d steps, %.2f s; bytes counted like the GPU line; "
+                      "the reference's per-step Tensor::cat copy of the cache is not included"
+                      % (n_seq, int(lens.min()) - steps, int(lens.max()) - steps, steps, el)}
+
+
 def bench_decode_layer(nne, torch, dev, steps=32, seed=0x5EED0013):
     """Config 3 as a GQA decode layer step (llama.rs:205-300, t = 1) minus
     the output GEMM: the fused projection + RoPE launch on packed weights
@@ -312,6 +348,8 @@ def main():
     if not args.no_decode:
         print("bench: config3 decode", file=sys.stderr, flush=True)
         line["decode"] = bench_decode(nne, torch, dev)
+        if not args.no_cpu:
+            line["decode"]["cpu_baseline"] = decode_cpu_baseline()
     if args.all:
         extra = []
         g = torch.Generator(device=dev).manual_seed(0x5EED0001)
