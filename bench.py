@@ -364,9 +364,17 @@ def main():
             o = torch.empty_like(q)
             ms_c, kms_c = time_prefill(nne, torch, q, k, v, causal, max(3, args.steps // 2), 2, o)
             fl = causal_flops(bb, h, tt, dd) if causal else full_flops(bb, h, tt, tt, dd)
-            extra.append({"workload": name, "TFLOP/s": round(fl / (kms_c / 1e3) / 1e12, 3),
-                          "kernel_ms": round(kms_c, 4),
-                          "frac": round(fl / (kms_c / 1e3) / 1e12 / PEAK_FP32_MATRIX_TFLOPS, 4)})
+            rec = {"workload": name}
+            if name == "config1":
+                # A ~15 us call: host-paced events measure Python's issue
+                # rate, so the device rate is taken with the calls queued.
+                paced = kms_c
+                kms_c = gpu_ms_per_call(
+                    torch, lambda i: nne.attention_forward(q, k, v, causal, out=o), 50, True)
+                rec["host_paced_kernel_ms"] = round(paced, 4)
+            rec.update({"TFLOP/s": round(fl / (kms_c / 1e3) / 1e12, 3), "kernel_ms": round(kms_c, 4),
+                        "frac": round(fl / (kms_c / 1e3) / 1e12 / PEAK_FP32_MATRIX_TFLOPS, 4)})
+            extra.append(rec)
             if name == "config5a":
                 # Three K/V sets (369 MB) rotated so no call finds its K/V in
                 # the 256 MB MALL.

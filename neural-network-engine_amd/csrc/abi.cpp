@@ -202,6 +202,17 @@ int run_attention(const float* q, const int64_t* qs_, const int64_t* qst, const 
     p.B = B; p.Hq = Hq; p.Hkv = Hkv; p.Tq = Tq; p.Tk = Tk; p.d = d;
     p.q_offset = qoff;
     p.qscale = scale * nne::kLog2e;
+    // Problems too small to fill the device split their key range across
+    // workgroups, with partial records in the stream's workspace.
+    const nne::PrefillSplit plan = nne::prefill_split_plan(p, causal, vec);
+    if (p.n_chunks > 1) {
+        uint32_t* counters = nullptr;
+        void* ws = nullptr;
+        hipError_t e = stream_resources(plan.n_counters, plan.ws_bytes, stream, &counters, &ws);
+        if (e != hipSuccess) return hip_fail(e, "prefill split workspace");
+        p.ws = static_cast<float*>(ws);
+        p.cnt = counters;
+    }
     hipError_t e = nne::launch_prefill(p, causal, vec, stream);
     if (e != hipSuccess) return hip_fail(e, "prefill attention launch");
     return NNE_OK;

@@ -40,6 +40,8 @@ struct OutView4 {
 // numbered u = row_block * G + g, and workgroup w of that KV head takes units
 // 4w .. 4w+3, so the G query heads of a group share every K/V tile the
 // workgroup stages in LDS.
+constexpr int kMaxSplitItems = 256;   // work items per KV head of a key-split launch
+
 struct PrefillParams {
     View4 q, k, v;
     OutView4 o;
@@ -58,6 +60,19 @@ struct PrefillParams {
     int n_pairs;
     int n_super;
     int per_xcd;
+    // Key split for problems too small to fill the chip (n_chunks > 1): the
+    // key tiles of every work item are cut into chunks of chunk_tiles tiles,
+    // one workgroup per (item, chunk); each leaves a partial (max, sum, O)
+    // record in ws and counts itself in cnt[item] (zeroed, left zeroed), and
+    // the last to arrive merges the item's records and writes O.
+    int n_chunks;       // largest chunk count of an item
+    int chunk_tiles;
+    float* ws;
+    uint32_t* cnt;
+    // Workgroup w of a KV head runs chunk w - part_prefix[i] of item i, where
+    // part_prefix[i] <= w < part_prefix[i + 1] (items of a head in rank order,
+    // empty items one chunk); part_prefix[n_wg] workgroups per head.
+    uint16_t part_prefix[kMaxSplitItems + 1];
 };
 
 // Fused decode prologue (qkv.hip): rows m < M of x [M, C] (row stride x_rs,

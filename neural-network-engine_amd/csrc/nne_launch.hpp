@@ -16,6 +16,15 @@ int splitk_max_rows();
 // `vec` selects 16-byte loads/stores: requires dim stride 1, d % 4 == 0,
 // 16-byte aligned base pointers and row/head/batch strides that are multiples of 4.
 hipError_t launch_prefill(PrefillParams p, bool causal, bool vec, hipStream_t stream);
+// Key-split plan for a prefill problem too small to fill the device (fills
+// p.n_chunks / p.chunk_tiles; n_chunks stays 0 when the problem is large
+// enough).  The caller then sets p.ws (ws_bytes) and p.cnt (n_counters zeroed
+// counters) before launch_prefill; without them the split is not used.
+struct PrefillSplit {
+    uint64_t ws_bytes;
+    int64_t n_counters;
+};
+PrefillSplit prefill_split_plan(PrefillParams& p, bool causal, bool vec);
 
 // Split-K workspace: per-sequence prefix (B+1 ints) and partial records for
 // up to splitk_max_workgroups() + B*Hkv (workgroup, head) pairs.

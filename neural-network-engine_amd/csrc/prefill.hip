@@ -30,7 +30,14 @@
 // the same staged tiles.  Workgroups are numbered so that each XCD works on a
 // contiguous range of KV heads (its own L2) and, within a head, the longest
 // causal row blocks start first.
+//
+// Problems with fewer work items than CUs instead cut each item's key tiles
+// into chunks, one workgroup per (item, chunk); the last chunk of an item to
+// finish folds the partial (max, sum, O) records in chunk order (the same
+// combine as the online softmax, so the result is independent of arrival
+// order) and writes O.
 #include <utility>
+#include <vector>
 
 #include "nne_common.hpp"
 #include "nne_launch.hpp"
@@ -117,8 +124,11 @@ __device__ __forceinline__ int item_at(const PrefillParams& p, int j, int x, int
     return 1;
 }
 
-template <int D, bool CAUSAL, bool VEC>
-__global__ __launch_bounds__(256, 2) void prefill_mfma_kernel(const PrefillParams p) {
+// Two workgroups per CU for the persistent schedule; the key-split variant
+// (small problems, one short chunk per workgroup) may take the whole register
+// file at d = 128 instead of spilling.
+template <int D, bool CAUSAL, bool VEC, bool SPLIT>
+__global__ __launch_bounds__(256, (SPLIT && D >= 128) ? 1 : 2) void prefill_mfma_kernel(const PrefillParams p) {
     constexpr int KS = D + 4;          // K row stride in LDS (16-byte reads conflict-free)
     constexpr int VS = D + 8;          // V row stride in LDS (lane halves on disjoint banks)
     constexpr int STAGE = 32 * KS + 32 * VS;
@@ -134,10 +144,29 @@ __global__ __launch_bounds__(256, 2) void prefill_mfma_kernel(const PrefillParam
 
 #pragma nounroll
     for (int j = 0;; ++j) {
-    int head = 0, wgi = 0;
-    const int st = item_at(p, j, x, q, S, head, wgi);
-    if (st == 0) break;
-    if (st == 2) continue;
+    int head = 0, wgi = 0, chunk = 0;
+    int n_parts = 1;
+    if constexpr (SPLIT) {
+        // Key split, one step only: the (item, chunk) pairs of a head are
+        // numbered contiguously, so consecutive workgroups (dealt to the 8
+        // XCDs in turn) carry equal work.
+        if (j > 0) break;
+        const int per_head = p.part_prefix[p.n_wg];
+        head = blockIdx.x / per_head;
+        const int r = blockIdx.x % per_head;
+        int lo = 0, hi = p.n_wg - 1;     // last item with part_prefix <= r
+        while (lo < hi) {
+            const int mid = (lo + hi + 1) >> 1;
+            if (p.part_prefix[mid] <= r) lo = mid; else hi = mid - 1;
+        }
+        wgi = lo;
+        chunk = r - p.part_prefix[lo];
+        n_parts = p.part_prefix[lo + 1] - p.part_prefix[lo];
+    } else {
+        const int st = item_at(p, j, x, q, S, head, wgi);
+        if (st == 0) break;
+        if (st == 2) continue;
+    }
     // Lane-derived addressing is recomputed for every item rather than held
     // live across the whole persistent loop.
     int tid = threadIdx.x;
@@ -163,6 +192,14 @@ __global__ __launch_bounds__(256, 2) void prefill_mfma_kernel(const PrefillParam
     if (n_tiles > n_kt) n_tiles = n_kt;
     const int wave_last_key = last_visible_key(p, rb, CAUSAL);
     const int wave_tiles = active ? (wave_last_key < 0 ? 0 : (wave_last_key >> 5) + 1) : 0;
+
+    // Key tiles [t0, t1) of this workgroup: all of them, or one chunk (an
+    // empty chunk still leaves its record).
+    int t0 = 0, t1 = n_tiles;
+    if constexpr (SPLIT) {
+        t0 = min(n_tiles, chunk * p.chunk_tiles);
+        t1 = min(n_tiles, t0 + p.chunk_tiles);
+    }
 
     // ---- Q^T fragment: qf[s] = Q[qrow][half*D/2 + s] * scale*log2(e) ----------
     float qf[D / 2];
@@ -197,16 +234,16 @@ __global__ __launch_bounds__(256, 2) void prefill_mfma_kernel(const PrefillParam
     float m_run = kNegInf, l_run = 0.f;
 
     TileLoader<D, VEC> ld;
-    if (n_tiles > 0) {
-        ld.load(p, kb, vb, 0, tid);
+    if (t1 > t0) {
+        ld.load(p, kb, vb, t0 * 32, tid);
         ld.store(lds, lds + 32 * KS, tid);
     }
     __syncthreads();
 
-    for (int kt = 0; kt < n_tiles; ++kt) {
-        const bool has_next = kt + 1 < n_tiles;
+    for (int kt = t0; kt < t1; ++kt) {
+        const bool has_next = kt + 1 < t1;
         const bool mine = kt < wave_tiles;
-        const float* Ks = lds + (kt & 1) * STAGE;
+        const float* Ks = lds + ((kt - t0) & 1) * STAGE;
         const float* Vs = Ks + 32 * KS;
         floatx16 s;
         if (mine) {
@@ -306,14 +343,85 @@ __global__ __launch_bounds__(256, 2) void prefill_mfma_kernel(const PrefillParam
         }
 
         if (has_next) {
-            float* ks = lds + ((kt + 1) & 1) * STAGE;
+            float* ks = lds + ((kt - t0 + 1) & 1) * STAGE;
             ld.store(ks, ks + 32 * KS, tid);
         }
         __syncthreads();
     }
 
+    float l_tot = pair_sum(l_run);
+    if constexpr (SPLIT) {
+        if (n_parts > 1) {
+            // Partial record of this chunk, lane-major so that every store and
+            // load is one coalesced wave access: O^T registers at
+            // ws[grid*512 + ((slot*4 + wave)*(D/2) + i)*64 + lane] and
+            // (max, sum) at ws[((slot*4 + wave)*64 + lane)*2], slot = blockIdx.
+            const int item = head * p.n_wg + wgi;
+            const int64_t o_base = (int64_t)gridDim.x * 512;
+            {
+                float* wo = p.ws + o_base + ((int64_t)blockIdx.x * 4 + wave) * (D / 2) * 64 + lane;
+#pragma unroll
+                for (int b = 0; b < NB; ++b)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) store_coherent(wo + (b * 16 + r) * 64, o[b][r]);
+                float* wml = p.ws + (((int64_t)blockIdx.x * 4 + wave) * 64 + lane) * 2;
+                store_coherent(wml, m_run);
+                store_coherent(wml + 1, l_tot);
+            }
+            wait_stores_performed();
+            __shared__ unsigned arrival_s;
+            __syncthreads();
+            if (tid == 0)
+                arrival_s = __hip_atomic_fetch_add(p.cnt + item, 1u, __ATOMIC_RELAXED,
+                                                   __HIP_MEMORY_SCOPE_AGENT);
+            __syncthreads();
+            if (arrival_s != (unsigned)(n_parts - 1)) break;   // not the last chunk (uniform)
+            if (tid == 0) __hip_atomic_store(p.cnt + item, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+
+            // Last chunk: fold the item's records, this one's included, in
+            // chunk order (online-softmax combine, GRP records per round
+            // trip), so the result does not depend on which chunk came last.
+            constexpr int GRP = D >= 128 ? 2 : 4;
+            float M = kNegInf;
+            l_tot = 0.f;
+#pragma unroll
+            for (int b = 0; b < NB; ++b)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) o[b][r] = 0.f;
+            const int slot0 = blockIdx.x - chunk;
+            for (int i = 0; i < n_parts; i += GRP) {
+                float mc[GRP], lc[GRP], oc[GRP][D / 2];
+#pragma unroll
+                for (int u = 0; u < GRP; ++u) {
+                    // A missing last record of a group reads this chunk's own
+                    // (finite) record with weight exp2(-inf) = 0.
+                    const bool ok = i + u < n_parts;
+                    const int64_t sl = ((int64_t)(slot0 + (ok ? i + u : chunk)) * 4 + wave);
+                    const float* ro = p.ws + o_base + sl * (D / 2) * 64 + lane;
+                    const float* rml = p.ws + (sl * 64 + lane) * 2;
+                    const float m_ld = load_coherent(rml), l_ld = load_coherent(rml + 1);
+                    mc[u] = ok ? m_ld : kNegInf;
+                    lc[u] = ok ? l_ld : 0.f;
+#pragma unroll
+                    for (int e = 0; e < D / 2; ++e) oc[u][e] = load_coherent(ro + e * 64);
+                }
+#pragma unroll
+                for (int u = 0; u < GRP; ++u) {
+                    const float m_new = fmaxf(M, mc[u]);
+                    const float mu = m_new == kNegInf ? 0.f : m_new;
+                    const float a = fast_exp2(M - mu), bw = fast_exp2(mc[u] - mu);
+                    l_tot = l_tot * a + lc[u] * bw;
+#pragma unroll
+                    for (int b = 0; b < NB; ++b)
+#pragma unroll
+                        for (int r = 0; r < 16; ++r) o[b][r] = o[b][r] * a + oc[u][b * 16 + r] * bw;
+                    M = m_new;
+                }
+            }
+        }
+    }
+
     // ---- normalise and write O[qrow][dim], dim = 32b + 8(r/4) + 4*half + r%4 --
-    const float l_tot = pair_sum(l_run);
     const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
     if (active && qrow < p.Tq) {
         float* op = p.o.p + bi * p.o.sb + hq * p.o.sh + (int64_t)qrow * p.o.st;
@@ -342,13 +450,14 @@ __global__ __launch_bounds__(256, 2) void prefill_mfma_kernel(const PrefillParam
 // CUs and resident workgroups per CU of the kernel on the current device.
 template <int D, bool CAUSAL, bool VEC>
 void residency(int& cus, int& per_cu) {
+    constexpr auto kernel = prefill_mfma_kernel<D, CAUSAL, VEC, false>;
     static int cached_cus[64] = {0}, cached_per[64] = {0};
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
     if (cached_cus[dev] == 0) {
         int c = 0, k = 0;
         if (hipDeviceGetAttribute(&c, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || c < 8) c = 256;
-        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&k, prefill_mfma_kernel<D, CAUSAL, VEC>, 256, 0) !=
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&k, kernel, 256, 0) !=
                 hipSuccess || k < 1)
             k = 1;
         cached_per[dev] = k;
@@ -367,6 +476,11 @@ void residency(int& cus, int& per_cu) {
 // so that every super-item costs the same.
 template <int D, bool CAUSAL, bool VEC>
 hipError_t launch_t(PrefillParams p, hipStream_t stream) {
+    if (p.n_chunks > 1 && p.ws && p.cnt) {
+        hipLaunchKernelGGL((prefill_mfma_kernel<D, CAUSAL, VEC, true>),
+                           dim3(p.B * p.Hkv * p.part_prefix[p.n_wg]), dim3(256), 0, stream, p);
+        return hipGetLastError();
+    }
     int cus = 0, k_max = 0;
     residency<D, CAUSAL, VEC>(cus, k_max);
     const int cu_per_xcd = cus / 8;
@@ -386,8 +500,30 @@ hipError_t launch_t(PrefillParams p, hipStream_t stream) {
     // A partly empty last round costs more than the hardware's own dispatch of
     // one super-item per workgroup (which also covers small problems).
     if (S >= p.per_xcd || (double)p.per_xcd / ((double)best_rounds * S) < 0.97) S = p.per_xcd;
-    hipLaunchKernelGGL((prefill_mfma_kernel<D, CAUSAL, VEC>), dim3(8 * S), dim3(256), 0, stream, p);
+    hipLaunchKernelGGL((prefill_mfma_kernel<D, CAUSAL, VEC, false>), dim3(8 * S), dim3(256), 0, stream, p);
     return hipGetLastError();
+}
+
+// Resident workgroups per CU of the key-split variant (cached per device).
+template <int D, bool CAUSAL, bool VEC>
+int split_per_cu() {
+    static int cached[64] = {0};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
+    if (cached[dev] == 0) {
+        int k = 0;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&k, prefill_mfma_kernel<D, CAUSAL, VEC, true>, 256,
+                                                         0) != hipSuccess || k < 1)
+            k = 1;
+        cached[dev] = k;
+    }
+    return cached[dev];
+}
+
+template <int D>
+int split_per_cu_d(bool causal, bool vec) {
+    if (causal) return vec ? split_per_cu<D, true, true>() : split_per_cu<D, true, false>();
+    return vec ? split_per_cu<D, false, true>() : split_per_cu<D, false, false>();
 }
 
 template <int D>
@@ -405,12 +541,87 @@ int prefill_padded_dim(int d) {
     return 0;
 }
 
-hipError_t launch_prefill(PrefillParams p, bool causal, bool vec, hipStream_t stream) {
+namespace {
+
+void derive_schedule(PrefillParams& p) {
     p.G = p.Hq / p.Hkv;
     p.n_rb = (p.Tq + 31) / 32;
     p.n_units = p.G * p.n_rb;
     p.n_wg = (p.n_units + 3) / 4;
     p.total = p.B * p.Hkv * p.n_wg;
+}
+
+int device_cus() {
+    static int cached[64] = {0};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
+    if (cached[dev] == 0) {
+        int c = 0;
+        if (hipDeviceGetAttribute(&c, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || c < 8)
+            c = 256;
+        cached[dev] = c;
+    }
+    return cached[dev];
+}
+
+}  // namespace
+
+// A problem with fewer work items than CUs leaves most SIMDs idle, and its
+// time is the longest item's chain of key tiles.  Cutting every item's tiles
+// into chunks of at least 2 tiles, sized so that the chunks fill one resident
+// round of the split kernel (at most 16 chunks per item), shortens that chain
+// to one chunk plus the merge of the item's records.
+PrefillSplit prefill_split_plan(PrefillParams& p, bool causal, bool vec) {
+    PrefillSplit r{0, 0};
+    p.n_chunks = 0;
+    p.chunk_tiles = 0;
+    derive_schedule(p);
+    const int D = prefill_padded_dim(p.d);
+    const int cus = device_cus();
+    if (p.total == 0 || D == 0 || p.total >= cus || p.n_wg > kMaxSplitItems) return r;
+    // Key tiles of each work item, as the kernel counts them.
+    const int n_kt = (p.Tk + 31) / 32;
+    std::vector<int> tiles(p.n_wg);
+    int max_t = 0;
+    for (int w = 0; w < p.n_wg; ++w) {
+        const int last_unit = std::min(w * 4 + 3, p.n_units - 1);
+        int lk = p.Tk - 1;
+        if (causal) {
+            const int last_row = std::min(last_unit / p.G * 32 + 31, p.Tq - 1);
+            lk = std::min(last_row + p.q_offset, p.Tk - 1);
+        }
+        tiles[w] = lk < 0 ? 0 : std::min(lk / 32 + 1, n_kt);
+        max_t = std::max(max_t, tiles[w]);
+    }
+    if (max_t < 4) return r;
+    const int per_cu = D == 32 ? split_per_cu_d<32>(causal, vec)
+                     : D == 64 ? split_per_cu_d<64>(causal, vec)
+                               : split_per_cu_d<128>(causal, vec);
+    const int64_t slots = (int64_t)cus * per_cu;
+    // Smallest chunk (>= 2 tiles, <= 16 chunks per item) whose non-empty
+    // chunks fit in one resident round.
+    int ch = std::max(2, (max_t + 15) / 16);
+    for (;; ++ch) {
+        int64_t n = 0;
+        for (int w = 0; w < p.n_wg; ++w) n += std::max(1, (tiles[w] + ch - 1) / ch);
+        if (n * p.B * p.Hkv <= slots || ch >= max_t) break;
+    }
+    const int nc = (max_t + ch - 1) / ch;
+    if (nc < 2) return r;
+    p.n_chunks = nc;
+    p.chunk_tiles = ch;
+    p.part_prefix[0] = 0;
+    for (int w = 0; w < p.n_wg; ++w)
+        p.part_prefix[w + 1] = (uint16_t)(p.part_prefix[w] + std::max(1, (tiles[w] + ch - 1) / ch));
+    // Per workgroup: (max, sum) of 4 waves x 64 lanes, and 4 x D/2 x 64 O values.
+    const uint64_t grid = (uint64_t)p.B * p.Hkv * p.part_prefix[p.n_wg];
+    r.ws_bytes = grid * (512 + 128 * (uint64_t)D) * 4;
+    r.n_counters = p.total;
+    return r;
+}
+
+hipError_t launch_prefill(PrefillParams p, bool causal, bool vec, hipStream_t stream) {
+    derive_schedule(p);
     if (p.total == 0) return hipSuccess;
     switch (prefill_padded_dim(p.d)) {
         case 32: return launch_d<32>(p, causal, vec, stream);

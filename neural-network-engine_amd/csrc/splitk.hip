@@ -30,13 +30,17 @@
 //     the next block's K and V loads are in flight while a block computes;
 //   * the 4 waves' (max, sum, O) are merged through LDS; a head covered by
 //     one workgroup is written directly, otherwise each workgroup leaves a
-//     partial record that the per-head combine kernel merges;
+//     partial record (agent-scope stores, then a wait until they are
+//     performed) and counts itself in on the head's arrival counter; the last
+//     of the head's workgroups merges its records inside the same launch.
+//     Without counters, or with too many sequences for the prefix to travel in
+//     the kernel arguments, the per-head combine kernel merges them instead;
 //   * in a decode step the new K/V row is read straight from the caller's
 //     k_new / v_new and written into the cache by the workgroup whose split
-//     holds it; the combine kernel then advances lens[b].
-// No cross-workgroup synchronisation is used inside the split kernel: on
-// gfx950 an agent-scope fence is a whole-L2 writeback and invalidate, far more
-// expensive than the second launch.
+//     holds it; lens[b] is advanced inside the launch (or by the combine
+//     kernel).
+// The hand-off uses per-access coherence rather than fences: on gfx950 an
+// agent-scope fence is a whole-L2 writeback and invalidate.
 #include <algorithm>
 #include <utility>
 

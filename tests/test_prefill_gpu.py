@@ -192,6 +192,55 @@ def test_few_query_split_k_row_tiles(nne, cuda, g, tq, tk, d):
     T.assert_close(got, T.ref_standard(q, k, v, False), what="few-query g=%d tq=%d" % (g, tq))
 
 
+# Problems with fewer work items (4 row blocks of 32 rows) than CUs and at
+# least 4 key tiles split every item's key tiles into chunks, one workgroup
+# each; the last workgroup of an item merges the partial (max, sum, O)
+# records.  Cases: config 1 (2 and 4 chunks), one item of 16 chunks (cached
+# multi-token step), the 16-chunk cap with an odd number of records to fold,
+# GQA through strided [B, T, H, d] views on the scalar path, a negative
+# offset (rows without keys), a padded head dim.
+@pytest.mark.parametrize("b,hq,hkv,tq,tk,d,causal,q_off,strided", [
+    (1, 4, 4, 256, 256, 64, True, 0, False),
+    (1, 2, 1, 9, 1000, 128, True, 991, False),
+    (1, 1, 1, 32, 4096, 64, False, 0, False),
+    (2, 8, 2, 160, 700, 32, True, 540, True),
+    (1, 3, 3, 200, 333, 128, True, -50, False),
+    (1, 2, 2, 130, 450, 80, False, 0, False),
+])
+def test_key_split_small_problems(nne, cuda, b, hq, hkv, tq, tk, d, causal, q_off, strided):
+    import torch
+    print("case key split", b, hq, hkv, tq, tk, d, causal, q_off, strided, flush=True)
+    s = 31 * tk + d
+    q, k, v = rnd(s, b, hq, tq, d), rnd(s + 1, b, hkv, tk, d), rnd(s + 2, b, hkv, tk, d)
+    if strided:
+        qd, kd, vd = (dev(x.transpose(0, 2, 1, 3), cuda).transpose(1, 2) for x in (q, k, v))
+        out = torch.zeros(b, tq, hq, d, device=cuda).transpose(1, 2)
+        nne.attention_forward(qd, kd, vd, causal, q_offset=q_off, out=out)
+    else:
+        out = nne.attention_forward(dev(q, cuda), dev(k, cuda), dev(v, cuda), causal, q_offset=q_off)
+    got = host(out)
+    r0 = max(0, -q_off) if causal else 0          # rows r < -q_off see no key
+    assert not got[:, :, :r0].any()
+    ref = T.ref_standard(q[:, :, r0:], k, v, causal, start_pos=q_off + r0)
+    T.assert_close(got[:, :, r0:], ref, what="key split")
+
+
+def test_key_split_workspace_reuse_is_deterministic(nne, cuda):
+    """Back-to-back split launches of different shapes share the stream's
+    workspace and arrival counters; every call leaves the counters at zero,
+    so repeating a call reproduces its output bit for bit."""
+    qa, ka, va = (dev(rnd(90 + i, 1, 4, 256, 64), cuda) for i in range(3))
+    qb = dev(rnd(93, 1, 2, 9, 128), cuda)
+    kb, vb = (dev(rnd(94 + i, 1, 1, 1000, 128), cuda) for i in range(2))
+    first = host(nne.attention_forward(qa, ka, va, True))
+    for _ in range(3):
+        ob = host(nne.attention_forward(qb, kb, vb, True, q_offset=991))
+        again = host(nne.attention_forward(qa, ka, va, True))
+        assert np.array_equal(again, first)
+    T.assert_close(ob, T.ref_standard(host(qb), host(kb), host(vb), True, start_pos=991),
+                   what="key split reuse")
+
+
 def test_linearity_in_v_full_config4_shape(nne, cuda):
     """O is linear in V: f(a V1 + b V2) = a f(V1) + b f(V2) at T = 16384."""
     t = 16384
