@@ -169,6 +169,52 @@ def cpu_baseline(target_seconds=15.0):
                       "(unmasked pairs only)" % (heads, el)}
 
 
+def flash_cpu_baseline(b, h, t, d, causal, std, sample, reps=1, seed=0x5EED0004):
+    """Oracle flash_attention_forward (flash_attention.rs:19-199, br = bc = 64
+    as in the FlashAttention layer) on the host cores, parallel over the B*H
+    heads as the reference is (:69); median of reps calls."""
+    import numpy as np
+    sys.path.insert(0, os.path.join(ROOT, "tests"))
+    import nne_testlib as T
+    threads = max(1, min(16, os.cpu_count() or 1, b * h))
+    rng = np.random.default_rng(seed)
+    q, k, v = (rng.standard_normal((b, h, t, d), dtype=np.float32) * std for _ in range(3))
+    times = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        T.ref_flash(q, k, v, causal, br=64, bc=64, threads=threads)
+        times.append(time.perf_counter() - t0)
+    el = sorted(times)[len(times) // 2]
+    fl = causal_flops(b, h, t, d) if causal else full_flops(b, h, t, t, d)
+    return {"value": round(fl / el / 1e12, 6), "unit": "TFLOP/s", "cores": threads, "kind": "port",
+            "sample": "%s; flash_attention_forward restated from flash_attention.rs:19-199 "
+                      "(br = bc = 64, f32), %s, median of %d: %.3f s" % (
+                          sample, "causal" if causal else "non-causal", reps, el)}
+
+
+def cross_cpu_baseline(b=8, h=20, tq=8, tk=1500, d=64, reps=5, seed=0x5EED0005):
+    """Oracle cross-attention core (attention.rs:193-203: scores, softmax, PV
+    over the cached memory K/V) for config 5b on the host cores."""
+    import numpy as np
+    sys.path.insert(0, os.path.join(ROOT, "tests"))
+    import nne_testlib as T
+    threads = max(1, min(16, os.cpu_count() or 1))
+    rng = np.random.default_rng(seed)
+    q = rng.standard_normal((b, h, tq, d), dtype=np.float32)
+    k, v = (rng.standard_normal((b, h, tk, d), dtype=np.float32) for _ in range(2))
+    times = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        T.ref_standard(q, k, v, masked=False, threads=threads)
+        times.append(time.perf_counter() - t0)
+    el = sorted(times)[len(times) // 2]
+    by = (2 * b * h * tk * d + 2 * b * h * tq * d) * 4
+    return {"value": round(by / el / 1e9, 2), "unit": "GB/s", "cores": threads, "kind": "port",
+            "sample": "config 5b in full (B=8, H=20, 8 queries onto 1500 frames, d=64), "
+                      "attention core restated from attention.rs:193-203 (f32), median of "
+                      "%d: %.4f s; bytes counted like the GPU line" % (reps, el)}
+
+
 def decode_cpu_baseline(seed=0x5EED0003, n_seq=8, steps=16):
     """Oracle decode step (append, then attend, llama.rs:239-296 with t = 1)
     on the first n_seq sequences of config 3, timed on the host cores."""
@@ -374,6 +420,19 @@ def main():
                 rec["host_paced_kernel_ms"] = round(paced, 4)
             rec.update({"TFLOP/s": round(fl / (kms_c / 1e3) / 1e12, 3), "kernel_ms": round(kms_c, 4),
                         "frac": round(fl / (kms_c / 1e3) / 1e12 / PEAK_FP32_MATRIX_TFLOPS, 4)})
+            if not args.no_cpu:
+                # Bounded samples of the same workload (a few seconds each).
+                rec["cpu_baseline"] = {
+                    "config1": lambda: flash_cpu_baseline(1, 4, 256, 64, True, 1.0,
+                                                          "config 1 in full (B=1, H=4, T=256, d=64)",
+                                                          reps=5),
+                    "config4": lambda: flash_cpu_baseline(1, 16, 4096, 64, True, 0.5,
+                                                          "config 4 at a quarter of its length "
+                                                          "(B=1, H=16, T=4096, d=64)"),
+                    "config5a": lambda: flash_cpu_baseline(1, 20, 1500, 64, False, 1.0,
+                                                           "one of the 8 batch elements of "
+                                                           "config 5a (H=20, T=1500, d=64)"),
+                }[name]()
             extra.append(rec)
             if name == "config5a":
                 # Three K/V sets (369 MB) rotated so no call finds its K/V in
@@ -396,6 +455,8 @@ def main():
                               "note": "3 K/V sets rotated (369 MB > 256 MB MALL); calls queued "
                                       "behind a spin kernel so the GPU runs them back to back; "
                                       "host_paced = issued from Python one by one"})
+                if not args.no_cpu:
+                    extra[-1]["cpu_baseline"] = cross_cpu_baseline()
                 del kvs
             del q, k, v, o
         print("bench: config3 decode layer step", file=sys.stderr, flush=True)
