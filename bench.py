@@ -387,7 +387,7 @@ def main():
                      "peak": PEAK_FP32_MATRIX_TFLOPS, "unit": "TFLOP/s",
                      "frac": round(achieved / PEAK_FP32_MATRIX_TFLOPS, 4),
                      "traffic": TRAFFIC_PREFILL_CONFIG2,
-                     "kernel": "prefill_mfma_kernel<128,causal,vec>",
+                     "kernel": "prefill_mfma_kernel<128, true, true, false>",
                      "kernel_ms": round(kms, 4)},
     }
     del q, k, v, out
