@@ -167,29 +167,37 @@ int run_attention(const float* q, const int64_t* qs_, const int64_t* qst, const 
     const bool vec = d % 4 == 0 && vec_view(q, qst) && vec_view(k, kst) && vec_view(v, vst) &&
                      vec_view(o, ost);
     const int G = Hq / Hkv;
-    const bool all_visible = !causal || (int64_t)qoff >= (int64_t)Tk - 1;
     const int64_t rows = (int64_t)G * Tq;
+    // Few query rows per KV head (decode-like steps, cross-attention, a few
+    // new tokens over a cache) go to the split-K kernel.  With a causal mask
+    // only the first tk keys are visible to any row (the last row sees keys
+    // <= qoff + Tq - 1), and rows see different prefixes of them when
+    // qoff < tk - 1.
+    const int64_t tk = causal ? std::min<int64_t>(Tk, (int64_t)qoff + Tq) : Tk;
+    const bool masked = causal && (int64_t)qoff < tk - 1;
 
-    if (vec && all_visible && rows <= nne::splitk_max_rows() && Tk > 0 &&
-        B <= nne::splitk_max_seqs() && (int64_t)B * Hkv * Tk < INT32_MAX &&
-        (int64_t)Tk * kst[2] < INT32_MAX && (int64_t)Tk * vst[2] < INT32_MAX) {
+    if (vec && rows <= nne::splitk_max_rows() && tk > 0 &&
+        B <= nne::splitk_max_seqs() && (int64_t)B * Hkv * tk < INT32_MAX &&
+        tk * kst[2] < INT32_MAX && tk * vst[2] < INT32_MAX) {
         nne::SplitKParams p{};
         p.q = make_view(q, qst);
         p.k = k; p.v = v;
         p.ksb = kst[0]; p.ksh = kst[1]; p.kst = kst[2];
         p.vsb = vst[0]; p.vsh = vst[1]; p.vst = vst[2];
         p.lens = nullptr;
-        p.tk = Tk;
-        p.max_keys = Tk;
+        p.tk = (int)tk;
+        p.max_keys = (int)tk;
         p.o = make_out(o, ost);
         p.B = B; p.Hq = Hq; p.Hkv = Hkv; p.Tq = Tq; p.d = d;
         p.qscale = scale * nne::kLog2e;
+        p.masked = masked ? 1 : 0;
+        p.q_off = qoff;
         const nne::SplitKWorkspace w = nne::splitk_workspace_layout(B, Hkv, (int)rows, d);
         uint32_t* counters = nullptr;
         void* ws = nullptr;
         hipError_t e = stream_resources((int64_t)B * Hkv, w.total_bytes, stream, &counters, &ws);
         if (e != hipSuccess) return hip_fail(e, "split-K workspace");
-        e = nne::launch_splitk(p, (int64_t)B * Hkv * Tk, Tk, ws, stream, nullptr, counters);
+        e = nne::launch_splitk(p, (int64_t)B * Hkv * tk, (int)tk, ws, stream, nullptr, counters);
         if (e != hipSuccess) return hip_fail(e, "split-K attention launch");
         return NNE_OK;
     }

@@ -117,6 +117,9 @@ struct SplitKParams {
     OutView4 o;
     int B, Hq, Hkv, G, Tq, d, R;
     float qscale;            // softmax scale * log2(e)
+    // Causal rows (masked != 0): query t sees keys c <= q_off + t only.
+    int masked;
+    int q_off;
     int n_wg;                // workgroups of the split kernel
     int chunk;               // flattened keys per workgroup
     // decode step only (k_new != null): the new row [B, Hkv, 1, d] is attended

@@ -3,7 +3,9 @@
 // Semantics: every query row attends to all keys of its sequence with no mask
 // -- the reference's single-token decode (src/models/llama.rs:239-296 with
 // t = 1: append first, then attend to all L rows including the new one) and
-// its cross-attention (src/nn/attention.rs:193-203).  Sequences may have
+// its cross-attention (src/nn/attention.rs:193-203) -- or, for a few causal
+// rows (masked), query t sees keys c <= q_off + t: a multi-token step over a
+// cache (the bottom-right mask of llama.rs:277-292 and attention.rs:101-108).  Sequences may have
 // different lengths (lens[b]); the reference handles ragged batches as
 // separate B = 1 calls.
 //
@@ -172,13 +174,14 @@ __device__ __forceinline__ void build_prefix(const SplitKParams& p, int* pref, i
 
 // Merges the n partial records (slots s0 .. s0+n-1) of one head into its
 // output, then clears the head's arrival counter.  n * R <= 1024 (the host
-// bounds the workgroups per head), so each thread holds at most 4 records.
+// bounds the workgroups per head), so each thread holds at most 4 (max, sum)
+// pairs; the O rows are read NPRE records per round trip.
 template <int D, int ROWS>
 __device__ __forceinline__ void merge_head_records(const SplitKParams& p, int b, int kvh, int head,
                                                    int64_t s0, int n, float* w_s, unsigned* red_m,
                                                    float* red_l, int tid) {
     constexpr int EPT = ROWS * D / 256;   // output elements per thread (R <= ROWS)
-    constexpr int NPRE = EPT >= 8 ? 2 : 4;  // partials per element loaded up front
+    constexpr int NPRE = EPT >= 8 ? 4 : 8;  // partials per element per round trip
     const int NR = n * p.R;
     const int RD = p.R * D;
     const float* o_src = p.ws_o + s0 * RD;
@@ -216,21 +219,41 @@ __device__ __forceinline__ void merge_head_records(const SplitKParams& p, int b,
         }
     }
     __syncthreads();
+    float acc[EPT];
+#pragma unroll
+    for (int j = 0; j < EPT; ++j) {
+        const int rr = (tid + 256 * j) / D;
+        acc[j] = 0.f;
+#pragma unroll
+        for (int c = 0; c < NPRE; ++c)
+            if (c < n && tid + 256 * j < RD) acc[j] += w_s[c * p.R + rr] * pre[j][c];
+    }
+    // Further records: all loads of a round issued before its first add.
+    for (int c0 = NPRE; c0 < n; c0 += NPRE) {
+#pragma unroll
+        for (int j = 0; j < EPT; ++j) {
+            const int e = tid + 256 * j;
+#pragma unroll
+            for (int c = 0; c < NPRE; ++c)
+                pre[j][c] = (e < RD && c0 + c < n) ? load_coherent(o_src + (int64_t)(c0 + c) * RD + e) : 0.f;
+        }
+#pragma unroll
+        for (int j = 0; j < EPT; ++j) {
+            const int rr = (tid + 256 * j) / D;
+#pragma unroll
+            for (int c = 0; c < NPRE; ++c)
+                if (c0 + c < n && tid + 256 * j < RD) acc[j] += w_s[(c0 + c) * p.R + rr] * pre[j][c];
+        }
+    }
 #pragma unroll
     for (int j = 0; j < EPT; ++j) {
         const int e = tid + 256 * j;
         if (e >= RD) break;
         const int rr = e / D, dd = e % D;
-        float acc = 0.f;
-#pragma unroll
-        for (int c = 0; c < NPRE; ++c)
-            if (c < n) acc += w_s[c * p.R + rr] * pre[j][c];
-        for (int c = NPRE; c < n; ++c)
-            acc += w_s[c * p.R + rr] * load_coherent(o_src + (int64_t)c * RD + e);
         if (dd < p.d) {
             const float den = red_l[rr];
             const int hq = kvh * p.G + rr / p.Tq, t = rr % p.Tq;
-            p.o.p[b * p.o.sb + hq * p.o.sh + t * p.o.st + dd] = den > 0.f ? acc / den : 0.f;
+            p.o.p[b * p.o.sb + hq * p.o.sh + t * p.o.st + dd] = den > 0.f ? acc[j] / den : 0.f;
         }
     }
     if (tid == 0)
@@ -464,6 +487,11 @@ __global__ __launch_bounds__(256, 2) void splitk_kernel(const SplitKParams p) {
 #pragma unroll
                 for (int r = 0; r < 4; ++r) s[r] = ok ? s[r] : kNegInf;
             }
+            if (p.masked && kb0 + KB - 1 > p.q_off) {   // causal rows: key <= q_off + t
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+                    s[r] = kb0 + col <= p.q_off + r % p.Tq ? s[r] : kNegInf;
+            }
             // Lazy rescale: keep each row's reference max until a score exceeds
             // it by 8 (a factor 256 in exp2), so most blocks skip the row max.
             bool grow = false;
@@ -512,6 +540,11 @@ __global__ __launch_bounds__(256, 2) void splitk_kernel(const SplitKParams p) {
             if (kb0 + KB > key_end) {
 #pragma unroll
                 for (int r = 0; r < 4; ++r) s[r] = (kb0 + 4 * grp + r < key_end) ? s[r] : kNegInf;
+            }
+            if (p.masked && kb0 + KB - 1 > p.q_off) {   // causal rows: key <= q_off + t
+                const int last = p.q_off + col % p.Tq;
+#pragma unroll
+                for (int r = 0; r < 4; ++r) s[r] = (kb0 + 4 * grp + r <= last) ? s[r] : kNegInf;
             }
             float mt = fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3]));
             mt = quad_rows_max(mt);
@@ -838,7 +871,8 @@ hipError_t launch_flat(SplitKParams p, int64_t total_keys, int max_len, hipStrea
     // Equal flattened chunks, whole 16-key blocks, and at most max_parts
     // workgroups sharing any one head (a chunk boundary can add two).
     int64_t chunk = (total_keys + slots - 1) / (slots > 0 ? slots : 1);
-    const int64_t min_chunk = (max_len + (p.max_parts - 2) - 1) / (p.max_parts - 2);
+    int64_t min_chunk = (max_len + (p.max_parts - 2) - 1) / (p.max_parts - 2);
+    if (min_chunk < 4 * KB) min_chunk = 4 * KB;   // a block for each of the 4 waves
     if (chunk < min_chunk) chunk = min_chunk;
     chunk = (chunk + KB - 1) / KB * KB;
     if (chunk < KB) chunk = KB;

@@ -192,6 +192,31 @@ def test_few_query_split_k_row_tiles(nne, cuda, g, tq, tk, d):
     T.assert_close(got, T.ref_standard(q, k, v, False), what="few-query g=%d tq=%d" % (g, tq))
 
 
+@pytest.mark.parametrize("g,tq,tk,q_off,d", [
+    (1, 9, 1000, 991, 64),     # cached multi-token MHA step (bottom-right mask)
+    (4, 4, 700, 696, 128),     # GQA 4-token step, 16 rows
+    (2, 2, 300, 298, 128),     # 4 rows: the 4x4 tile
+    (1, 3, 40, 5, 64),         # only keys <= 7 visible to any row
+    (2, 8, 100, -3, 64),       # rows t < 3 see no key
+    (1, 16, 2000, 1984, 32),   # padded head dim
+    (4, 1, 500, 10, 128),      # one row: keys <= 10, no per-row mask
+])
+def test_few_query_causal_rows(nne, cuda, g, tq, tk, q_off, d):
+    """Causal problems with G*Tq <= 16 rows per KV head run on the split-K
+    kernel over the keys any row can see, masking key c > q_off + t per row
+    (llama.rs:277-292, attention.rs:101-108)."""
+    print("case causal few-query g=%d tq=%d tk=%d q_off=%d d=%d" % (g, tq, tk, q_off, d), flush=True)
+    hkv = 2
+    q = rnd(800 + g + tq, 2, hkv * g, tq, d)
+    k = rnd(801 + tk, 2, hkv, tk, d)
+    v = rnd(802 + d, 2, hkv, tk, d)
+    got = host(nne.attention_forward(dev(q, cuda), dev(k, cuda), dev(v, cuda), True, q_offset=q_off))
+    r0 = max(0, -q_off)
+    assert not got[:, :, :r0].any()
+    ref = T.ref_standard(q[:, :, r0:], k, v, True, start_pos=q_off + r0)
+    T.assert_close(got[:, :, r0:], ref, what="causal few-query g=%d tq=%d" % (g, tq))
+
+
 # Problems with fewer work items (4 row blocks of 32 rows) than CUs and at
 # least 4 key tiles split every item's key tiles into chunks, one workgroup
 # each; the last workgroup of an item merges the partial (max, sum, O)
