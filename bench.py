@@ -251,6 +251,31 @@ def decode_cpu_baseline(seed=0x5EED0003, n_seq=8, steps=16):
                       % (n_seq, int(lens.min()) - steps, int(lens.max()) - steps, steps, el)}
 
 
+def prologue_cpu_baseline(seed=0x5EED0014):
+    """Oracle decode prologue (llama.rs:226-235: q/k/v Linear with bias
+    order of linear.rs:47-57, head split, RotaryEmbedding::apply) for one
+    config-3 step (B = 32 rows, d_model 4096), single-threaded."""
+    import numpy as np
+    sys.path.insert(0, os.path.join(ROOT, "tests"))
+    import nne_testlib as T
+    b, hq, hkv, d = 32, 32, 8, 128
+    c = hq * d
+    rng = np.random.default_rng(seed)
+    x = rng.standard_normal((b, 1, c), dtype=np.float32)
+    w = [rng.standard_normal((h * d, c), dtype=np.float32) * (1.0 / c) ** 0.5 for h in (hq, hkv, hkv)]
+    cos, sin = T.ref_rope_tables(4200, d)
+    pos = rng.integers(512, 4097, size=b).astype(np.int32)
+    t0 = time.perf_counter()
+    T.ref_qkv_rope(x, w[0], w[1], w[2], None, None, None, cos, sin, pos, hq, hkv)
+    el = time.perf_counter() - t0
+    wbytes = (hq + 2 * hkv) * d * c * 4
+    return {"value": round(wbytes / el / 1e9, 3), "unit": "GB/s", "cores": 1, "kind": "port",
+            "sample": "one config-3 decode prologue (B = 32, d_model 4096, Hq = 32, Hkv = 8, "
+                      "d = 128) restated from llama.rs:226-235 (q/k/v projections, head split, "
+                      "RoPE; f32), one thread: %.2f s, %.2f GFLOP/s; GB/s of weights like the "
+                      "GPU line" % (el, 2.0 * b * c * (hq + 2 * hkv) * d / el / 1e9)}
+
+
 def bench_decode_layer(nne, torch, dev, steps=32, seed=0x5EED0013):
     """Config 3 as a GQA decode layer step (llama.rs:205-300, t = 1) minus
     the output GEMM: the fused projection + RoPE launch on packed weights
@@ -461,6 +486,8 @@ def main():
             del q, k, v, o
         print("bench: config3 decode layer step", file=sys.stderr, flush=True)
         extra.append(bench_decode_layer(nne, torch, dev))
+        if not args.no_cpu:
+            extra[-1]["cpu_baseline"] = prologue_cpu_baseline()
         line["other_configs"] = extra
     if not args.no_cpu:
         print("bench: cpu baseline", file=sys.stderr, flush=True)
