@@ -181,7 +181,7 @@ __device__ __forceinline__ void merge_head_records(const SplitKParams& p, int b,
                                                    int64_t s0, int n, float* w_s, unsigned* red_m,
                                                    float* red_l, int tid) {
     constexpr int EPT = ROWS * D / 256;   // output elements per thread (R <= ROWS)
-    constexpr int NPRE = EPT >= 8 ? 4 : 8;  // partials per element per round trip
+    constexpr int NPRE = EPT >= 8 ? 2 : 4;  // partials per element per round trip
     const int NR = n * p.R;
     const int RD = p.R * D;
     const float* o_src = p.ws_o + s0 * RD;
@@ -270,7 +270,8 @@ __device__ __forceinline__ void merge_head_records(const SplitKParams& p, int b,
 //     row, 64 / LPR keys per load), P is the broadcast A operand (one register
 //     holds the 16 keys' probabilities, regrouped through LDS); each key group
 //     accumulates its own partial O, summed once per segment.
-template <int D, bool APPEND, int ROWS>
+// MASK: causal rows (p.masked), compiled only into the variants that serve them.
+template <int D, bool APPEND, int ROWS, bool MASK = false>
 __global__ __launch_bounds__(256, 2) void splitk_kernel(const SplitKParams p) {
     constexpr bool NARROW = ROWS == 4;
     constexpr int KS = D + 4;            // LDS row stride (16-byte reads conflict-free)
@@ -487,7 +488,7 @@ __global__ __launch_bounds__(256, 2) void splitk_kernel(const SplitKParams p) {
 #pragma unroll
                 for (int r = 0; r < 4; ++r) s[r] = ok ? s[r] : kNegInf;
             }
-            if (p.masked && kb0 + KB - 1 > p.q_off) {   // causal rows: key <= q_off + t
+            if (MASK && kb0 + KB - 1 > p.q_off) {   // causal rows: key <= q_off + t
 #pragma unroll
                 for (int r = 0; r < 4; ++r)
                     s[r] = kb0 + col <= p.q_off + r % p.Tq ? s[r] : kNegInf;
@@ -541,7 +542,7 @@ __global__ __launch_bounds__(256, 2) void splitk_kernel(const SplitKParams p) {
 #pragma unroll
                 for (int r = 0; r < 4; ++r) s[r] = (kb0 + 4 * grp + r < key_end) ? s[r] : kNegInf;
             }
-            if (p.masked && kb0 + KB - 1 > p.q_off) {   // causal rows: key <= q_off + t
+            if (MASK && kb0 + KB - 1 > p.q_off) {   // causal rows: key <= q_off + t
                 const int last = p.q_off + col % p.Tq;
 #pragma unroll
                 for (int r = 0; r < 4; ++r) s[r] = (kb0 + 4 * grp + r <= last) ? s[r] : kNegInf;
@@ -775,8 +776,12 @@ hipError_t launch_splitk_d(const SplitKParams& p, hipStream_t stream) {
             hipLaunchKernelGGL((splitk_kernel<D, true, 4>), dim3(p.n_wg), dim3(256), 0, stream, p);
         else if (p.k_new)
             hipLaunchKernelGGL((splitk_kernel<D, true, 16>), dim3(p.n_wg), dim3(256), 0, stream, p);
+        else if (narrow && p.masked)
+            hipLaunchKernelGGL((splitk_kernel<D, false, 4, true>), dim3(p.n_wg), dim3(256), 0, stream, p);
         else if (narrow)
             hipLaunchKernelGGL((splitk_kernel<D, false, 4>), dim3(p.n_wg), dim3(256), 0, stream, p);
+        else if (p.masked)
+            hipLaunchKernelGGL((splitk_kernel<D, false, 16, true>), dim3(p.n_wg), dim3(256), 0, stream, p);
         else
             hipLaunchKernelGGL((splitk_kernel<D, false, 16>), dim3(p.n_wg), dim3(256), 0, stream, p);
         hipError_t e = hipGetLastError();
