@@ -416,11 +416,14 @@ def main():
                      "kernel_ms": round(kms, 4)},
     }
     del q, k, v, out
+    # CPU legs run after every GPU measurement: an idle GPU drops its clocks,
+    # and a launch timed right after seconds of host work would pay the ramp.
+    cpu_jobs = []
     if not args.no_decode:
         print("bench: config3 decode", file=sys.stderr, flush=True)
         line["decode"] = bench_decode(nne, torch, dev)
         if not args.no_cpu:
-            line["decode"]["cpu_baseline"] = decode_cpu_baseline()
+            cpu_jobs.append((line["decode"], decode_cpu_baseline))
     if args.all:
         extra = []
         g = torch.Generator(device=dev).manual_seed(0x5EED0001)
@@ -447,7 +450,7 @@ def main():
                         "frac": round(fl / (kms_c / 1e3) / 1e12 / PEAK_FP32_MATRIX_TFLOPS, 4)})
             if not args.no_cpu:
                 # Bounded samples of the same workload (a few seconds each).
-                rec["cpu_baseline"] = {
+                cpu_jobs.append((rec, {
                     "config1": lambda: flash_cpu_baseline(1, 4, 256, 64, True, 1.0,
                                                           "config 1 in full (B=1, H=4, T=256, d=64)",
                                                           reps=5),
@@ -457,7 +460,7 @@ def main():
                     "config5a": lambda: flash_cpu_baseline(1, 20, 1500, 64, False, 1.0,
                                                            "one of the 8 batch elements of "
                                                            "config 5a (H=20, T=1500, d=64)"),
-                }[name]()
+                }[name]))
             extra.append(rec)
             if name == "config5a":
                 # Three K/V sets (369 MB) rotated so no call finds its K/V in
@@ -481,16 +484,18 @@ def main():
                                       "behind a spin kernel so the GPU runs them back to back; "
                                       "host_paced = issued from Python one by one"})
                 if not args.no_cpu:
-                    extra[-1]["cpu_baseline"] = cross_cpu_baseline()
+                    cpu_jobs.append((extra[-1], cross_cpu_baseline))
                 del kvs
             del q, k, v, o
         print("bench: config3 decode layer step", file=sys.stderr, flush=True)
         extra.append(bench_decode_layer(nne, torch, dev))
         if not args.no_cpu:
-            extra[-1]["cpu_baseline"] = prologue_cpu_baseline()
+            cpu_jobs.append((extra[-1], prologue_cpu_baseline))
         line["other_configs"] = extra
     if not args.no_cpu:
         print("bench: cpu baseline", file=sys.stderr, flush=True)
+        for rec, job in cpu_jobs:
+            rec["cpu_baseline"] = job()
         line["cpu_baseline"] = cpu_baseline()
     print(json.dumps(line), flush=True)
 
