@@ -465,6 +465,9 @@ def main():
                 kms_c = gpu_ms_per_call(
                     torch, lambda i: nne.attention_forward(q, k, v, causal, out=o), 50, True)
                 rec["host_paced_kernel_ms"] = round(paced, 4)
+                # The floor any launch pays: an (almost) empty kernel, queued the same way.
+                rec["empty_kernel_ms"] = round(gpu_ms_per_call(
+                    torch, lambda i: torch.cuda._sleep(1), 50, True), 4)
             rec.update({"TFLOP/s": round(fl / (kms_c / 1e3) / 1e12, 3), "kernel_ms": round(kms_c, 4),
                         "frac": round(fl / (kms_c / 1e3) / 1e12 / PEAK_FP32_MATRIX_TFLOPS, 4)})
             if not args.no_cpu:
