@@ -71,8 +71,11 @@ int nne_flash_attention_forward(const float *q, const int64_t q_shape[4], const 
  * key c is visible to row r iff c <= r + q_offset (llama.rs uses
  * q_offset = start_pos, attention.rs uses Tk - Tq).  The reference's additive
  * -1e4 mask and this exact exclusion give identical f32 results whenever
- * |scores| < ~4e3.  Few-query problems (Hq/Hkv * Tq <= 16 rows per KV head
- * with every key visible) run on the split-K kernel. */
+ * |scores| < ~4e3.  Few-query problems (Hq/Hkv * Tq <= 16 rows per KV head,
+ * causal or not) run on the split-K kernel; problems with fewer work items
+ * than the device has CUs split their key range across workgroups.  Both use
+ * the library's per-stream workspace and counters (as nne_decode_attention
+ * with a NULL workspace); calls on one stream run in order. */
 int nne_attention_forward(const float *q, const int64_t q_shape[4], const int64_t q_strides[4],
                           const float *k, const int64_t k_shape[4], const int64_t k_strides[4],
                           const float *v, const int64_t v_shape[4], const int64_t v_strides[4],
