@@ -13,9 +13,9 @@
 // kernel is organised around streaming each KV head's cache exactly once and
 // keeping everything else off the critical path:
 //   * the (sequence, KV head, key) rows of the whole batch are flattened and
-//     cut into equal chunks, one per workgroup, launched as exactly one
-//     resident wave of workgroups: every CU streams the same number of bytes
-//     whatever the ragged lengths (per-head splits leave a long tail);
+//     cut into equal chunks, one per workgroup and one workgroup per CU:
+//     every CU streams the same number of bytes whatever the ragged lengths
+//     (per-head splits leave a long tail);
 //   * a workgroup serves all R = G * T_q <= 16 query rows that read a KV head,
 //     so grouped-query sharing costs no extra HBM traffic;
 //   * its 4 waves run independently over interleaved 16-key blocks (no
@@ -181,7 +181,7 @@ __device__ __forceinline__ void merge_head_records(const SplitKParams& p, int b,
                                                    int64_t s0, int n, float* w_s, unsigned* red_m,
                                                    float* red_l, int tid) {
     constexpr int EPT = ROWS * D / 256;   // output elements per thread (R <= ROWS)
-    constexpr int NPRE = EPT >= 8 ? 2 : 4;  // partials per element per round trip
+    constexpr int NPRE = EPT >= 16 ? 2 : 32 / EPT;   // partials per element per round trip
     const int NR = n * p.R;
     const int RD = p.R * D;
     const float* o_src = p.ws_o + s0 * RD;
@@ -848,36 +848,38 @@ SplitKWorkspace splitk_workspace_layout(int B, int Hkv, int R, int d) {
 
 namespace {
 
-// Resident workgroups of the split kernel on the current device: one full
-// wave of them covers the flattened key range exactly once.
-template <int D, bool APPEND, int ROWS>
-int resident_workgroups() {
+// Workgroups of a split launch: one per CU.  Measured on MI355X against one
+// per resident slot (2-3 per CU): the same at config-3 decode, and 4-13 %
+// faster where more than one fits (config-5b cross-attention 28.2 against
+// 32.6 us, d = 64 decode 59.5 against 61.8 us, B = 8 decode 40.1 against
+// 42.5 us): a CU serves the loads of its first workgroup ahead of the others,
+// so co-resident workgroups with equal chunks finish at different times,
+// and fewer chunks also mean fewer partial records to merge.
+int split_workgroups() {
     static int cached[64] = {0};
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
     if (cached[dev] == 0) {
-        int cus = 0, per_cu = 0;
-        if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+        int cus = 0;
+        if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus < 1)
             cus = 256;
-        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, splitk_kernel<D, APPEND, ROWS>, 256, 0) !=
-                hipSuccess || per_cu < 1)
-            per_cu = 1;
-        int n = cus * per_cu;
-        cached[dev] = n < MAX_WG ? n : MAX_WG;
+        cached[dev] = cus < MAX_WG ? cus : MAX_WG;
     }
     return cached[dev];
 }
 
 template <int D>
 hipError_t launch_flat(SplitKParams p, int64_t total_keys, int max_len, hipStream_t stream) {
-    const bool narrow = p.R <= 4;
-    const int slots = p.k_new ? (narrow ? resident_workgroups<D, true, 4>() : resident_workgroups<D, true, 16>())
-                              : (narrow ? resident_workgroups<D, false, 4>() : resident_workgroups<D, false, 16>());
+    const int slots = split_workgroups();
     // Equal flattened chunks, whole 16-key blocks, and at most max_parts
     // workgroups sharing any one head (a chunk boundary can add two).
     int64_t chunk = (total_keys + slots - 1) / (slots > 0 ? slots : 1);
     int64_t min_chunk = (max_len + (p.max_parts - 2) - 1) / (p.max_parts - 2);
     if (min_chunk < 4 * KB) min_chunk = 4 * KB;   // a block for each of the 4 waves
+    // At most ~8 workgroups per head: a small problem (few, short heads)
+    // otherwise splits into many short chunks whose records cost the merging
+    // workgroup more round trips than the extra keys per chunk cost to stream.
+    if (min_chunk < (max_len + 7) / 8) min_chunk = (max_len + 7) / 8;
     if (chunk < min_chunk) chunk = min_chunk;
     chunk = (chunk + KB - 1) / KB * KB;
     if (chunk < KB) chunk = KB;
