@@ -34,10 +34,10 @@ PEAK_HBM_GBS = 8000.0
 # the `--probe` workload, each scaled by its reading for a plain 1 GiB device copy
 # (FETCH_SIZE x2.00, WRITE_SIZE x1.00).  Config 2 prefill: 232.9 MB read + 134.2 MB
 # written (algorithmic 201.3 + 134.2; part of the shared K/V is fetched twice).
-# Config 3 decode step (one launch, split heads merged inside it): 648.1 MB read +
-# 3.1 MB written (algorithmic ~646 + 0.8, plus the partial records of split heads).
+# Config 3 decode step (one launch, split heads merged inside it): 646.7 MB read +
+# 2.2 MB written (algorithmic ~646 + 0.8, plus the partial records of split heads).
 TRAFFIC_PREFILL_CONFIG2 = round(232.9e6 + 134.2e6)
-TRAFFIC_DECODE_CONFIG3_STEP = round(648.1e6 + 3.1e6)
+TRAFFIC_DECODE_CONFIG3_STEP = round(646.7e6 + 2.2e6)
 
 
 def load_pkg():
