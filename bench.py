@@ -351,6 +351,71 @@ def bench_decode_layer(nne, torch, dev, steps=32, seed=0x5EED0013):
             "prologue_bytes": pbytes, "layer_step_ms": round(step_ms, 4)}
 
 
+def bench_mha_decode_layer(nne, torch, dev, steps=32, layers=12, seed=0x5EED0015):
+    """GPT-2-small-style MultiHeadAttention decode step (attention.rs:51-129
+    with t = 1; d_model 768, 12 heads, d = 64) for B = 32 sequences with
+    cached lengths U[128, 1024]: the fused biased q/k/v projection (no RoPE)
+    on packed weights, then the append + attend launch; the output GEMM is
+    left out.  The q/k/v weights of 12 layers rotate, as in the model."""
+    import numpy as np
+    b, h, d = 32, 12, 64
+    c = h * d
+    rng = np.random.default_rng(seed)
+    lens0 = rng.integers(128, 1025, size=b).astype(np.int32)
+    cap = 1024 + 2 * steps + 8
+    g = torch.Generator(device=dev).manual_seed(seed)
+    bound = (1.0 / c) ** 0.5
+    packed, biases = [], []
+    for _ in range(layers):
+        w = [(torch.rand(c, c, generator=g, device=dev) * 2 - 1) * bound for _ in range(3)]
+        packed.append(nne.qkv_pack(w[0], w[1], w[2], h, h))
+        biases.append([(torch.rand(c, generator=g, device=dev) * 2 - 1) * bound for _ in range(3)])
+        del w
+    cache = nne.KVCache(1, b, h, cap, d, device=dev)
+    cache.k[0].normal_(generator=g)
+    cache.v[0].normal_(generator=g)
+    xs = torch.randn(steps, b, c, generator=g, device=dev)
+    q = torch.empty(b, h, 1, d, device=dev)
+    kn = torch.empty(b, h, 1, d, device=dev)
+    vn = torch.empty(b, h, 1, d, device=dev)
+    out = torch.empty(b, h, 1, d, device=dev)
+    cache.set_lengths(0, lens0)
+
+    def prologue(i):
+        bq, bk, bv = biases[i % layers]
+        nne.qkv_rope(xs[i % steps], packed[i % layers], bq, bk, bv, None, None, None, h, h, q, kn,
+                     vn, head_dim=d)
+
+    def attend(i):
+        cache.decode_step(0, q, kn, vn, out=out)
+
+    def layer_step(i):
+        prologue(i)
+        attend(i)
+
+    for i in range(3):
+        prologue(i)
+    pro_ms = gpu_ms_per_call(torch, prologue, steps, queued=True)
+    cache.set_lengths(0, lens0)
+    att_ms = gpu_ms_per_call(torch, attend, steps, queued=True)
+    cache.set_lengths(0, lens0)
+    step_ms = gpu_ms_per_call(torch, layer_step, steps, queued=True)
+    kv_bytes = 0.0
+    for i in range(steps):
+        kv_bytes += float((lens0 + i + 1).sum()) * h * d * 4 * 2 + 2 * b * h * d * 4 + b * h * d * 8
+    kv_bytes /= steps
+    pbytes = 3 * c * c * 4 + 3 * c * 4 + b * c * 4 + 3 * b * c * 4
+    return {"workload": "GPT-2-small MHA decode layer step (d_model 768, 12 heads, d 64, B=32, "
+                        "L0~U[128,1024]): fused biased q/k/v projection (12 layers' weights "
+                        "rotated) + append/attend",
+            "prologue_ms": round(pro_ms, 4),
+            "prologue_GB/s": round(pbytes / (pro_ms / 1e3) / 1e9, 1),
+            "attend_ms": round(att_ms, 4),
+            "attend_GB/s": round(kv_bytes / (att_ms / 1e3) / 1e9, 1),
+            "attend_frac_hbm": round(kv_bytes / (att_ms / 1e3) / 1e9 / PEAK_HBM_GBS, 4),
+            "layer_step_ms": round(step_ms, 4)}
+
+
 def probe(nne, torch, dev):
     """Fixed, short workload for rocprofv3 --pmc runs (one counter set per run)."""
     x = torch.empty(1 << 28, dtype=torch.float32, device=dev)     # 1 GiB
@@ -513,6 +578,8 @@ def main():
         extra.append(bench_decode_layer(nne, torch, dev))
         if not args.no_cpu:
             cpu_jobs.append((extra[-1], prologue_cpu_baseline))
+        print("bench: MHA decode layer step", file=sys.stderr, flush=True)
+        extra.append(bench_mha_decode_layer(nne, torch, dev))
         line["other_configs"] = extra
     if not args.no_cpu:
         print("bench: cpu baseline", file=sys.stderr, flush=True)
