@@ -30,7 +30,7 @@ enum {
     NNE_EHIP = 4       /* HIP runtime failure            -> EngineError::GpuError (src/error.rs:48) */
 };
 
-#define NNE_ABI_VERSION 2
+#define NNE_ABI_VERSION 3
 
 int nne_abi_version(void);
 
@@ -46,6 +46,15 @@ int nne_memcpy_h2d(void *dst, const void *src, uint64_t bytes, void *stream);
 int nne_memcpy_d2h(void *dst, const void *src, uint64_t bytes, void *stream);
 int nne_memcpy_d2d(void *dst, const void *src, uint64_t bytes, void *stream);
 int nne_stream_sync(void *stream);
+/* Frees the workspace and arrival counters the library keeps for `stream` on
+ * the current device (used by nne_attention_forward and
+ * nne_flash_attention_forward on small or few-query problems, by the decode
+ * entry points with a NULL workspace and by nne_qkv_rope), after waiting for
+ * the stream.  Call it before destroying a stream the library has used; a
+ * later call on the stream allocates them again.  No counterpart in the
+ * reference, whose CPU path allocates per call: it is for long-running
+ * callers that create and destroy streams. */
+int nne_stream_release(void *stream);
 
 /* ---- prefill -------------------------------------------------------------
  * Replaces `flash_attention_forward(q, k, v, is_causal, scale, block_size_r,

@@ -75,6 +75,7 @@ SIGNATURES = {
     "nne_memcpy_d2h": (ctypes.c_int, [_vp, _vp, ctypes.c_uint64, _vp]),
     "nne_memcpy_d2d": (ctypes.c_int, [_vp, _vp, ctypes.c_uint64, _vp]),
     "nne_stream_sync": (ctypes.c_int, [_vp]),
+    "nne_stream_release": (ctypes.c_int, [_vp]),
     "nne_flash_attention_forward": (ctypes.c_int, [
         _vp, _i64p, _i64p, _vp, _i64p, _i64p, _vp, _i64p, _i64p, _vp, _i64p,
         ctypes.c_int, ctypes.c_int, ctypes.c_float, ctypes.c_int64, ctypes.c_int64, _vp]),
@@ -140,6 +141,13 @@ def _stream(stream=None):
     import torch
     s = stream if stream is not None else torch.cuda.current_stream()
     return ctypes.c_void_p(s.cuda_stream)
+
+
+def release_stream(stream=None):
+    """Frees the workspace and counters the library keeps for ``stream``
+    (default: the current stream) after waiting for it; the next call on the
+    stream allocates them again."""
+    check(lib().nne_stream_release(_stream(stream)))
 
 
 def _require_f32_cuda(*ts):

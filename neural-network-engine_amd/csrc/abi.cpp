@@ -304,6 +304,27 @@ int nne_stream_sync(void* stream) {
     return e == hipSuccess ? NNE_OK : hip_fail(e, "hipStreamSynchronize");
 }
 
+int nne_stream_release(void* stream) {
+    const hipStream_t s = as_stream(stream);
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
+    const std::thread::id th =
+        s == hipStreamPerThread ? std::this_thread::get_id() : std::thread::id();
+    e = hipStreamSynchronize(s);
+    if (e != hipSuccess) return hip_fail(e, "hipStreamSynchronize");
+    std::lock_guard<std::mutex> lock(g_res_mu);
+    for (size_t i = 0; i < g_res.size(); ++i) {
+        StreamResources& r = g_res[i];
+        if (r.dev != dev || r.stream != s || r.thread != th) continue;
+        if (r.counters) e = hipFree(r.counters);
+        if (e == hipSuccess && r.ws) e = hipFree(r.ws);
+        g_res.erase(g_res.begin() + (std::ptrdiff_t)i);
+        return e == hipSuccess ? NNE_OK : hip_fail(e, "hipFree");
+    }
+    return NNE_OK;
+}
+
 int nne_flash_attention_forward(const float* q, const int64_t q_shape[4], const int64_t q_strides[4],
                                 const float* k, const int64_t k_shape[4], const int64_t k_strides[4],
                                 const float* v, const int64_t v_shape[4], const int64_t v_strides[4],

@@ -22,7 +22,7 @@ def test_library_exports_header_symbols(nne):
     for name in declared:
         assert hasattr(lib, name), name
         assert name in nne.SIGNATURES, name
-    assert lib.nne_abi_version() == 2
+    assert lib.nne_abi_version() == 3
 
 
 def test_flash_shape_mismatch_is_shape_error(nne):

@@ -295,3 +295,21 @@ def test_flash_layer_matches_composition(nne, cuda):
     v = lin(layer.v_proj, xs).reshape(b, t, 4, 16).transpose(0, 2, 1, 3)
     core = T.ref_flash(q, k, v, True).transpose(0, 2, 1, 3).reshape(b, t, c)
     T.assert_close(got, lin(layer.out_proj, core), atol=2e-4, rtol=2e-3, what="layer")
+
+
+def test_stream_release_frees_and_reallocates(nne, cuda):
+    """nne_stream_release drops a stream's workspace and counters; the next
+    call on the stream allocates them again and gives the same result."""
+    import torch
+    s = torch.cuda.Stream(device=cuda)
+    q, k, v = (dev(rnd(400 + i, 1, 4, 256, 64), cuda) for i in range(3))   # key-split path
+    torch.cuda.synchronize()
+    with torch.cuda.stream(s):
+        a = nne.attention_forward(q, k, v, True, stream=s)
+    nne.release_stream(s)
+    nne.release_stream(s)                       # nothing left to free: still OK
+    with torch.cuda.stream(s):
+        b = nne.attention_forward(q, k, v, True, stream=s)
+    s.synchronize()
+    assert np.array_equal(host(a), host(b))
+    T.assert_close(host(b), T.ref_flash(host(q), host(k), host(v), True), what="after release")
