@@ -144,16 +144,21 @@ __global__ __launch_bounds__(256, (SPLIT && D >= 128) ? 1 : 2) void prefill_mfma
 
 #pragma nounroll
     for (int j = 0;; ++j) {
-    int head = 0, wgi = 0, chunk = 0;
+    int head = 0, wgi = 0, chunk = 0, pair = 0;
     int n_parts = 1;
     if constexpr (SPLIT) {
-        // Key split, one step only: the (item, chunk) pairs of a head are
-        // numbered contiguously, so consecutive workgroups (dealt to the 8
-        // XCDs in turn) carry equal work.
+        // Key split, one step only.  The (item, chunk) pairs are numbered
+        // contiguously per head; XCD x (= workgroup id % 8, the hardware's
+        // dealing order) takes the x-th eighth of that list, so the chunks of
+        // an item share one L2 (they all read the item's Q).
         if (j > 0) break;
         const int per_head = p.part_prefix[p.n_wg];
-        head = blockIdx.x / per_head;
-        const int r = blockIdx.x % per_head;
+        const int pairs = p.B * p.Hkv * per_head;
+        const int ppx = (pairs + 7) >> 3;
+        pair = (blockIdx.x & 7) * ppx + (blockIdx.x >> 3);
+        if (pair >= pairs) break;
+        head = pair / per_head;
+        const int r = pair % per_head;
         int lo = 0, hi = p.n_wg - 1;     // last item with part_prefix <= r
         while (lo < hi) {
             const int mid = (lo + hi + 1) >> 1;
@@ -355,16 +360,16 @@ __global__ __launch_bounds__(256, (SPLIT && D >= 128) ? 1 : 2) void prefill_mfma
             // Partial record of this chunk, lane-major so that every store and
             // load is one coalesced wave access: O^T registers at
             // ws[grid*512 + ((slot*4 + wave)*(D/2) + i)*64 + lane] and
-            // (max, sum) at ws[((slot*4 + wave)*64 + lane)*2], slot = blockIdx.
+            // (max, sum) at ws[((slot*4 + wave)*64 + lane)*2], slot = pair.
             const int item = head * p.n_wg + wgi;
             const int64_t o_base = (int64_t)gridDim.x * 512;
             {
-                float* wo = p.ws + o_base + ((int64_t)blockIdx.x * 4 + wave) * (D / 2) * 64 + lane;
+                float* wo = p.ws + o_base + ((int64_t)pair * 4 + wave) * (D / 2) * 64 + lane;
 #pragma unroll
                 for (int b = 0; b < NB; ++b)
 #pragma unroll
                     for (int r = 0; r < 16; ++r) store_coherent(wo + (b * 16 + r) * 64, o[b][r]);
-                float* wml = p.ws + (((int64_t)blockIdx.x * 4 + wave) * 64 + lane) * 2;
+                float* wml = p.ws + (((int64_t)pair * 4 + wave) * 64 + lane) * 2;
                 store_coherent(wml, m_run);
                 store_coherent(wml + 1, l_tot);
             }
@@ -388,7 +393,7 @@ __global__ __launch_bounds__(256, (SPLIT && D >= 128) ? 1 : 2) void prefill_mfma
             for (int b = 0; b < NB; ++b)
 #pragma unroll
                 for (int r = 0; r < 16; ++r) o[b][r] = 0.f;
-            const int slot0 = blockIdx.x - chunk;
+            const int slot0 = pair - chunk;
             for (int i = 0; i < n_parts; i += GRP) {
                 float mc[GRP], lc[GRP], oc[GRP][D / 2];
 #pragma unroll
@@ -478,7 +483,7 @@ template <int D, bool CAUSAL, bool VEC>
 hipError_t launch_t(PrefillParams p, hipStream_t stream) {
     if (p.n_chunks > 1 && p.ws && p.cnt) {
         hipLaunchKernelGGL((prefill_mfma_kernel<D, CAUSAL, VEC, true>),
-                           dim3(p.B * p.Hkv * p.part_prefix[p.n_wg]), dim3(256), 0, stream, p);
+                           dim3(8 * ((p.B * p.Hkv * p.part_prefix[p.n_wg] + 7) / 8)), dim3(256), 0, stream, p);
         return hipGetLastError();
     }
     int cus = 0, k_max = 0;
@@ -502,28 +507,6 @@ hipError_t launch_t(PrefillParams p, hipStream_t stream) {
     if (S >= p.per_xcd || (double)p.per_xcd / ((double)best_rounds * S) < 0.97) S = p.per_xcd;
     hipLaunchKernelGGL((prefill_mfma_kernel<D, CAUSAL, VEC, false>), dim3(8 * S), dim3(256), 0, stream, p);
     return hipGetLastError();
-}
-
-// Resident workgroups per CU of the key-split variant (cached per device).
-template <int D, bool CAUSAL, bool VEC>
-int split_per_cu() {
-    static int cached[64] = {0};
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
-    if (cached[dev] == 0) {
-        int k = 0;
-        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&k, prefill_mfma_kernel<D, CAUSAL, VEC, true>, 256,
-                                                         0) != hipSuccess || k < 1)
-            k = 1;
-        cached[dev] = k;
-    }
-    return cached[dev];
-}
-
-template <int D>
-int split_per_cu_d(bool causal, bool vec) {
-    if (causal) return vec ? split_per_cu<D, true, true>() : split_per_cu<D, true, false>();
-    return vec ? split_per_cu<D, false, true>() : split_per_cu<D, false, false>();
 }
 
 template <int D>
@@ -568,10 +551,11 @@ int device_cus() {
 
 // A problem with fewer work items than CUs leaves most SIMDs idle, and its
 // time is the longest item's chain of key tiles.  Cutting every item's tiles
-// into chunks of at least 2 tiles, sized so that the chunks fill one resident
-// round of the split kernel (at most 16 chunks per item), shortens that chain
-// to one chunk plus the merge of the item's records.
+// into chunks of at least 2 tiles, sized so that the chunks fill the CUs once
+// (at most 16 chunks per item), shortens that chain to one chunk plus the
+// merge of the item's records.
 PrefillSplit prefill_split_plan(PrefillParams& p, bool causal, bool vec) {
+    (void)vec;
     PrefillSplit r{0, 0};
     p.n_chunks = 0;
     p.chunk_tiles = 0;
@@ -594,10 +578,10 @@ PrefillSplit prefill_split_plan(PrefillParams& p, bool causal, bool vec) {
         max_t = std::max(max_t, tiles[w]);
     }
     if (max_t < 4) return r;
-    const int per_cu = D == 32 ? split_per_cu_d<32>(causal, vec)
-                     : D == 64 ? split_per_cu_d<64>(causal, vec)
-                               : split_per_cu_d<128>(causal, vec);
-    const int64_t slots = (int64_t)cus * per_cu;
+    // One workgroup per CU: measured against two per CU where they fit (d = 64),
+    // the longer chunks with half the records and prologues are faster
+    // (GPT-2 prompt, T = 1024: 33.9 against 31.0 us).
+    const int64_t slots = cus;
     // Smallest chunk (>= 2 tiles, <= 16 chunks per item) whose non-empty
     // chunks fit in one resident round.
     int ch = std::max(2, (max_t + 15) / 16);
@@ -614,7 +598,7 @@ PrefillSplit prefill_split_plan(PrefillParams& p, bool causal, bool vec) {
     for (int w = 0; w < p.n_wg; ++w)
         p.part_prefix[w + 1] = (uint16_t)(p.part_prefix[w] + std::max(1, (tiles[w] + ch - 1) / ch));
     // Per workgroup: (max, sum) of 4 waves x 64 lanes, and 4 x D/2 x 64 O values.
-    const uint64_t grid = (uint64_t)p.B * p.Hkv * p.part_prefix[p.n_wg];
+    const uint64_t grid = ((uint64_t)p.B * p.Hkv * p.part_prefix[p.n_wg] + 7) / 8 * 8;
     r.ws_bytes = grid * (512 + 128 * (uint64_t)D) * 4;
     r.n_counters = p.total;
     return r;
