@@ -284,6 +284,7 @@ __global__ __launch_bounds__(256, 2) void splitk_kernel(const SplitKParams p) {
     constexpr int OS = D + 4;            // merge-buffer row stride (rows start 4 banks apart)
     constexpr int NQN = D / 16;          // narrow: Q registers per lane
     constexpr int CBV = D == 128 ? 3 : 2;  // narrow: PV broadcast group (LPR / 4 blocks)
+    constexpr int DEPTH = 2;             // K/V blocks held in registers per wave
     static_assert(ROWS == 16 || ROWS == 4, "row tile");
     static_assert(4 * ROWS * OS <= 4 * KB * KS, "merge buffer must fit in the K slices");
     static_assert(NK == 4 * NH, "K and V loads per block");
@@ -578,22 +579,32 @@ __global__ __launch_bounds__(256, 2) void splitk_kernel(const SplitKParams p) {
           }
         };
 
-        // Ping-pong over this wave's blocks (wave, wave+4, ...): while one
-        // block computes, the next one's loads are in flight.
-        // The loop has a single exit at its end, which lets the next block's
-        // loads issue before the wait for the current block's data.
+        // Ring of DEPTH register buffers over this wave's blocks (wave,
+        // wave+4, ...): while one block computes, the next DEPTH-1 blocks'
+        // loads are in flight.  The loop has a single exit at its end, which
+        // lets the next blocks' loads issue before the wait for the current
+        // block's data.  At d = 64 (8 KB of K/V per 16-key block) 3 and 4
+        // buffers measured slower than 2: cross-attention over 1500 frames
+        // 29.6 and 30.5 against 28.9 us, GPT-2 decode attend 35.0 and 35.3
+        // against 32.5 us.
         const int n_blocks = (key_end - key_begin + KB - 1) / KB;
         const int n_mine = wave < n_blocks ? (n_blocks - wave + 3) / 4 : 0;
-        vf4 ka[NK], va[4 * NH], kb2[NK], vb2[4 * NH];
-        load_block(ka, va, key_begin + wave * KB);
+        vf4 kq[DEPTH][NK], vq[DEPTH][4 * NH];
         int kb0 = key_begin + wave * KB;
-        for (int i = 0; i + 2 <= n_mine; i += 2, kb0 += 8 * KB) {
-            load_block(kb2, vb2, kb0 + 4 * KB);
-            block(ka, va, kb0);
-            load_block(ka, va, kb0 + 8 * KB);
-            block(kb2, vb2, kb0 + 4 * KB);
+#pragma unroll
+        for (int s = 0; s + 1 < DEPTH; ++s) load_block(kq[s], vq[s], kb0 + 4 * KB * s);
+        int done = 0;
+        for (; done + DEPTH <= n_mine; done += DEPTH, kb0 += 4 * KB * DEPTH) {
+#pragma unroll
+            for (int s = 0; s < DEPTH; ++s) {
+                load_block(kq[(s + DEPTH - 1) % DEPTH], vq[(s + DEPTH - 1) % DEPTH],
+                           kb0 + 4 * KB * (s + DEPTH - 1));
+                block(kq[s], vq[s], kb0 + 4 * KB * s);
+            }
         }
-        if (n_mine & 1) block(ka, va, kb0);
+#pragma unroll
+        for (int s = 0; s + 1 < DEPTH; ++s)
+            if (done + s < n_mine) block(kq[s], vq[s], kb0 + 4 * KB * s);
         if (NARROW && has_new && wave == 0 && lane < LPR && 4 * lane < p.d) {
             const int row = Lb - 1;
             *reinterpret_cast<vf4*>(const_cast<float*>(kb) + row * kst + 4 * lane) = nk;
