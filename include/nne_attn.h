@@ -12,6 +12,14 @@
  * Return value: NNE_OK or an error code that maps onto the reference's
  * EngineError (src/error.rs:6-58); nne_last_error() returns the message of the
  * calling thread's last failure.  No call aborts the process.
+ *
+ * Threads: any entry point may be called from several threads at once, as the
+ * reference's functions may (Module: Send + Sync, src/nn/module.rs:7).  Calls
+ * on one stream, from one thread or several (the NULL stream is shared by
+ * all threads), run in that stream's order and share the workspace and
+ * counters the library keeps for it.  The caller orders calls that write the
+ * same output or the same KV cache, and calls nne_stream_release only when no
+ * other call uses that stream.
  */
 #ifndef NNE_ATTN_H
 #define NNE_ATTN_H

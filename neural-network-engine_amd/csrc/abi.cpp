@@ -66,9 +66,12 @@ bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) ==
 //   * arrival counters of the in-launch combine, zeroed by a fill kernel when
 //     allocated and left zeroed by every launch;
 //   * the workspace used when the caller passes none.
-// Both grow on demand (stream-ordered allocation; the replaced buffer is freed
-// in stream order after the launches queued before it) and are kept until the
-// process ends.
+// Both grow on demand (stream-ordered allocation).  A replaced buffer is
+// retired, not freed: another thread that took it for a launch on the same
+// stream (the null stream is shared by all threads) may not have queued that
+// launch yet.  Sizes double, so the retired buffers together are smaller than
+// the live one.  Everything is kept until nne_stream_release or the end of
+// the process.
 struct StreamResources {
     int dev;
     hipStream_t stream;
@@ -77,6 +80,7 @@ struct StreamResources {
     int64_t n_counters;
     void* ws;
     uint64_t ws_bytes;
+    std::vector<void*> retired;
 };
 std::mutex g_res_mu;
 std::vector<StreamResources> g_res;
@@ -94,7 +98,7 @@ hipError_t stream_resources(int64_t n, uint64_t ws_bytes, hipStream_t s, uint32_
     for (auto& x : g_res)
         if (x.dev == dev && x.stream == s && x.thread == th) r = &x;
     if (!r) {
-        g_res.push_back(StreamResources{dev, s, th, nullptr, 0, nullptr, 0});
+        g_res.push_back(StreamResources{dev, s, th, nullptr, 0, nullptr, 0, {}});
         r = &g_res.back();
     }
     if (r->n_counters < n) {
@@ -105,7 +109,7 @@ hipError_t stream_resources(int64_t n, uint64_t ws_bytes, hipStream_t s, uint32_
         if (e != hipSuccess) return e;
         e = nne::zero_counters(p, cap, s);
         if (e != hipSuccess) return e;
-        if (r->counters) (void)hipFreeAsync(r->counters, s);
+        if (r->counters) r->retired.push_back(r->counters);
         r->counters = p;
         r->n_counters = cap;
     }
@@ -117,7 +121,7 @@ hipError_t stream_resources(int64_t n, uint64_t ws_bytes, hipStream_t s, uint32_
             void* p = nullptr;
             e = hipMallocAsync(&p, cap, s);
             if (e != hipSuccess) return e;
-            if (r->ws) (void)hipFreeAsync(r->ws, s);
+            if (r->ws) r->retired.push_back(r->ws);
             r->ws = p;
             r->ws_bytes = cap;
         }
@@ -319,6 +323,8 @@ int nne_stream_release(void* stream) {
         if (r.dev != dev || r.stream != s || r.thread != th) continue;
         if (r.counters) e = hipFree(r.counters);
         if (e == hipSuccess && r.ws) e = hipFree(r.ws);
+        for (void* old : r.retired)
+            if (e == hipSuccess) e = hipFree(old);
         g_res.erase(g_res.begin() + (std::ptrdiff_t)i);
         return e == hipSuccess ? NNE_OK : hip_fail(e, "hipFree");
     }

@@ -215,10 +215,24 @@ __device__ __forceinline__ void merge_head_records(const SplitKParams& p, int b,
             const float M = float_unorder(red_m[e % p.R]);
             const float f = fast_exp2(mv[k] - (M == kNegInf ? 0.f : M));
             w_s[e] = f;
-            atomicAdd(red_l + e % p.R, f * lv[k]);
+            w_s[1024 + e] = f * lv[k];
         }
     }
     __syncthreads();
+    // Denominators in a fixed order: 16 lanes per row (record c to lane
+    // c % 16), then a butterfly over the 16, so repeated calls give the same
+    // bits whichever workgroup merges and however its waves are scheduled.
+    {
+        const int rr = tid >> 4, part = tid & 15;
+        float l = 0.f;
+        if (rr < p.R)
+            for (int c = part; c < n; c += 16) l += w_s[1024 + c * p.R + rr];
+        l += __shfl_xor(l, 1, 16);
+        l += __shfl_xor(l, 2, 16);
+        l += __shfl_xor(l, 4, 16);
+        l += __shfl_xor(l, 8, 16);
+        if (rr < p.R && part == 0) red_l[rr] = l;
+    }
     float acc[EPT];
 #pragma unroll
     for (int j = 0; j < EPT; ++j) {
@@ -245,6 +259,7 @@ __device__ __forceinline__ void merge_head_records(const SplitKParams& p, int b,
                 if (c0 + c < n && tid + 256 * j < RD) acc[j] += w_s[(c0 + c) * p.R + rr] * pre[j][c];
         }
     }
+    __syncthreads();                      // red_l complete
 #pragma unroll
     for (int j = 0; j < EPT; ++j) {
         const int e = tid + 256 * j;
@@ -287,6 +302,7 @@ __global__ __launch_bounds__(256, 2) void splitk_kernel(const SplitKParams p) {
     constexpr int DEPTH = 2;             // K/V blocks held in registers per wave
     static_assert(ROWS == 16 || ROWS == 4, "row tile");
     static_assert(4 * ROWS * OS <= 4 * KB * KS, "merge buffer must fit in the K slices");
+    static_assert(2048 <= 4 * KB * KS, "merge weights (2 x 1024) must fit in the K slices");
     static_assert(NK == 4 * NH, "K and V loads per block");
 
     __shared__ __attribute__((aligned(16))) float lds[4 * KB * KS];
