@@ -4,6 +4,7 @@
 // and fills the launch-parameter structs; it never computes attention itself.
 // There is no CPU fallback: every compute entry point either launches a HIP
 // kernel or returns an error.
+#include <atomic>
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -640,17 +641,17 @@ int check_qkv_geometry(int64_t C, int64_t Hq, int64_t Hkv, int64_t d) {
 }
 
 int device_cus() {
-    static int cached[64] = {0};
+    static std::atomic<int> cached[64];   // callers on several threads may fill it at once
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
-    if (cached[dev] == 0) {
-        int cus = 0;
+    int cus = cached[dev].load(std::memory_order_relaxed);
+    if (cus == 0) {
         if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
             cus <= 0)
             cus = 256;
-        cached[dev] = cus;
+        cached[dev].store(cus, std::memory_order_relaxed);
     }
-    return cached[dev];
+    return cus;
 }
 
 }  // namespace

@@ -36,6 +36,7 @@
 // finish folds the partial (max, sum, O) records in chunk order (the same
 // combine as the online softmax, so the result is independent of arrival
 // order) and writes O.
+#include <atomic>
 #include <utility>
 #include <vector>
 
@@ -456,20 +457,22 @@ __global__ __launch_bounds__(256, (SPLIT && D >= 128) ? 1 : 2) void prefill_mfma
 template <int D, bool CAUSAL, bool VEC>
 void residency(int& cus, int& per_cu) {
     constexpr auto kernel = prefill_mfma_kernel<D, CAUSAL, VEC, false>;
-    static int cached_cus[64] = {0}, cached_per[64] = {0};
+    // Atomic: callers on several threads may fill the cache at once.
+    static std::atomic<int> cached_cus[64], cached_per[64];
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
-    if (cached_cus[dev] == 0) {
-        int c = 0, k = 0;
+    int c = cached_cus[dev].load(std::memory_order_acquire);
+    int k = cached_per[dev].load(std::memory_order_relaxed);
+    if (c == 0 || k == 0) {
         if (hipDeviceGetAttribute(&c, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || c < 8) c = 256;
         if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&k, kernel, 256, 0) !=
                 hipSuccess || k < 1)
             k = 1;
-        cached_per[dev] = k;
-        cached_cus[dev] = c;
+        cached_per[dev].store(k, std::memory_order_relaxed);
+        cached_cus[dev].store(c, std::memory_order_release);
     }
-    cus = cached_cus[dev];
-    per_cu = cached_per[dev];
+    cus = c;
+    per_cu = k;
 }
 
 // One resident wave of persistent workgroups: k per CU on every CU (an
@@ -535,16 +538,16 @@ void derive_schedule(PrefillParams& p) {
 }
 
 int device_cus() {
-    static int cached[64] = {0};
+    static std::atomic<int> cached[64];
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
-    if (cached[dev] == 0) {
-        int c = 0;
+    int c = cached[dev].load(std::memory_order_relaxed);
+    if (c == 0) {
         if (hipDeviceGetAttribute(&c, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || c < 8)
             c = 256;
-        cached[dev] = c;
+        cached[dev].store(c, std::memory_order_relaxed);
     }
-    return cached[dev];
+    return c;
 }
 
 }  // namespace

@@ -43,6 +43,7 @@
 //     kernel).
 // The hand-off uses per-access coherence rather than fences: on gfx950 an
 // agent-scope fence is a whole-L2 writeback and invalidate.
+#include <atomic>
 #include <algorithm>
 #include <utility>
 
@@ -883,16 +884,18 @@ namespace {
 // so co-resident workgroups with equal chunks finish at different times,
 // and fewer chunks also mean fewer partial records to merge.
 int split_workgroups() {
-    static int cached[64] = {0};
+    static std::atomic<int> cached[64];   // callers on several threads may fill it at once
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
-    if (cached[dev] == 0) {
+    int n = cached[dev].load(std::memory_order_relaxed);
+    if (n == 0) {
         int cus = 0;
         if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus < 1)
             cus = 256;
-        cached[dev] = cus < MAX_WG ? cus : MAX_WG;
+        n = cus < MAX_WG ? cus : MAX_WG;
+        cached[dev].store(n, std::memory_order_relaxed);
     }
-    return cached[dev];
+    return n;
 }
 
 template <int D>
