@@ -554,9 +554,9 @@ int device_cus() {
 
 // A problem with fewer work items than CUs leaves most SIMDs idle, and its
 // time is the longest item's chain of key tiles.  Cutting every item's tiles
-// into chunks of at least 2 tiles, sized so that the chunks fill the CUs once
-// (at most 16 chunks per item), shortens that chain to one chunk plus the
-// merge of the item's records.
+// into chunks, sized so that the chunks fill the CUs once (at most 16 chunks
+// per item), shortens that chain to one chunk plus the merge of the item's
+// records.
 PrefillSplit prefill_split_plan(PrefillParams& p, bool causal, bool vec) {
     (void)vec;
     PrefillSplit r{0, 0};
@@ -585,9 +585,11 @@ PrefillSplit prefill_split_plan(PrefillParams& p, bool causal, bool vec) {
     // the longer chunks with half the records and prologues are faster
     // (GPT-2 prompt, T = 1024: 33.9 against 31.0 us).
     const int64_t slots = cus;
-    // Smallest chunk (>= 2 tiles, <= 16 chunks per item) whose non-empty
-    // chunks fit in one resident round.
-    int ch = std::max(2, (max_t + 15) / 16);
+    // Smallest chunk (<= 16 chunks per item) whose non-empty chunks fill the
+    // CUs at most once.  One-tile chunks, where they fit, beat two-tile ones
+    // (config 1: 12.4 against 13.0 us): the chain of tiles halves, the merge
+    // grows by one round trip.
+    int ch = std::max(1, (max_t + 15) / 16);
     for (;; ++ch) {
         int64_t n = 0;
         for (int w = 0; w < p.n_wg; ++w) n += std::max(1, (tiles[w] + ch - 1) / ch);

@@ -220,7 +220,7 @@ def test_few_query_causal_rows(nne, cuda, g, tq, tk, q_off, d):
 # Problems with fewer work items (4 row blocks of 32 rows) than CUs and at
 # least 4 key tiles split every item's key tiles into chunks, one workgroup
 # each; the last workgroup of an item merges the partial (max, sum, O)
-# records.  Cases: config 1 (2 and 4 chunks), one item of 16 chunks (cached
+# records.  Cases: config 1 (4 and 8 one-tile chunks), one item of 16 chunks (cached
 # multi-token step), the 16-chunk cap with an odd number of records to fold,
 # GQA through strided [B, T, H, d] views on the scalar path, a negative
 # offset (rows without keys), a padded head dim.
