@@ -356,7 +356,10 @@ def bench_mha_decode_layer(nne, torch, dev, steps=32, layers=12, seed=0x5EED0015
     with t = 1; d_model 768, 12 heads, d = 64) for B = 32 sequences with
     cached lengths U[128, 1024]: the fused biased q/k/v projection (no RoPE)
     on packed weights, then the append + attend launch; the output GEMM is
-    left out.  The q/k/v weights of 12 layers rotate, as in the model."""
+    left out.  The q/k/v weights of 12 layers rotate, as in the model, and
+    so do 3 layers' KV caches (3 x 217 MB at capacity, past the 256 MB MALL;
+    with one cache re-read every step, loads that allocate in the MALL would
+    find it there, which a 12-layer model never does)."""
     import numpy as np
     b, h, d = 32, 12, 64
     c = h * d
@@ -371,15 +374,22 @@ def bench_mha_decode_layer(nne, torch, dev, steps=32, layers=12, seed=0x5EED0015
         packed.append(nne.qkv_pack(w[0], w[1], w[2], h, h))
         biases.append([(torch.rand(c, generator=g, device=dev) * 2 - 1) * bound for _ in range(3)])
         del w
-    cache = nne.KVCache(1, b, h, cap, d, device=dev)
-    cache.k[0].normal_(generator=g)
-    cache.v[0].normal_(generator=g)
+    n_kv = 3
+    cache = nne.KVCache(n_kv, b, h, cap, d, device=dev)
+    for layer in range(n_kv):
+        cache.k[layer].normal_(generator=g)
+        cache.v[layer].normal_(generator=g)
     xs = torch.randn(steps, b, c, generator=g, device=dev)
     q = torch.empty(b, h, 1, d, device=dev)
     kn = torch.empty(b, h, 1, d, device=dev)
     vn = torch.empty(b, h, 1, d, device=dev)
     out = torch.empty(b, h, 1, d, device=dev)
-    cache.set_lengths(0, lens0)
+
+    def reset():
+        for layer in range(n_kv):
+            cache.set_lengths(layer, lens0)
+
+    reset()
 
     def prologue(i):
         bq, bk, bv = biases[i % layers]
@@ -387,7 +397,7 @@ def bench_mha_decode_layer(nne, torch, dev, steps=32, layers=12, seed=0x5EED0015
                      vn, head_dim=d)
 
     def attend(i):
-        cache.decode_step(0, q, kn, vn, out=out)
+        cache.decode_step(i % n_kv, q, kn, vn, out=out)
 
     def layer_step(i):
         prologue(i)
@@ -396,18 +406,18 @@ def bench_mha_decode_layer(nne, torch, dev, steps=32, layers=12, seed=0x5EED0015
     for i in range(3):
         prologue(i)
     pro_ms = gpu_ms_per_call(torch, prologue, steps, queued=True)
-    cache.set_lengths(0, lens0)
+    reset()
     att_ms = gpu_ms_per_call(torch, attend, steps, queued=True)
-    cache.set_lengths(0, lens0)
+    reset()
     step_ms = gpu_ms_per_call(torch, layer_step, steps, queued=True)
     kv_bytes = 0.0
-    for i in range(steps):
-        kv_bytes += float((lens0 + i + 1).sum()) * h * d * 4 * 2 + 2 * b * h * d * 4 + b * h * d * 8
+    for i in range(steps):   # step i appends to layer i % n_kv, its (i // n_kv + 1)-th row
+        kv_bytes += float((lens0 + i // n_kv + 1).sum()) * h * d * 4 * 2 + 2 * b * h * d * 4 + b * h * d * 8
     kv_bytes /= steps
     pbytes = 3 * c * c * 4 + 3 * c * 4 + b * c * 4 + 3 * b * c * 4
     return {"workload": "GPT-2-small MHA decode layer step (d_model 768, 12 heads, d 64, B=32, "
                         "L0~U[128,1024]): fused biased q/k/v projection (12 layers' weights "
-                        "rotated) + append/attend",
+                        "rotated) + append/attend (3 layers' KV caches rotated)",
             "prologue_ms": round(pro_ms, 4),
             "prologue_GB/s": round(pbytes / (pro_ms / 1e3) / 1e9, 1),
             "attend_ms": round(att_ms, 4),
