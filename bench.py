@@ -15,9 +15,12 @@ same line carries:
     GB/s against HBM peak (8 TB/s);
   * cpu_baseline -- the CPU restatement of the reference's GQA attention path
     (oracle/oracle.c, a "port"), timed on this host's cores on a bounded sample
-    of the same workload.
+    of the same workload, with as many threads as Rayon's global pool would
+    take here (the available parallelism: affinity mask and cgroup quota);
+  * other_configs -- configs 1, 4, 5a and 5b and the decode layer steps, each
+    with its own kernel time, roofline fraction and cpu_baseline.
 
-    python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-cpu] [--all]
+    python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-cpu] [--headline]
 """
 import argparse
 import json
@@ -38,6 +41,41 @@ PEAK_HBM_GBS = 8000.0
 # 2.2 MB written (algorithmic ~646 + 0.8, plus the partial records of split heads).
 TRAFFIC_PREFILL_CONFIG2 = round(232.9e6 + 134.2e6)
 TRAFFIC_DECODE_CONFIG3_STEP = round(646.7e6 + 2.2e6)
+
+
+def cpu_threads():
+    """Threads of the CPU legs: the parallelism Rayon's global pool takes by
+    default (std::thread::available_parallelism on Linux: the CPUs of the
+    scheduler affinity mask, capped by a cgroup v2 cpu.max quota)."""
+    n = len(os.sched_getaffinity(0))
+    try:
+        with open("/sys/fs/cgroup/cpu.max") as f:
+            quota, period = f.read().split()[:2]
+        if quota != "max":
+            n = min(n, max(1, int(quota) // int(period)))
+    except (OSError, ValueError):
+        pass
+    return max(1, n)
+
+
+def host_cpu():
+    """The host facts each cpu_baseline records."""
+    model = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return {"cpu_model": model, "cpu_count": os.cpu_count(),
+            "affinity_cpus": len(os.sched_getaffinity(0))}
+
+
+def with_host(rec):
+    rec.update(host_cpu())
+    return rec
 
 
 def load_pkg():
@@ -160,29 +198,29 @@ def cpu_baseline(target_seconds=15.0):
     import numpy as np
     sys.path.insert(0, os.path.join(ROOT, "tests"))
     import nne_testlib as T
-    threads = min(16, os.cpu_count() or 1)
+    threads = cpu_threads()
     t, d, hkv_s = 2048, 128, 1
     rng = np.random.default_rng(0x5EED0002)
     s = rng.uniform(0.5, 1.5, size=t).astype(np.float32)
     # one batch element, growing numbers of query heads sharing one KV head
     k = rng.standard_normal((1, hkv_s, t, d)).astype(np.float32) * s[None, None, :, None]
     v = rng.standard_normal((1, hkv_s, t, d)).astype(np.float32)
-    heads = threads
+    heads = max(16, threads)
     while True:
         q = rng.standard_normal((1, heads, t, d)).astype(np.float32) * s[None, None, :, None]
         t0 = time.perf_counter()
         T.ref_standard(q, k, v, masked=True, threads=threads)
         el = time.perf_counter() - t0
-        if el >= target_seconds / 4 or heads >= 128:
+        if el >= target_seconds / 4 or heads >= 1024:
             break
         heads *= 2
     flops = causal_flops(1, heads, t, d)
-    return {"value": round(flops / el / 1e12, 6), "unit": "TFLOP/s", "cores": threads,
+    return with_host({"value": round(flops / el / 1e12, 6), "unit": "TFLOP/s", "cores": threads,
             "kind": "port",
             "sample": "config 2 GQA causal prefill restated from llama.rs:253-296 "
                       "(repeat-KV, -1e4 mask, softmax, PV; f32), B=1, %d query heads on one "
                       "KV head, T=2048, d=128; %.2f s wall; FLOPs counted like the GPU "
-                      "(unmasked pairs only)" % (heads, el)}
+                      "(unmasked pairs only)" % (heads, el)})
 
 
 def flash_cpu_baseline(b, h, t, d, causal, std, sample, reps=1, seed=0x5EED0004):
@@ -192,7 +230,7 @@ def flash_cpu_baseline(b, h, t, d, causal, std, sample, reps=1, seed=0x5EED0004)
     import numpy as np
     sys.path.insert(0, os.path.join(ROOT, "tests"))
     import nne_testlib as T
-    threads = max(1, min(16, os.cpu_count() or 1, b * h))
+    threads = cpu_threads()
     rng = np.random.default_rng(seed)
     q, k, v = (rng.standard_normal((b, h, t, d), dtype=np.float32) * std for _ in range(3))
     times = []
@@ -202,10 +240,13 @@ def flash_cpu_baseline(b, h, t, d, causal, std, sample, reps=1, seed=0x5EED0004)
         times.append(time.perf_counter() - t0)
     el = sorted(times)[len(times) // 2]
     fl = causal_flops(b, h, t, d) if causal else full_flops(b, h, t, t, d)
-    return {"value": round(fl / el / 1e12, 6), "unit": "TFLOP/s", "cores": threads, "kind": "port",
-            "sample": "%s; flash_attention_forward restated from flash_attention.rs:19-199 "
-                      "(br = bc = 64, f32), %s, median of %d: %.3f s" % (
-                          sample, "causal" if causal else "non-causal", reps, el)}
+    return with_host({
+        "value": round(fl / el / 1e12, 6), "unit": "TFLOP/s", "cores": min(threads, b * h),
+        "kind": "port",
+        "sample": "%s; flash_attention_forward restated from flash_attention.rs:19-199 "
+                  "(br = bc = 64, f32), parallel over the B*H heads as the reference's "
+                  "par_chunks_mut (:69) on a pool of %d threads, %s, median of %d: %.3f s" % (
+                      sample, threads, "causal" if causal else "non-causal", reps, el)})
 
 
 def cross_cpu_baseline(b=8, h=20, tq=8, tk=1500, d=64, reps=5, seed=0x5EED0005):
@@ -214,7 +255,7 @@ def cross_cpu_baseline(b=8, h=20, tq=8, tk=1500, d=64, reps=5, seed=0x5EED0005):
     import numpy as np
     sys.path.insert(0, os.path.join(ROOT, "tests"))
     import nne_testlib as T
-    threads = max(1, min(16, os.cpu_count() or 1))
+    threads = cpu_threads()
     rng = np.random.default_rng(seed)
     q = rng.standard_normal((b, h, tq, d), dtype=np.float32)
     k, v = (rng.standard_normal((b, h, tk, d), dtype=np.float32) for _ in range(2))
@@ -225,22 +266,24 @@ def cross_cpu_baseline(b=8, h=20, tq=8, tk=1500, d=64, reps=5, seed=0x5EED0005):
         times.append(time.perf_counter() - t0)
     el = sorted(times)[len(times) // 2]
     by = (2 * b * h * tk * d + 2 * b * h * tq * d) * 4
-    return {"value": round(by / el / 1e9, 2), "unit": "GB/s", "cores": threads, "kind": "port",
+    return with_host({"value": round(by / el / 1e9, 2), "unit": "GB/s", "cores": threads, "kind": "port",
             "sample": "config 5b in full (B=8, H=20, 8 queries onto 1500 frames, d=64), "
                       "attention core restated from attention.rs:193-203 (f32), median of "
-                      "%d: %.4f s; bytes counted like the GPU line" % (reps, el)}
+                      "%d: %.4f s; bytes counted like the GPU line" % (reps, el)})
 
 
-def decode_cpu_baseline(seed=0x5EED0003, n_seq=8, steps=16):
+def decode_cpu_baseline(seed=0x5EED0003, n_seq=8, steps=16, shape=(32, 32, 8, 128),
+                        len_range=(512, 4096), label="config 3 decode step"):
     """Oracle decode step (append, then attend, llama.rs:239-296 with t = 1)
-    on the first n_seq sequences of config 3, timed on the host cores."""
+    on the first n_seq sequences of a decode workload (default config 3),
+    timed on the host cores."""
     import numpy as np
     sys.path.insert(0, os.path.join(ROOT, "tests"))
     import nne_testlib as T
-    threads = min(16, os.cpu_count() or 1)
-    b, hq, hkv, d = 32, 32, 8, 128
+    threads = cpu_threads()
+    b, hq, hkv, d = shape
     rng = np.random.default_rng(seed)
-    lens = rng.integers(512, 4097, size=b).astype(np.int32)[:n_seq].copy()
+    lens = rng.integers(len_range[0], len_range[1] + 1, size=b).astype(np.int32)[:n_seq].copy()
     cap = int(lens.max()) + steps
     kc = rng.standard_normal((n_seq, hkv, cap, d), dtype=np.float32)
     vc = rng.standard_normal((n_seq, hkv, cap, d), dtype=np.float32)
@@ -259,12 +302,13 @@ def decode_cpu_baseline(seed=0x5EED0003, n_seq=8, steps=16):
         el += time.perf_counter() - t0
         assert rc == 0
         total += float(lens.sum()) * hkv * d * 4 * 2 + 2 * n_seq * hq * d * 4 + n_seq * hkv * d * 8
-    return {"value": round(total / el / 1e9, 2), "unit": "GB/s", "cores": threads, "kind": "port",
-            "sample": "config 3 decode step restated from llama.rs:239-296 (append in place, "
-                      "repeat-KV head mapping, softmax, PV; f32), the first %d sequences "
+    return with_host({"value": round(total / el / 1e9, 2), "unit": "GB/s", "cores": threads, "kind": "port",
+            "sample": "%s (B=%d, Hq=%d, Hkv=%d, d=%d) restated from llama.rs:239-296 (append "
+                      "in place, repeat-KV head mapping, softmax, PV; f32), the first %d sequences "
                       "(lengths %d-%d), %d steps, %.2f s; bytes counted like the GPU line; "
                       "the reference's per-step Tensor::cat copy of the cache is not included"
-                      % (n_seq, int(lens.min()) - steps, int(lens.max()) - steps, steps, el)}
+                      % (label, b, hq, hkv, d, n_seq, int(lens.min()) - steps,
+                         int(lens.max()) - steps, steps, el)})
 
 
 def prologue_cpu_baseline(seed=0x5EED0014):
@@ -285,11 +329,11 @@ def prologue_cpu_baseline(seed=0x5EED0014):
     T.ref_qkv_rope(x, w[0], w[1], w[2], None, None, None, cos, sin, pos, hq, hkv)
     el = time.perf_counter() - t0
     wbytes = (hq + 2 * hkv) * d * c * 4
-    return {"value": round(wbytes / el / 1e9, 3), "unit": "GB/s", "cores": 1, "kind": "port",
+    return with_host({"value": round(wbytes / el / 1e9, 3), "unit": "GB/s", "cores": 1, "kind": "port",
             "sample": "one config-3 decode prologue (B = 32, d_model 4096, Hq = 32, Hkv = 8, "
                       "d = 128) restated from llama.rs:226-235 (q/k/v projections, head split, "
                       "RoPE; f32), one thread: %.2f s, %.2f GFLOP/s; GB/s of weights like the "
-                      "GPU line" % (el, 2.0 * b * c * (hq + 2 * hkv) * d / el / 1e9)}
+                      "GPU line" % (el, 2.0 * b * c * (hq + 2 * hkv) * d / el / 1e9)})
 
 
 def bench_decode_layer(nne, torch, dev, steps=32, seed=0x5EED0013):
@@ -348,7 +392,10 @@ def bench_decode_layer(nne, torch, dev, steps=32, seed=0x5EED0013):
             "prologue_ms": round(pro_ms, 4), "prologue_GB/s": round(gbs, 1),
             "prologue_TFLOP/s": round(flops / (pro_ms / 1e3) / 1e12, 2),
             "prologue_frac_hbm": round(gbs / PEAK_HBM_GBS, 4),
-            "prologue_bytes": pbytes, "layer_step_ms": round(step_ms, 4)}
+            "prologue_bytes": pbytes, "layer_step_ms": round(step_ms, 4),
+            "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS,
+                         "unit": "GB/s", "frac": round(gbs / PEAK_HBM_GBS, 4),
+                         "kernel": "qkv_rope_kernel", "bytes": pbytes}}
 
 
 def bench_mha_decode_layer(nne, torch, dev, steps=32, layers=12, seed=0x5EED0015):
@@ -423,7 +470,11 @@ def bench_mha_decode_layer(nne, torch, dev, steps=32, layers=12, seed=0x5EED0015
             "attend_ms": round(att_ms, 4),
             "attend_GB/s": round(kv_bytes / (att_ms / 1e3) / 1e9, 1),
             "attend_frac_hbm": round(kv_bytes / (att_ms / 1e3) / 1e9 / PEAK_HBM_GBS, 4),
-            "layer_step_ms": round(step_ms, 4)}
+            "layer_step_ms": round(step_ms, 4),
+            "roofline": {"bound": "hbm", "achieved": round(kv_bytes / (att_ms / 1e3) / 1e9, 1),
+                         "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                         "frac": round(kv_bytes / (att_ms / 1e3) / 1e9 / PEAK_HBM_GBS, 4),
+                         "kernel": "splitk_kernel (append + attend)", "bytes": round(kv_bytes)}}
 
 
 def probe(nne, torch, dev):
@@ -463,7 +514,10 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-decode", action="store_true")
-    ap.add_argument("--all", action="store_true", help="also print lines for configs 1, 4, 5")
+    ap.add_argument("--all", action="store_true",
+                    help="kept for old command lines: every config is measured by default")
+    ap.add_argument("--headline", action="store_true",
+                    help="measure only the config-2 prefill and the config-3 decode")
     ap.add_argument("--probe", action="store_true",
                     help="counter-collection run: a 1 GiB device copy (calibrates FETCH_SIZE/"
                          "WRITE_SIZE), 3 config-2 prefills, 8 config-3 decode steps, 6 "
@@ -518,7 +572,7 @@ def main():
         line["decode"] = bench_decode(nne, torch, dev)
         if not args.no_cpu:
             cpu_jobs.append((line["decode"], decode_cpu_baseline))
-    if args.all:
+    if not args.headline:
         extra = []
         g = torch.Generator(device=dev).manual_seed(0x5EED0001)
         for name, (bb, h, tt, dd, causal, std) in {
@@ -543,8 +597,13 @@ def main():
                 # The floor any launch pays: an (almost) empty kernel, queued the same way.
                 rec["empty_kernel_ms"] = round(gpu_ms_per_call(
                     torch, lambda i: torch.cuda._sleep(1), 50, True), 4)
-            rec.update({"TFLOP/s": round(fl / (kms_c / 1e3) / 1e12, 3), "kernel_ms": round(kms_c, 4),
-                        "frac": round(fl / (kms_c / 1e3) / 1e12 / PEAK_FP32_MATRIX_TFLOPS, 4)})
+            ach = fl / (kms_c / 1e3) / 1e12
+            rec.update({"TFLOP/s": round(ach, 3), "kernel_ms": round(kms_c, 4),
+                        "frac": round(ach / PEAK_FP32_MATRIX_TFLOPS, 4),
+                        "roofline": {"bound": "mfma", "achieved": round(ach, 3),
+                                     "peak": PEAK_FP32_MATRIX_TFLOPS, "unit": "TFLOP/s",
+                                     "frac": round(ach / PEAK_FP32_MATRIX_TFLOPS, 4),
+                                     "flops": fl}})
             if not args.no_cpu:
                 # Bounded samples of the same workload (a few seconds each).
                 cpu_jobs.append((rec, {
@@ -573,9 +632,13 @@ def main():
                 kms_x = gpu_ms_per_call(torch, call, reps, queued=True)
                 hms_x = gpu_ms_per_call(torch, call, reps, queued=False)
                 by = (2 * 8 * 20 * 1500 * 64 + 2 * 8 * 20 * 8 * 64) * 4
+                gbs_x = by / (kms_x / 1e3) / 1e9
                 extra.append({"workload": "config5b cross 8q->1500", "GB/s":
-                              round(by / (kms_x / 1e3) / 1e9, 1), "kernel_ms": round(kms_x, 4),
-                              "frac": round(by / (kms_x / 1e3) / 1e9 / PEAK_HBM_GBS, 4),
+                              round(gbs_x, 1), "kernel_ms": round(kms_x, 4),
+                              "frac": round(gbs_x / PEAK_HBM_GBS, 4),
+                              "roofline": {"bound": "hbm", "achieved": round(gbs_x, 1),
+                                           "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                                           "frac": round(gbs_x / PEAK_HBM_GBS, 4), "bytes": by},
                               "host_paced_GB/s": round(by / (hms_x / 1e3) / 1e9, 1),
                               "note": "3 K/V sets rotated (369 MB > 256 MB MALL); calls queued "
                                       "behind a spin kernel so the GPU runs them back to back; "
@@ -590,6 +653,10 @@ def main():
             cpu_jobs.append((extra[-1], prologue_cpu_baseline))
         print("bench: MHA decode layer step", file=sys.stderr, flush=True)
         extra.append(bench_mha_decode_layer(nne, torch, dev))
+        if not args.no_cpu:
+            cpu_jobs.append((extra[-1], lambda: decode_cpu_baseline(
+                seed=0x5EED0015, n_seq=32, steps=8, shape=(32, 12, 12, 64), len_range=(128, 1024),
+                label="GPT-2-small MHA decode attend")))
         line["other_configs"] = extra
     if not args.no_cpu:
         print("bench: cpu baseline", file=sys.stderr, flush=True)

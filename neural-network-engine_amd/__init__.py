@@ -303,13 +303,20 @@ class KVCache:
         return out
 
     def decode_step(self, layer_idx, q, k_new, v_new, out=None, scale=None, stream=None):
-        """Append one row per sequence, then attend (llama.rs:239-296, t = 1)."""
+        """Append one row per sequence, then attend (llama.rs:239-296, t = 1).
+
+        Every sequence attends to its own rows only, whatever the other
+        sequences' lengths.  Geometries the fused decode kernel does not take
+        (a head dim that is not a multiple of 4) append with the append kernel
+        and attend with the attention kernel, one call per distinct length."""
         import torch
         self._check_layer(layer_idx)
         _require_f32_cuda(q, k_new, v_new)
         hq = q.shape[1]
         if out is None:
             out = torch.empty(q.shape, dtype=torch.float32, device=q.device)
+        if not decode_kernel_fits(self.batch, hq, self.num_kv_heads, self.head_dim):
+            return self._append_then_attend(layer_idx, q, k_new, v_new, out, scale, stream)
         ws = self.workspace(hq)
         check(lib().nne_decode_step(
             q.data_ptr(), _i64(q.stride()), self.k[layer_idx].data_ptr(),
@@ -321,6 +328,32 @@ class KVCache:
             ws.data_ptr() if ws is not None else None, ws.numel() if ws is not None else 0,
             _stream(stream)))
         return out
+
+    def _append_then_attend(self, layer_idx, q, k_new, v_new, out, scale, stream):
+        # The same semantics as decode_step on the general kernels: append,
+        # then attend sequence b to its first lens[b] rows (no mask for t = 1,
+        # llama.rs:277), batching the sequences that share a length.
+        self.update(layer_idx, k_new, v_new, stream=stream)
+        lens = self.lens_host[layer_idx]
+        kl, vl = self.k[layer_idx], self.v[layer_idx]
+        for L in np.unique(lens):
+            idx = np.nonzero(lens == L)[0]
+            if len(idx) == self.batch:
+                attention_forward(q, kl[:, :, :L], vl[:, :, :L], False, scale=scale, out=out,
+                                  stream=stream)
+                break
+            for bi in idx:
+                bi = int(bi)
+                attention_forward(q[bi:bi + 1], kl[bi:bi + 1, :, :L], vl[bi:bi + 1, :, :L], False,
+                                  scale=scale, out=out[bi:bi + 1], stream=stream)
+        return out
+
+
+def decode_kernel_fits(batch, num_heads, num_kv_heads, head_dim):
+    """True when the fused append + attend kernel takes this geometry (the
+    library reports a workspace size for it)."""
+    return lib().nne_decode_workspace_bytes(max(int(batch), 1), int(num_heads),
+                                            int(num_kv_heads), int(head_dim), 1) > 0
 
 
 class FlashAttention:
@@ -515,9 +548,23 @@ class GroupedQueryAttention:
             if not np.array_equal(sp, cache.lens_host[layer_idx]):
                 raise InvalidArgument("Invalid configuration or argument: start_pos must equal "
                                       "the cached length of every sequence")
-        if cache is not None and t == 1 and self.w_packed is not None:
-            q, k_new, v_new = qkv_rope(x, self.w_packed, None, None, None, self.rope,
-                                       cache.lens_dev[layer_idx], sp, hq, hkv, stream=stream)
+            # Checked before anything is appended, so a refused step leaves
+            # the cache as it was.
+            if t > 1 and b > 1 and not (sp == sp[0]).all():
+                raise InvalidArgument("Invalid configuration or argument: multi-token steps need "
+                                      "equal cached lengths")
+        if cache is not None and t == 1:
+            if self.w_packed is not None:
+                q, k_new, v_new = qkv_rope(x, self.w_packed, None, None, None, self.rope,
+                                           cache.lens_dev[layer_idx], sp, hq, hkv, stream=stream)
+            else:
+                q = torch.nn.functional.linear(x, self.wq).view(b, 1, hq, d).transpose(1, 2)
+                k_new = torch.nn.functional.linear(x, self.wk).view(b, 1, hkv, d).transpose(1, 2)
+                v_new = torch.nn.functional.linear(x, self.wv).view(b, 1, hkv, d).transpose(1, 2)
+                q = self.rope.apply(q, sp, stream=stream)
+                k_new = self.rope.apply(k_new, sp, stream=stream)
+                v_new = v_new.contiguous()
+            # append, then attend each sequence to its own rows (ragged lengths)
             ctx = cache.decode_step(layer_idx, q, k_new, v_new, stream=stream)
             return torch.nn.functional.linear(ctx.view(b, 1, hq * d), self.wo)
         q = torch.nn.functional.linear(x, self.wq).view(b, t, hq, d).transpose(1, 2)
@@ -527,9 +574,6 @@ class GroupedQueryAttention:
         k = self.rope.apply(k, sp, stream=stream)
         if cache is not None:
             k_all, v_all = cache.update(layer_idx, k, v, stream=stream)
-            if b > 1 and not (sp == sp[0]).all():
-                raise InvalidArgument("Invalid configuration or argument: multi-token steps need "
-                                      "equal cached lengths")
         else:
             k_all, v_all = k, v
         out = torch.empty((b, t, hq, d), dtype=torch.float32, device=x.device)
@@ -588,20 +632,26 @@ class MultiHeadAttention:
         h, d = self.num_heads, self.head_dim
         if cache is not None:
             cache._check_layer(layer_idx)
-        if cache is not None and t == 1 and self.w_packed is not None:
-            q, k_new, v_new = qkv_rope(x, self.w_packed, self.q_proj[1], self.k_proj[1],
-                                       self.v_proj[1], None, None, None, h, h, stream=stream,
-                                       head_dim=d)
+            lens = cache.lens_host[layer_idx]
+            if t > 1 and b > 1 and not (lens == lens[0]).all():
+                raise InvalidArgument("Invalid configuration or argument: multi-token steps need "
+                                      "equal cached lengths")
+        if cache is not None and t == 1:
+            if self.w_packed is not None:
+                q, k_new, v_new = qkv_rope(x, self.w_packed, self.q_proj[1], self.k_proj[1],
+                                           self.v_proj[1], None, None, None, h, h, stream=stream,
+                                           head_dim=d)
+            else:
+                q = self._heads(torch.nn.functional.linear(x, *self.q_proj), b, 1)
+                k_new = self._heads(torch.nn.functional.linear(x, *self.k_proj), b, 1).contiguous()
+                v_new = self._heads(torch.nn.functional.linear(x, *self.v_proj), b, 1).contiguous()
+            # append, then attend each sequence to its own rows (ragged lengths)
             ctx = cache.decode_step(layer_idx, q, k_new, v_new, stream=stream)
             return torch.nn.functional.linear(ctx.view(b, 1, c), *self.out_proj)
         q = self._heads(torch.nn.functional.linear(x, *self.q_proj), b, t)
         k = self._heads(torch.nn.functional.linear(x, *self.k_proj), b, t)
         v = self._heads(torch.nn.functional.linear(x, *self.v_proj), b, t)
         if cache is not None:
-            lens = cache.lens_host[layer_idx]
-            if t > 1 and b > 1 and not (lens == lens[0]).all():
-                raise InvalidArgument("Invalid configuration or argument: multi-token steps need "
-                                      "equal cached lengths")
             k_all, v_all = cache.update(layer_idx, k.contiguous(), v.contiguous(), stream=stream)
             total = int(cache.lens_host[layer_idx][0]) if b else 0
         else:

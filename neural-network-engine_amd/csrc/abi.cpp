@@ -247,7 +247,9 @@ void resolve_strides(Resolved& r, const int64_t* qs_, const int64_t* qst, const 
     for (int i = 0; i < 4; ++i) r.v[i] = vst ? vst[i] : c[i];
 }
 
-int check_kv_cache_args(int64_t B, int64_t Hq, int64_t Hkv, int64_t capacity, int64_t d) {
+// Cache geometry; `decode` adds the decode kernel's head-dim limits (the
+// append kernel is element-wise and takes any head dim).
+int check_kv_cache_args(int64_t B, int64_t Hq, int64_t Hkv, int64_t capacity, int64_t d, bool decode) {
     if (B < 0 || Hq < 0 || Hkv <= 0 || capacity < 0 || d <= 0 || B > INT32_MAX ||
         Hq > INT32_MAX || Hkv > INT32_MAX || capacity > INT32_MAX || d > INT32_MAX)
         return fail(NNE_EINVAL, "Invalid configuration or argument: bad KV cache geometry "
@@ -257,7 +259,7 @@ int check_kv_cache_args(int64_t B, int64_t Hq, int64_t Hkv, int64_t capacity, in
         return fail(NNE_EINVAL, "Invalid configuration or argument: num_heads (%lld) must be "
                                 "divisible by num_kv_heads (%lld) for GQA",
                     (long long)Hq, (long long)Hkv);
-    if (d % 4 != 0 || nne::splitk_padded_dim((int)d) == 0)
+    if (decode && (d % 4 != 0 || nne::splitk_padded_dim((int)d) == 0))
         return fail(NNE_EINVAL, "Invalid configuration or argument: KV cache head dim %lld must be "
                                 "a multiple of 4 and at most 128", (long long)d);
     return NNE_OK;
@@ -398,7 +400,7 @@ int nne_kv_append(float* k_cache, float* v_cache, int32_t* lens_dev, int32_t* le
                   const float* k_new, const int64_t k_new_strides[4], const float* v_new,
                   const int64_t v_new_strides[4], int64_t B, int64_t Hkv, int64_t capacity,
                   int64_t d, int64_t t_new, void* stream) {
-    int rc = check_kv_cache_args(B, Hkv, Hkv, capacity, d);
+    int rc = check_kv_cache_args(B, Hkv, Hkv, capacity, d, false);
     if (rc) return rc;
     if (t_new < 0 || t_new > INT32_MAX)
         return fail(NNE_EINVAL, "Invalid configuration or argument: t_new = %lld", (long long)t_new);
@@ -411,6 +413,8 @@ int nne_kv_append(float* k_cache, float* v_cache, int32_t* lens_dev, int32_t* le
                         (long long)t_new, (long long)b, lens_host[b], (long long)capacity);
     }
     if (B == 0 || t_new == 0) return NNE_OK;
+    if (!k_cache || !v_cache || !lens_dev || !k_new || !v_new)
+        return fail(NNE_EINVAL, "Invalid configuration or argument: null tensor pointer");
     const int64_t shape[4] = {B, Hkv, t_new, d};
     int64_t c[4];
     contiguous_strides(shape, c);
@@ -424,7 +428,7 @@ int nne_kv_append(float* k_cache, float* v_cache, int32_t* lens_dev, int32_t* le
 }
 
 uint64_t nne_decode_workspace_bytes(int64_t B, int64_t Hq, int64_t Hkv, int64_t d, int64_t max_len) {
-    if (B <= 0 || Hkv <= 0 || Hq <= 0 || Hq % Hkv != 0 || d <= 0 || max_len < 0 ||
+    if (B <= 0 || Hkv <= 0 || Hq <= 0 || Hq % Hkv != 0 || d <= 0 || d % 4 != 0 || max_len < 0 ||
         nne::splitk_padded_dim((int)d) == 0 || Hq / Hkv > nne::splitk_max_rows() ||
         B > nne::splitk_max_seqs())
         return 0;
@@ -440,7 +444,7 @@ int run_decode(const float* q, const int64_t* q_strides, const float* k_cache, c
                const int64_t* o_strides, int64_t B, int64_t Hq, int64_t Hkv, int64_t capacity,
                int64_t d, int has_scale, float scale, void* workspace, uint64_t workspace_bytes,
                hipStream_t s) {
-    int rc = check_kv_cache_args(B, Hq, Hkv, capacity, d);
+    int rc = check_kv_cache_args(B, Hq, Hkv, capacity, d, true);
     if (rc) return rc;
     if (Hq / Hkv > nne::splitk_max_rows())
         return fail(NNE_EINVAL, "Invalid configuration or argument: %lld query heads per KV head "
@@ -453,6 +457,8 @@ int run_decode(const float* q, const int64_t* q_strides, const float* k_cache, c
         return fail(NNE_EINVAL, "Invalid configuration or argument: decode batch of %lld sequences "
                                 "exceeds %d", (long long)B, nne::splitk_max_seqs());
     const bool append = k_new != nullptr;
+    if (!q || !o || !k_cache || !v_cache || !lens_dev || (append && !v_new))
+        return fail(NNE_EINVAL, "Invalid configuration or argument: null tensor pointer");
     int max_len = 0;
     int64_t total_keys = 0;
     std::vector<int32_t> seq_lens((size_t)B);
@@ -489,6 +495,11 @@ int run_decode(const float* q, const int64_t* q_strides, const float* k_cache, c
     const int64_t* vnst = vn_strides ? vn_strides : ckv;
     if (qst[3] != 1 || ost[3] != 1)
         return fail(NNE_EINVAL, "Invalid configuration or argument: decode q/o need unit dim stride");
+    // The 16-row tile (more than 4 query heads per KV head) reads q rows as
+    // 16-byte vectors.
+    if (Hq / Hkv > 4 && !vec_view(q, qst))
+        return fail(NNE_EINVAL, "Invalid configuration or argument: decode q needs 16-byte alignment "
+                                "and strides that are multiples of 4");
     if (!aligned16(k_cache) || !aligned16(v_cache))
         return fail(NNE_EINVAL, "Invalid configuration or argument: KV cache must be 16-byte aligned");
     if (append && (!vec_view(k_new, knst) || !vec_view(v_new, vnst)))

@@ -553,6 +553,28 @@ Result<RawTensor> KVCache::decode_step(size_t layer_idx, const RawTensor& q, con
     Layer& l = layers_[layer_idx];
     RawTensor out = RawTensor::zeros(q.shape());
     const auto qst = as_i64(q.strides()), ost = as_i64(out.strides());
+    const int64_t hq = (int64_t)q.shape()[1];
+    if (nne_decode_workspace_bytes(std::max<int64_t>((int64_t)batch, 1), hq, (int64_t)num_kv_heads,
+                                   (int64_t)head_dim, 1) == 0) {
+        // Geometry the fused kernel does not take (head dim not a multiple of
+        // 4): append, then attend every sequence to its own first lens[b]
+        // rows, no mask (llama.rs:239-296 with t = 1), on the general kernel.
+        auto kv = update(layer_idx, k_new, v_new);
+        if (kv.is_err()) return kv.error();
+        for (size_t b = 0; b < batch; ++b) {
+            const size_t L = (size_t)l.lens_host[b];
+            RawTensor qb = q.slice(0, b, b + 1).value(), ob = out.slice(0, b, b + 1).value();
+            RawTensor kb = k(layer_idx).slice(0, b, b + 1).value().slice(2, 0, L).value();
+            RawTensor vb = v(layer_idx).slice(0, b, b + 1).value().slice(2, 0, L).value();
+            const auto qs = as_i64(qb.shape()), qbs = as_i64(qb.strides()), obs = as_i64(ob.strides());
+            const auto ks = as_i64(kb.shape()), kbs = as_i64(kb.strides()), vbs = as_i64(vb.strides());
+            const int rc = nne_attention_forward(qb.data(), qs.data(), qbs.data(), kb.data(), ks.data(), kbs.data(),
+                                                 vb.data(), ks.data(), vbs.data(), ob.data(), obs.data(), 0, 0,
+                                                 scale ? 1 : 0, scale.value_or(0.f), nullptr);
+            if (rc != NNE_OK) return from_status(rc);
+        }
+        return out;
+    }
     const auto kst = as_i64(k_new.strides()), vst = as_i64(v_new.strides());
     void* ws = workspace(q.shape()[1]);
     const int rc = nne_decode_step(q.data(), qst.data(), l.k.get(), l.v.get(), l.lens_dev.get(),
@@ -798,17 +820,41 @@ Result<RawTensor> MultiHeadAttention::forward_attention_cached(const RawTensor& 
         if (cache->batch != b || cache->num_kv_heads != h || cache->head_dim != d)
             return EngineError::shape_mismatch({b, h, cache->capacity, d},
                                                {cache->batch, cache->num_kv_heads, cache->capacity, cache->head_dim});
+        // Checked before anything is appended, so a refused step leaves the
+        // cache as it was.
+        const auto& lens = cache->lengths(layer_idx);
+        for (int32_t L : lens)
+            if (t > 1 && L != lens[0])
+                return EngineError::invalid_argument("multi-token steps need equal cached lengths");
     }
-    if (cache && t == 1 && w_packed_) {
-        // Decode step: fused biased projections (no rotation), then append + attend.
-        RawTensor xc = x.to_contiguous();
-        RawTensor q = RawTensor::zeros({b, h, 1, d}), k_new = RawTensor::zeros({b, h, 1, d}),
-                  v_new = RawTensor::zeros({b, h, 1, d});
-        const int rc = nne_qkv_rope(xc.data(), (int64_t)c, w_packed_.get(), q_proj.bias->data(), k_proj.bias->data(),
-                                    v_proj.bias->data(), nullptr, nullptr, 0, (int64_t)d, nullptr, nullptr, q.data(),
-                                    k_new.data(), v_new.data(), (int64_t)b, (int64_t)c, (int64_t)h, (int64_t)h,
-                                    (int64_t)d, nullptr);
-        if (rc != NNE_OK) return from_status(rc);
+    if (cache && t == 1) {
+        // Decode step: biased projections (no rotation), then append + attend
+        // with each sequence seeing its own rows (ragged lengths).
+        RawTensor q, k_new, v_new;
+        if (w_packed_) {
+            RawTensor xc = x.to_contiguous();
+            q = RawTensor::zeros({b, h, 1, d});
+            k_new = RawTensor::zeros({b, h, 1, d});
+            v_new = RawTensor::zeros({b, h, 1, d});
+            const int rc = nne_qkv_rope(xc.data(), (int64_t)c, w_packed_.get(), q_proj.bias->data(),
+                                        k_proj.bias->data(), v_proj.bias->data(), nullptr, nullptr, 0, (int64_t)d,
+                                        nullptr, nullptr, q.data(), k_new.data(), v_new.data(), (int64_t)b,
+                                        (int64_t)c, (int64_t)h, (int64_t)h, (int64_t)d, nullptr);
+            if (rc != NNE_OK) return from_status(rc);
+        } else {
+            auto head_view = [&](const Linear& lin) -> Result<RawTensor> {
+                auto y = lin.forward(x);                             // [B, 1, C]
+                if (y.is_err()) return y.error();
+                return y.value().reshape({b, 1, h, d}).value().transpose(1, 2).value().to_contiguous();
+            };
+            auto qp = head_view(q_proj), kp = head_view(k_proj), vp = head_view(v_proj);
+            if (qp.is_err()) return qp.error();
+            if (kp.is_err()) return kp.error();
+            if (vp.is_err()) return vp.error();
+            q = qp.value();
+            k_new = kp.value();
+            v_new = vp.value();
+        }
         auto ctx = cache->decode_step(layer_idx, q, k_new, v_new);
         if (ctx.is_err()) return ctx.error();
         auto merged = ctx.value().reshape({b, 1, c});
@@ -825,10 +871,6 @@ Result<RawTensor> MultiHeadAttention::forward_attention_cached(const RawTensor& 
     RawTensor q = heads(qp.value()), k_all = heads(kp.value()), v_all = heads(vp.value());
     size_t total = t;
     if (cache) {                                                     // :78-91
-        const auto& lens = cache->lengths(layer_idx);
-        for (int32_t L : lens)
-            if (t > 1 && L != lens[0])
-                return EngineError::invalid_argument("multi-token steps need equal cached lengths");
         auto kv = cache->update(layer_idx, k_all, v_all);
         if (kv.is_err()) return kv.error();
         k_all = kv.value().first;

@@ -20,6 +20,7 @@
 #include <vector>
 
 #include "nne.hpp"
+#include "nne_attn.h"
 
 extern "C" {
 void oracle_flash_forward(const float* q, const float* k, const float* v, float* out, int64_t b, int64_t h,
@@ -392,6 +393,46 @@ TEST_GPU(test_mha_cached_self_attention_matches_oracle) {                 // att
     CHECK(cache.self_attn.current_seq_len(0) == t0 + steps);
     auto r = m.forward_attention(RawTensor::randn({b, c}, 0.f, 1.f));    // :56-62
     CHECK(r.is_err() && r.error().kind == EngineError::Kind::IncompatibleShapes);
+}
+
+// A single-token step over sequences of different cached lengths, with
+// projections that do not take the packed launch (d = 32 on the fused append +
+// attend kernel, d = 30 on the general kernels): each sequence attends to its
+// own rows, as the reference's per-sequence B = 1 calls do (attention.rs:79-122).
+TEST_GPU(test_mha_ragged_decode_step_matches_oracle) {
+    for (size_t c : {size_t(128), size_t(120)}) {
+        const size_t b = 3, h = 4, d = c / h, cap = 32;
+        manual_seed(15 + c);
+        MultiHeadAttention m(c, h, true);
+        KVCache cache(1, b, h, cap, d);
+        const std::vector<int32_t> lens{5, 20, 11};
+        RawTensor kc = RawTensor::randn({b, h, cap, d}, 0.f, 1.f), vc = RawTensor::randn({b, h, cap, d}, 0.f, 1.f);
+        const uint64_t bytes = b * h * cap * d * 4;
+        CHECK(nne_memcpy_d2d(cache.k(0).data(), kc.data(), bytes, nullptr) == NNE_OK);
+        CHECK(nne_memcpy_d2d(cache.v(0).data(), vc.data(), bytes, nullptr) == NNE_OK);
+        CHECK(nne_stream_sync(nullptr) == NNE_OK);
+        cache.set_lengths(0, lens).unwrap();
+        RawTensor x = RawTensor::randn({b, 1, c}, 0.f, 1.f);
+        const auto y = m.forward_attention_cached(x, &cache, 0).unwrap().to_vec();
+        const auto xv = x.to_vec(), kh = kc.to_vec(), vh = vc.to_vec();
+        for (size_t bi = 0; bi < b; ++bi) {
+            const size_t L = (size_t)lens[bi];
+            std::vector<float> kp(h * L * d), vp(h * L * d);
+            for (size_t hh = 0; hh < h; ++hh)
+                for (size_t r = 0; r < L; ++r)
+                    for (size_t e = 0; e < d; ++e) {
+                        kp[(hh * L + r) * d + e] = kh[((bi * h + hh) * cap + r) * d + e];
+                        vp[(hh * L + r) * d + e] = vh[((bi * h + hh) * cap + r) * d + e];
+                    }
+            const std::vector<float> xb(xv.begin() + bi * c, xv.begin() + (bi + 1) * c);
+            const auto kall = project_heads(m.k_proj, xb, 1, 1, h, kp, L);
+            const auto vall = project_heads(m.v_proj, xb, 1, 1, h, vp, L);
+            const auto ref = oracle_mha(m, xb, 1, 1, kall, vall, L + 1, true);
+            const std::vector<float> got(y.begin() + bi * c, y.begin() + (bi + 1) * c);
+            check_close(got, ref, c == 128 ? "ragged mha decode d=32" : "ragged mha decode d=30");
+            CHECK(cache.lengths(0)[bi] == lens[bi] + 1);
+        }
+    }
 }
 
 TEST_GPU(test_cross_attention_cached_slot) {                              // attention.rs:139-210

@@ -96,6 +96,7 @@ def test_decode_workspace_size(nne):
     lib = nne.lib()
     assert lib.nne_decode_workspace_bytes(1, 4, 3, 64, 100) == 0   # 3 does not divide 4
     assert lib.nne_decode_workspace_bytes(1, 4, 4, 256, 100) == 0  # head dim > 128
+    assert lib.nne_decode_workspace_bytes(1, 4, 4, 30, 100) == 0   # head dim not a multiple of 4
     assert lib.nne_decode_workspace_bytes(1, 32, 1, 64, 100) == 0  # 32 rows per KV head > 16
     small = lib.nne_decode_workspace_bytes(2, 4, 2, 64, 4160)
     big = lib.nne_decode_workspace_bytes(32, 32, 8, 128, 4160)
@@ -187,3 +188,52 @@ def test_qkv_packed_bytes(nne):
     assert lib.nne_qkv_packed_bytes(100, 4, 2, 64) == 0        # C % 64
     assert lib.nne_qkv_packed_bytes(256, 4, 2, 32) == 0        # d % 64
     assert lib.nne_qkv_pack(FAKE, FAKE, FAKE, FAKE, 256, 4, 2, 32, None) == nne.NNE_EINVAL
+
+
+def test_decode_and_append_reject_null_device_pointers(nne):
+    """A NULL device pointer with work to do is an InvalidArgument on the
+    host, never a launch that would fault."""
+    lib = nne.lib()
+    lens = np.array([3, 4], np.int32)
+    lp = lens.ctypes.data_as(ctypes.POINTER(ctypes.c_int32))
+    for bad in range(5):
+        ptrs = [FAKE] * 5
+        ptrs[bad] = None
+        kc, vc, ld, kn, vn = ptrs
+        assert lib.nne_kv_append(kc, vc, ld, lp, kn, None, vn, None, 2, 2, 16, 16, 1,
+                                 None) == nne.NNE_EINVAL
+        assert "null tensor pointer" in lib.nne_last_error().decode()
+    assert list(lens) == [3, 4]
+    for bad in range(7):
+        ptrs = [FAKE] * 7
+        ptrs[bad] = None
+        q, kc, vc, ld, kn, vn, o = ptrs
+        rc = lib.nne_decode_step(q, None, kc, vc, ld, lp, kn, None, vn, None, o, None, 2, 4, 2,
+                                 16, 16, 0, 0.0, None, 0, None)
+        assert rc == nne.NNE_EINVAL, bad
+    assert list(lens) == [3, 4]
+    # attention only: q, caches, lengths and output
+    for bad in range(5):
+        ptrs = [FAKE] * 5
+        ptrs[bad] = None
+        q, kc, vc, ld, o = ptrs
+        rc = lib.nne_decode_attention(q, None, kc, vc, ld, lp, o, None, 2, 4, 2, 16, 16, 0, 0.0,
+                                      None, 0, None)
+        assert rc == nne.NNE_EINVAL, bad
+
+
+def test_decode_16_row_tile_needs_vector_q(nne):
+    """More than 4 query heads per KV head read q as 16-byte vectors: a
+    misaligned q or strides that are not multiples of 4 are refused."""
+    lib = nne.lib()
+    lens = np.array([3], np.int32)
+    lp = lens.ctypes.data_as(ctypes.POINTER(ctypes.c_int32))
+    misaligned = ctypes.c_void_p(4096 + 4)
+    rc = lib.nne_decode_attention(misaligned, None, FAKE, FAKE, FAKE, lp, FAKE, None, 1, 8, 1, 16,
+                                  16, 0, 0.0, None, 0, None)
+    assert rc == nne.NNE_EINVAL
+    assert "16-byte alignment" in lib.nne_last_error().decode()
+    odd = i64(8 * 16, 18, 16, 1)       # head stride 18 floats
+    rc = lib.nne_decode_attention(FAKE, odd, FAKE, FAKE, FAKE, lp, FAKE, None, 1, 8, 1, 16, 16, 0,
+                                  0.0, None, 0, None)
+    assert rc == nne.NNE_EINVAL

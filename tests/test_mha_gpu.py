@@ -143,3 +143,45 @@ def test_mha_shape_errors_match_reference(nne, cuda):
     with pytest.raises(nne.InvalidArgument, match=r"d_model \(30\) must be divisible by "
                                                   r"num_heads \(4\)"):
         nne.MultiHeadAttention(30, 4, True, device=cuda)
+
+
+@pytest.mark.parametrize("c,h", [(128, 4), (160, 2), (120, 4)])   # d = 32, 80, 30
+def test_mha_ragged_decode_step_matches_oracle(nne, cuda, c, h):
+    """A single-token step over a cache whose sequences have different
+    lengths, with projections that do not take the packed launch: every
+    sequence attends to its own rows only (the reference runs such a batch
+    as separate B = 1 calls, attention.rs:79-122)."""
+    rng = np.random.default_rng(c + 7 * h)
+    b, cap = 3, 64
+    d = c // h
+    lens = np.array([5, 40, 17], np.int32)
+    layer = nne.MultiHeadAttention(c, h, True, device=cuda, seed=11)
+    assert layer.w_packed is None
+    w = weights(layer)
+    cache = nne.KVCache(1, b, h, cap, d, device=cuda)
+    kc = np.zeros((b, h, cap, d), np.float32)
+    vc = np.zeros_like(kc)
+    for i, L in enumerate(lens):
+        kc[i, :, :L] = rnd(rng, h, L, d)
+        vc[i, :, :L] = rnd(rng, h, L, d)
+    cache.k[0].copy_(dev(kc, cuda))
+    cache.v[0].copy_(dev(vc, cuda))
+    cache.set_lengths(0, lens)
+    x = rnd(rng, b, 1, c)
+    y = host(layer.forward_attention_cached(dev(x, cuda), cache, 0))
+    for i, L in enumerate(lens):
+        ry, rk, rv = oracle_self(w, x[i:i + 1], kc[i:i + 1, :, :L], vc[i:i + 1, :, :L], h, True)
+        T.assert_close(y[i:i + 1], ry, what="ragged mha decode seq %d (d=%d)" % (i, d))
+        T.assert_close(host(cache.k[0])[i:i + 1, :, :L + 1], rk, what="cached K seq %d" % i)
+    assert list(cache.lens_host[0]) == list(lens + 1)
+    assert list(host(cache.lens_dev[0])) == list(lens + 1)
+
+
+def test_mha_ragged_multi_token_step_is_refused_before_append(nne, cuda):
+    layer = nne.MultiHeadAttention(128, 2, True, device=cuda, seed=12)
+    cache = nne.KVCache(1, 2, 2, 16, 64, device=cuda)
+    cache.set_lengths(0, [3, 5])
+    import torch
+    with pytest.raises(nne.InvalidArgument, match="equal cached lengths"):
+        layer.forward_attention_cached(torch.zeros(2, 2, 128, device=cuda), cache, 0)
+    assert list(cache.lens_host[0]) == [3, 5]

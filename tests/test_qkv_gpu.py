@@ -145,6 +145,11 @@ def oracle_gqa_step(layer, x, cache_k, cache_v, lens):
 @pytest.mark.parametrize("b,c,hq,hkv,lens", [
     (4, 256, 4, 2, [0, 3, 17, 64]),
     (3, 512, 8, 8, [5, 129, 300]),
+    # unpacked projections (d not a multiple of 64), ragged lengths: d = 32,
+    # d = 80 on the fused append + attend kernel, d = 30 on the general kernels
+    (4, 128, 4, 2, [0, 3, 17, 64]),
+    (3, 160, 2, 1, [5, 129, 300]),
+    (3, 60, 2, 2, [1, 40, 7]),
 ])
 def test_gqa_decode_step_matches_oracle(nne, cuda, b, c, hq, hkv, lens):
     rng = np.random.default_rng(21 + b)
