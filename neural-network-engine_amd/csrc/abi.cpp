@@ -16,6 +16,7 @@
 #include <thread>
 #include <vector>
 
+#include "nne_abi_internal.hpp"
 #include "nne_attn.h"
 #include "nne_launch.hpp"
 
@@ -267,6 +268,14 @@ int check_kv_cache_args(int64_t B, int64_t Hq, int64_t Hkv, int64_t capacity, in
 
 }  // namespace
 
+namespace nne {
+
+int fail_message(int code, const char* msg) { return fail(code, "%s", msg); }
+
+int fail_hip(hipError_t e, const char* what) { return hip_fail(e, what); }
+
+}  // namespace nne
+
 extern "C" {
 
 int nne_abi_version(void) { return NNE_ABI_VERSION; }
@@ -435,15 +444,18 @@ uint64_t nne_decode_workspace_bytes(int64_t B, int64_t Hq, int64_t Hkv, int64_t 
     return nne::splitk_workspace_layout((int)B, (int)Hkv, (int)(Hq / Hkv), (int)d).total_bytes;
 }
 
-namespace {
+}  // extern "C"
 
-// Shared body of nne_decode_attention and nne_decode_step.
+namespace nne {
+
+// Shared body of the decode entry points.  With a NULL workspace or NULL
+// counters the stream's library-side ones are used.
 int run_decode(const float* q, const int64_t* q_strides, const float* k_cache, const float* v_cache,
                const int32_t* lens_dev, int32_t* lens_dev_w, int32_t* lens_host, const float* k_new,
                const int64_t* kn_strides, const float* v_new, const int64_t* vn_strides, float* o,
                const int64_t* o_strides, int64_t B, int64_t Hq, int64_t Hkv, int64_t capacity,
                int64_t d, int has_scale, float scale, void* workspace, uint64_t workspace_bytes,
-               hipStream_t s) {
+               uint32_t* caller_counters, hipStream_t s) {
     int rc = check_kv_cache_args(B, Hq, Hkv, capacity, d, true);
     if (rc) return rc;
     if (Hq / Hkv > nne::splitk_max_rows())
@@ -530,9 +542,14 @@ int run_decode(const float* q, const int64_t* q_strides, const float* k_cache, c
         return fail(NNE_EINVAL, "Invalid configuration or argument: decode workspace of %llu bytes "
                                 "is smaller than the %llu required",
                     (unsigned long long)workspace_bytes, (unsigned long long)w.total_bytes);
-    uint32_t* counters = nullptr;
-    hipError_t e = stream_resources(B * Hkv, ws ? 0 : w.total_bytes, s, &counters, &ws);
-    if (e != hipSuccess) return hip_fail(e, "decode workspace");
+    uint32_t* counters = caller_counters;
+    hipError_t e = hipSuccess;
+    if (!counters || !ws) {
+        uint32_t* lib_counters = nullptr;
+        e = stream_resources(counters ? 0 : B * Hkv, ws ? 0 : w.total_bytes, s, &lib_counters, &ws);
+        if (e != hipSuccess) return hip_fail(e, "decode workspace");
+        if (!counters) counters = lib_counters;
+    }
     e = nne::launch_splitk(p, total_keys, max_len, ws, s, seq_lens.data(), counters);
     if (e != hipSuccess) return hip_fail(e, "decode attention launch");
     if (append)
@@ -540,17 +557,20 @@ int run_decode(const float* q, const int64_t* q_strides, const float* k_cache, c
     return NNE_OK;
 }
 
-}  // namespace
+}  // namespace nne
+
+extern "C" {
+
 
 int nne_decode_attention(const float* q, const int64_t q_strides[4], const float* k_cache,
                          const float* v_cache, const int32_t* lens_dev, const int32_t* lens_host,
                          float* o, const int64_t o_strides[4], int64_t B, int64_t Hq, int64_t Hkv,
                          int64_t capacity, int64_t d, int has_scale, float scale, void* workspace,
                          uint64_t workspace_bytes, void* stream) {
-    return run_decode(q, q_strides, k_cache, v_cache, lens_dev, nullptr,
+    return nne::run_decode(q, q_strides, k_cache, v_cache, lens_dev, nullptr,
                       const_cast<int32_t*>(lens_host), nullptr, nullptr, nullptr, nullptr, o,
                       o_strides, B, Hq, Hkv, capacity, d, has_scale, scale, workspace,
-                      workspace_bytes, as_stream(stream));
+                      workspace_bytes, nullptr, as_stream(stream));
 }
 
 int nne_decode_step(const float* q, const int64_t q_strides[4], float* k_cache, float* v_cache,
@@ -562,9 +582,9 @@ int nne_decode_step(const float* q, const int64_t q_strides[4], float* k_cache, 
                     void* stream) {
     if (!k_new || !v_new)
         return fail(NNE_EINVAL, "Invalid configuration or argument: decode step needs k_new and v_new");
-    return run_decode(q, q_strides, k_cache, v_cache, lens_dev, lens_dev, lens_host, k_new,
+    return nne::run_decode(q, q_strides, k_cache, v_cache, lens_dev, lens_dev, lens_host, k_new,
                       k_new_strides, v_new, v_new_strides, o, o_strides, B, Hq, Hkv, capacity, d,
-                      has_scale, scale, workspace, workspace_bytes, as_stream(stream));
+                      has_scale, scale, workspace, workspace_bytes, nullptr, as_stream(stream));
 }
 
 // ---- decode prologue: projections and rotary position embedding ----------

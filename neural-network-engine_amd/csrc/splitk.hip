@@ -854,26 +854,6 @@ __global__ void lens_bump_kernel(int32_t* lens, int B, int t_new) {
 
 }  // namespace
 
-int splitk_padded_dim(int d) {
-    if (d <= 64) return 64;
-    if (d <= 128) return 128;
-    return 0;
-}
-
-int splitk_max_rows() { return 16; }
-int splitk_max_seqs() { return MAX_SEQS; }
-int splitk_max_workgroups() { return MAX_WG; }
-
-SplitKWorkspace splitk_workspace_layout(int B, int Hkv, int R, int d) {
-    SplitKWorkspace w;
-    const int D = splitk_padded_dim(d);
-    const uint64_t slots = (uint64_t)MAX_WG + (uint64_t)B * Hkv;
-    w.ml_offset = ((uint64_t)(B + 1) * 4 + 255) / 256 * 256;
-    w.o_offset = w.ml_offset + (slots * R * 2 * 4 + 255) / 256 * 256;
-    w.total_bytes = w.o_offset + slots * R * D * 4;
-    return w;
-}
-
 namespace {
 
 // Workgroups of a split launch: one per CU.  Measured on MI355X against one
@@ -897,6 +877,32 @@ int split_workgroups() {
     }
     return n;
 }
+
+}  // namespace
+
+int splitk_padded_dim(int d) {
+    if (d <= 64) return 64;
+    if (d <= 128) return 128;
+    return 0;
+}
+
+int splitk_max_rows() { return 16; }
+int splitk_max_seqs() { return MAX_SEQS; }
+int splitk_max_workgroups() { return MAX_WG; }
+
+SplitKWorkspace splitk_workspace_layout(int B, int Hkv, int R, int d) {
+    SplitKWorkspace w;
+    const int D = splitk_padded_dim(d);
+    // Record slot = workgroup + head: a launch has at most split_workgroups()
+    // workgroups on this device (its chunks are at least total / that many keys).
+    const uint64_t slots = (uint64_t)split_workgroups() + (uint64_t)B * Hkv;
+    w.ml_offset = ((uint64_t)(B + 1) * 4 + 255) / 256 * 256;
+    w.o_offset = w.ml_offset + (slots * R * 2 * 4 + 255) / 256 * 256;
+    w.total_bytes = w.o_offset + slots * R * D * 4;
+    return w;
+}
+
+namespace {
 
 template <int D>
 hipError_t launch_flat(SplitKParams p, int64_t total_keys, int max_len, hipStream_t stream) {
