@@ -153,6 +153,28 @@ int nne_decode_step(const float *q, const int64_t q_strides[4], float *k_cache, 
                     int has_scale, float scale, void *workspace, uint64_t workspace_bytes,
                     void *stream);
 
+/* Bytes of device scratch behind nne_decode_step_noalloc, one copy per GPU. */
+#define NNE_NOALLOC_SCRATCH_BYTES (16u << 20)
+
+/* No counterpart in the reference: a variant of nne_decode_step for callers
+ * that cannot allocate device memory during the call (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc).  Same
+ * arguments, semantics and errors as nne_decode_step without the workspace:
+ * its split-K partial records and arrival counters live in a static device
+ * array of NNE_NOALLOC_SCRATCH_BYTES that every GPU the library runs on holds
+ * until the process ends, and the call makes no hipMalloc, hipFree or other
+ * allocation.  NNE_EINVAL if the step needs more scratch than that (at
+ * d = 128 it holds about 7800 (sequence, KV head) pairs with up to 4 query
+ * heads per KV head, about 1700 with up to 16).  Every
+ * call on a GPU shares that GPU's array: calls that overlap in time on one
+ * GPU (any stream, any thread) race, and the caller must serialise them. */
+int nne_decode_step_noalloc(const float *q, const int64_t q_strides[4], float *k_cache,
+                            float *v_cache, int32_t *lens_dev, int32_t *lens_host,
+                            const float *k_new, const int64_t k_new_strides[4], const float *v_new,
+                            const int64_t v_new_strides[4], float *o, const int64_t o_strides[4],
+                            int64_t B, int64_t Hq, int64_t Hkv, int64_t capacity, int64_t d,
+                            int has_scale, float scale, void *stream);
+
 /* ---- decode prologue -----------------------------------------------------
  * The steps of GroupedQueryAttention::forward_gqa_cached before attention
  * (src/models/llama.rs:226-235): q/k/v projections (Linear::forward,

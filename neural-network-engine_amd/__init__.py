@@ -95,6 +95,10 @@ SIGNATURES = {
         _vp, _i64p, _vp, _vp, _vp, _i32p, _vp, _i64p, _vp, _i64p, _vp, _i64p,
         ctypes.c_int64, ctypes.c_int64, ctypes.c_int64, ctypes.c_int64, ctypes.c_int64,
         ctypes.c_int, ctypes.c_float, _vp, ctypes.c_uint64, _vp]),
+    "nne_decode_step_noalloc": (ctypes.c_int, [
+        _vp, _i64p, _vp, _vp, _vp, _i32p, _vp, _i64p, _vp, _i64p, _vp, _i64p,
+        ctypes.c_int64, ctypes.c_int64, ctypes.c_int64, ctypes.c_int64, ctypes.c_int64,
+        ctypes.c_int, ctypes.c_float, _vp]),
     "nne_rope_tables": (ctypes.c_int, [_vp, _vp, ctypes.c_int64, ctypes.c_int64, ctypes.c_float]),
     "nne_rope_apply": (ctypes.c_int, [
         _vp, _i64p, _i64p, _vp, _i64p, _vp, _vp, ctypes.c_int64, ctypes.c_int64, _vp, _i32p,
