@@ -17,9 +17,14 @@
  * reference's functions may (Module: Send + Sync, src/nn/module.rs:7).  Calls
  * on one stream, from one thread or several (the NULL stream is shared by
  * all threads), run in that stream's order and share the workspace and
- * counters the library keeps for it.  The caller orders calls that write the
- * same output or the same KV cache, and calls nne_stream_release only when no
- * other call uses that stream.
+ * counters the library keeps for it when the caller passes none.  The caller
+ * orders calls that write the same output or the same KV cache, and calls
+ * nne_stream_release only when no other call uses that stream.
+ *
+ * Ownership: every device buffer a call touches can be the caller's.  Inputs,
+ * outputs and KV caches always are; the scratch of split computations is the
+ * caller's nne_workspace_t when one is passed (see below), and only a NULL
+ * workspace makes the library use memory of its own.
  */
 #ifndef NNE_ATTN_H
 #define NNE_ATTN_H
@@ -38,7 +43,7 @@ enum {
     NNE_EHIP = 4       /* HIP runtime failure            -> EngineError::GpuError (src/error.rs:48) */
 };
 
-#define NNE_ABI_VERSION 3
+#define NNE_ABI_VERSION 4
 
 int nne_abi_version(void);
 
@@ -63,6 +68,44 @@ int nne_stream_sync(void *stream);
  * reference, whose CPU path allocates per call: it is for long-running
  * callers that create and destroy streams. */
 int nne_stream_release(void *stream);
+
+/* Bytes of device memory the library holds for `stream` on the current
+ * device (its per-stream workspace and counters, retired ones included); 0
+ * when every call on the stream brought its own workspace.  No counterpart
+ * in the reference: a check for callers that own all buffers. */
+uint64_t nne_stream_resource_bytes(void *stream);
+
+/* ---- caller-owned workspace ----------------------------------------------
+ * Split computations hand partial results between the workgroups of one
+ * launch: split-K decode and few-query attention, the key split of prefill
+ * problems too small to fill the device, and the fused decode prologue.
+ * They need
+ *   records   device memory for the partial records (no initialisation), and
+ *   counters  uint32 arrival counters that are zero when the call starts;
+ *             every call leaves the counters it used at zero, so an array
+ *             zeroed once with nne_counters_init serves any number of calls
+ *             of any entry point.
+ * The *_workspace_size queries give what a call needs; one workspace sized
+ * for the largest of them serves every call.  Calls that share a workspace
+ * must not overlap in time (calls on one stream never do).  A NULL
+ * workspace makes the call use the library's per-stream one (allocated in
+ * stream order on first use, kept until nne_stream_release or the end of the
+ * process). */
+typedef struct nne_workspace {
+    void *records;          /* device memory, records_bytes long */
+    uint64_t records_bytes;
+    uint32_t *counters;     /* device array of n_counters zeroed counters */
+    uint64_t n_counters;
+} nne_workspace_t;
+
+typedef struct nne_workspace_size {
+    uint64_t records_bytes;
+    uint64_t n_counters;
+} nne_workspace_size_t;
+
+/* Zeroes n counters on the stream with a fill kernel (no memset node, so the
+ * call can be captured in a HIP graph). */
+int nne_counters_init(uint32_t *counters, uint64_t n, void *stream);
 
 /* ---- prefill -------------------------------------------------------------
  * Replaces `flash_attention_forward(q, k, v, is_causal, scale, block_size_r,
@@ -91,13 +134,34 @@ int nne_flash_attention_forward(const float *q, const int64_t q_shape[4], const 
  * |scores| < ~4e3.  Few-query problems (Hq/Hkv * Tq <= 16 rows per KV head,
  * causal or not) run on the split-K kernel; problems with fewer work items
  * than the device has CUs split their key range across workgroups.  Both use
- * the library's per-stream workspace and counters (as nne_decode_attention
- * with a NULL workspace); calls on one stream run in order. */
+ * the library's per-stream workspace and counters here; nne_attention_forward_ws
+ * takes the caller's. */
 int nne_attention_forward(const float *q, const int64_t q_shape[4], const int64_t q_strides[4],
                           const float *k, const int64_t k_shape[4], const int64_t k_strides[4],
                           const float *v, const int64_t v_shape[4], const int64_t v_strides[4],
                           float *o, const int64_t o_strides[4], int is_causal, int64_t q_offset,
                           int has_scale, float scale, void *stream);
+
+/* Workspace a prefill call of this geometry may need (an upper bound over
+ * every layout of the same shapes); {0, 0} for problems that need none.
+ * NNE_ESHAPE / NNE_EINVAL as the call itself would return. */
+int nne_attention_workspace_size(const int64_t q_shape[4], const int64_t k_shape[4], int is_causal,
+                                 int64_t q_offset, nne_workspace_size_t *out);
+
+/* nne_flash_attention_forward and nne_attention_forward with the caller's
+ * workspace (NULL: the library's per-stream one). */
+int nne_flash_attention_forward_ws(const float *q, const int64_t q_shape[4],
+                                   const int64_t q_strides[4], const float *k,
+                                   const int64_t k_shape[4], const int64_t k_strides[4],
+                                   const float *v, const int64_t v_shape[4],
+                                   const int64_t v_strides[4], float *o, const int64_t o_strides[4],
+                                   int is_causal, int has_scale, float scale, int64_t block_size_r,
+                                   int64_t block_size_c, const nne_workspace_t *ws, void *stream);
+int nne_attention_forward_ws(const float *q, const int64_t q_shape[4], const int64_t q_strides[4],
+                             const float *k, const int64_t k_shape[4], const int64_t k_strides[4],
+                             const float *v, const int64_t v_shape[4], const int64_t v_strides[4],
+                             float *o, const int64_t o_strides[4], int is_causal, int64_t q_offset,
+                             int has_scale, float scale, const nne_workspace_t *ws, void *stream);
 
 /* ---- KV cache ------------------------------------------------------------
  * Replaces KVCache (src/nn/kv_cache.rs:11-74) and the per-layer
@@ -117,41 +181,36 @@ int nne_kv_append(float *k_cache, float *v_cache, int32_t *lens_dev, int32_t *le
                   const int64_t v_new_strides[4], int64_t B, int64_t Hkv, int64_t capacity,
                   int64_t d, int64_t t_new, void *stream);
 
-/* Device workspace bytes needed by nne_decode_attention / nne_decode_step for
- * sequences up to max_len keys (0 for invalid geometry).  It holds per-split
- * partial results; calls that share a workspace must not overlap in time. */
+/* Records bytes a decode call of this geometry needs (any cache length; 0
+ * for geometry the decode kernel does not take).  Decode calls also need
+ * B * Hkv counters: nne_decode_workspace_size gives both. */
 uint64_t nne_decode_workspace_bytes(int64_t B, int64_t Hq, int64_t Hkv, int64_t d, int64_t max_len);
-
+int nne_decode_workspace_size(int64_t B, int64_t Hq, int64_t Hkv, int64_t d,
+                              nne_workspace_size_t *out);
 
 /* Single-token decode attention over the cache: q [B, Hq, 1, d] attends to
  * the first lens[b] rows of its sequence, no mask (llama.rs:239-296 with
- * t = 1).  Ragged lengths are allowed; Hq / Hkv <= 16.  workspace may be NULL
- * (the library then uses its own per-stream workspace, allocated in stream
- * order on first use and kept until the process ends) or a device buffer of
- * at least nne_decode_workspace_bytes(B, Hq, Hkv, d, max(lens_host)) bytes.
- * The library also keeps, per (device, stream), a small zeroed array of
- * arrival counters that launches on that stream share; launches on
- * different streams never share it. */
+ * t = 1).  Ragged lengths are allowed; Hq / Hkv <= 16.  ws: the caller's
+ * workspace of at least nne_decode_workspace_size, or NULL for the library's
+ * per-stream one. */
 int nne_decode_attention(const float *q, const int64_t q_strides[4], const float *k_cache,
                          const float *v_cache, const int32_t *lens_dev, const int32_t *lens_host,
                          float *o, const int64_t o_strides[4], int64_t B, int64_t Hq, int64_t Hkv,
-                         int64_t capacity, int64_t d, int has_scale, float scale, void *workspace,
-                         uint64_t workspace_bytes, void *stream);
+                         int64_t capacity, int64_t d, int has_scale, float scale,
+                         const nne_workspace_t *ws, void *stream);
 
 /* One decode step with the semantics of nne_kv_append of one row followed by
  * nne_decode_attention -- the append-then-attend order of llama.rs:239-296
  * and attention.rs:79-122 -- fused: the new row is attended from k_new /
  * v_new directly and stored into the cache by the attention kernel, and
- * lens_dev / lens_host advance by one.  Workspace sized for max(lens_host) + 1
- * keys (or NULL).
+ * lens_dev / lens_host advance by one.  ws as for nne_decode_attention.
  * NNE_ECAPACITY (nothing written) if a sequence is full. */
 int nne_decode_step(const float *q, const int64_t q_strides[4], float *k_cache, float *v_cache,
                     int32_t *lens_dev, int32_t *lens_host, const float *k_new,
                     const int64_t k_new_strides[4], const float *v_new,
                     const int64_t v_new_strides[4], float *o, const int64_t o_strides[4],
                     int64_t B, int64_t Hq, int64_t Hkv, int64_t capacity, int64_t d,
-                    int has_scale, float scale, void *workspace, uint64_t workspace_bytes,
-                    void *stream);
+                    int has_scale, float scale, const nne_workspace_t *ws, void *stream);
 
 /* Bytes of device scratch behind nne_decode_step_noalloc, one copy per GPU. */
 #define NNE_NOALLOC_SCRATCH_BYTES (16u << 20)
@@ -224,7 +283,8 @@ int nne_qkv_pack(const float *wq, const float *wk, const float *wv, float *packe
  * [H * d] or NULL (llama.rs uses Linear::without_bias).  One launch streams
  * the weights once; the reduction over C is split across workgroups whose
  * partial sums are merged inside the launch, in a fixed order, with the
- * library's per-stream workspace and counters (as nne_decode_attention).
+ * library's per-stream workspace and counters (nne_qkv_rope_ws takes the
+ * caller's).
  * Requires d % 64 == 0, C % 64 == 0, x rows 16-byte aligned with
  * x_row_stride >= C and a multiple of 4.  NNE_ESHAPE if d != table_head_dim;
  * NNE_EINVAL if pos[b] >= max_seq_len.  With cos_table = sin_table = NULL
@@ -236,6 +296,17 @@ int nne_qkv_rope(const float *x, int64_t x_row_stride, const float *w_packed, co
                  int64_t max_seq_len, int64_t table_head_dim, const int32_t *pos_dev,
                  const int32_t *pos_host, float *q_out, float *k_out, float *v_out, int64_t B,
                  int64_t C, int64_t Hq, int64_t Hkv, int64_t d, void *stream);
+
+/* Workspace of nne_qkv_rope_ws (any B). */
+int nne_qkv_workspace_size(int64_t C, int64_t Hq, int64_t Hkv, int64_t d, nne_workspace_size_t *out);
+
+/* nne_qkv_rope with the caller's workspace (NULL: the library's per-stream one). */
+int nne_qkv_rope_ws(const float *x, int64_t x_row_stride, const float *w_packed, const float *bq,
+                    const float *bk, const float *bv, const float *cos_table, const float *sin_table,
+                    int64_t max_seq_len, int64_t table_head_dim, const int32_t *pos_dev,
+                    const int32_t *pos_host, float *q_out, float *k_out, float *v_out, int64_t B,
+                    int64_t C, int64_t Hq, int64_t Hkv, int64_t d, const nne_workspace_t *ws,
+                    void *stream);
 
 #ifdef __cplusplus
 }

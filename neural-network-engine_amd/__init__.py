@@ -65,6 +65,21 @@ _i64p = ctypes.POINTER(ctypes.c_int64)
 _i32p = ctypes.POINTER(ctypes.c_int32)
 _vp = ctypes.c_void_p
 
+
+class NneWorkspace(ctypes.Structure):
+    """nne_workspace_t: caller-owned records buffer and zeroed counters."""
+    _fields_ = [("records", ctypes.c_void_p), ("records_bytes", ctypes.c_uint64),
+                ("counters", ctypes.c_void_p), ("n_counters", ctypes.c_uint64)]
+
+
+class NneWorkspaceSize(ctypes.Structure):
+    """nne_workspace_size_t."""
+    _fields_ = [("records_bytes", ctypes.c_uint64), ("n_counters", ctypes.c_uint64)]
+
+
+_wsp = ctypes.POINTER(NneWorkspace)
+_wszp = ctypes.POINTER(NneWorkspaceSize)
+
 # exported symbol -> (restype, argtypes); mirrors include/nne_attn.h
 SIGNATURES = {
     "nne_abi_version": (ctypes.c_int, []),
@@ -76,25 +91,37 @@ SIGNATURES = {
     "nne_memcpy_d2d": (ctypes.c_int, [_vp, _vp, ctypes.c_uint64, _vp]),
     "nne_stream_sync": (ctypes.c_int, [_vp]),
     "nne_stream_release": (ctypes.c_int, [_vp]),
+    "nne_stream_resource_bytes": (ctypes.c_uint64, [_vp]),
+    "nne_counters_init": (ctypes.c_int, [_vp, ctypes.c_uint64, _vp]),
     "nne_flash_attention_forward": (ctypes.c_int, [
         _vp, _i64p, _i64p, _vp, _i64p, _i64p, _vp, _i64p, _i64p, _vp, _i64p,
         ctypes.c_int, ctypes.c_int, ctypes.c_float, ctypes.c_int64, ctypes.c_int64, _vp]),
     "nne_attention_forward": (ctypes.c_int, [
         _vp, _i64p, _i64p, _vp, _i64p, _i64p, _vp, _i64p, _i64p, _vp, _i64p,
         ctypes.c_int, ctypes.c_int64, ctypes.c_int, ctypes.c_float, _vp]),
+    "nne_flash_attention_forward_ws": (ctypes.c_int, [
+        _vp, _i64p, _i64p, _vp, _i64p, _i64p, _vp, _i64p, _i64p, _vp, _i64p,
+        ctypes.c_int, ctypes.c_int, ctypes.c_float, ctypes.c_int64, ctypes.c_int64, _wsp, _vp]),
+    "nne_attention_forward_ws": (ctypes.c_int, [
+        _vp, _i64p, _i64p, _vp, _i64p, _i64p, _vp, _i64p, _i64p, _vp, _i64p,
+        ctypes.c_int, ctypes.c_int64, ctypes.c_int, ctypes.c_float, _wsp, _vp]),
+    "nne_attention_workspace_size": (ctypes.c_int, [_i64p, _i64p, ctypes.c_int, ctypes.c_int64,
+                                                    _wszp]),
     "nne_kv_append": (ctypes.c_int, [
         _vp, _vp, _vp, _i32p, _vp, _i64p, _vp, _i64p, ctypes.c_int64, ctypes.c_int64,
         ctypes.c_int64, ctypes.c_int64, ctypes.c_int64, _vp]),
     "nne_decode_workspace_bytes": (ctypes.c_uint64, [
         ctypes.c_int64, ctypes.c_int64, ctypes.c_int64, ctypes.c_int64, ctypes.c_int64]),
+    "nne_decode_workspace_size": (ctypes.c_int, [
+        ctypes.c_int64, ctypes.c_int64, ctypes.c_int64, ctypes.c_int64, _wszp]),
     "nne_decode_attention": (ctypes.c_int, [
         _vp, _i64p, _vp, _vp, _vp, _i32p, _vp, _i64p, ctypes.c_int64, ctypes.c_int64,
-        ctypes.c_int64, ctypes.c_int64, ctypes.c_int64, ctypes.c_int, ctypes.c_float, _vp,
-        ctypes.c_uint64, _vp]),
+        ctypes.c_int64, ctypes.c_int64, ctypes.c_int64, ctypes.c_int, ctypes.c_float, _wsp,
+        _vp]),
     "nne_decode_step": (ctypes.c_int, [
         _vp, _i64p, _vp, _vp, _vp, _i32p, _vp, _i64p, _vp, _i64p, _vp, _i64p,
         ctypes.c_int64, ctypes.c_int64, ctypes.c_int64, ctypes.c_int64, ctypes.c_int64,
-        ctypes.c_int, ctypes.c_float, _vp, ctypes.c_uint64, _vp]),
+        ctypes.c_int, ctypes.c_float, _wsp, _vp]),
     "nne_decode_step_noalloc": (ctypes.c_int, [
         _vp, _i64p, _vp, _vp, _vp, _i32p, _vp, _i64p, _vp, _i64p, _vp, _i64p,
         ctypes.c_int64, ctypes.c_int64, ctypes.c_int64, ctypes.c_int64, ctypes.c_int64,
@@ -111,6 +138,12 @@ SIGNATURES = {
         _vp, ctypes.c_int64, _vp, _vp, _vp, _vp, _vp, _vp, ctypes.c_int64,
         ctypes.c_int64, _vp, _i32p, _vp, _vp, _vp, ctypes.c_int64, ctypes.c_int64,
         ctypes.c_int64, ctypes.c_int64, ctypes.c_int64, _vp]),
+    "nne_qkv_workspace_size": (ctypes.c_int, [
+        ctypes.c_int64, ctypes.c_int64, ctypes.c_int64, ctypes.c_int64, _wszp]),
+    "nne_qkv_rope_ws": (ctypes.c_int, [
+        _vp, ctypes.c_int64, _vp, _vp, _vp, _vp, _vp, _vp, ctypes.c_int64,
+        ctypes.c_int64, _vp, _i32p, _vp, _vp, _vp, ctypes.c_int64, ctypes.c_int64,
+        ctypes.c_int64, ctypes.c_int64, ctypes.c_int64, _wsp, _vp]),
 }
 
 
@@ -154,6 +187,56 @@ def release_stream(stream=None):
     check(lib().nne_stream_release(_stream(stream)))
 
 
+def stream_resource_bytes(stream=None):
+    """Bytes the library holds for ``stream`` (0 when every call on it
+    brought its own workspace)."""
+    return int(lib().nne_stream_resource_bytes(_stream(stream)))
+
+
+class Workspace:
+    """A caller-owned workspace (nne_workspace_t): a records buffer and an
+    array of arrival counters zeroed once (every call leaves them zeroed),
+    both torch tensors on ``device``, grown on demand by ``reserve``.  One
+    workspace serves every entry point; calls that share it must not overlap
+    in time (calls on one stream never do)."""
+
+    def __init__(self, device="cuda"):
+        self.device = device
+        self.records = None
+        self.counters = None
+
+    def reserve(self, size, stream=None):
+        """Grows the buffers to at least ``size`` (an NneWorkspaceSize)."""
+        import torch
+        if size.records_bytes and (self.records is None or
+                                   self.records.numel() < size.records_bytes):
+            self.records = torch.empty(int(size.records_bytes), dtype=torch.uint8,
+                                       device=self.device)
+        if size.n_counters and (self.counters is None or
+                                self.counters.numel() < size.n_counters):
+            self.counters = torch.empty(int(size.n_counters), dtype=torch.int32,
+                                        device=self.device)
+            check(lib().nne_counters_init(self.counters.data_ptr(), self.counters.numel(),
+                                          _stream(stream)))
+        return self
+
+    def struct(self):
+        w = NneWorkspace()
+        if self.records is not None:
+            w.records, w.records_bytes = self.records.data_ptr(), self.records.numel()
+        if self.counters is not None:
+            w.counters, w.n_counters = self.counters.data_ptr(), self.counters.numel()
+        return ctypes.byref(w), w
+
+
+def _ws_arg(workspace, size, stream):
+    """(pointer argument, keep-alive) for an optional Workspace."""
+    if workspace is None:
+        return None, None
+    workspace.reserve(size, stream)
+    return workspace.struct()
+
+
 def _require_f32_cuda(*ts):
     import torch
     for t in ts:
@@ -169,12 +252,20 @@ def _shape4(t, what):
     return t.shape, t.stride()
 
 
+def attention_workspace_size(q_shape, k_shape, is_causal, q_offset=0):
+    size = NneWorkspaceSize()
+    check(lib().nne_attention_workspace_size(_i64(q_shape), _i64(k_shape), int(bool(is_causal)),
+                                             int(q_offset), ctypes.byref(size)))
+    return size
+
+
 def flash_attention_forward(q, k, v, is_causal, scale=None, block_size_r=64, block_size_c=64,
-                            out=None, stream=None):
+                            out=None, stream=None, workspace=None):
     """flash_attention_forward (src/nn/flash_attention.rs:19-199) on the GPU.
 
     q, k, v: float32 CUDA tensors [B, H, T, d] with any strides.  Returns a new
-    contiguous [B, H, Tq, d] tensor (or fills ``out``)."""
+    contiguous [B, H, Tq, d] tensor (or fills ``out``).  ``workspace``: a
+    Workspace the call uses instead of the library's per-stream one."""
     import torch
     qs, qst = _shape4(q, "Q")
     ks, kst = _shape4(k, "K")
@@ -182,19 +273,25 @@ def flash_attention_forward(q, k, v, is_causal, scale=None, block_size_r=64, blo
     _require_f32_cuda(q, k, v)
     if out is None:
         out = torch.empty(tuple(qs), dtype=torch.float32, device=q.device)
-    check(lib().nne_flash_attention_forward(
+    wsp, keep = None, None
+    if workspace is not None and qs[1] == ks[1]:
+        wsp, keep = _ws_arg(workspace, attention_workspace_size(qs, ks, is_causal), stream)
+    check(lib().nne_flash_attention_forward_ws(
         q.data_ptr(), _i64(qs), _i64(qst), k.data_ptr(), _i64(ks), _i64(kst),
         v.data_ptr(), _i64(vs), _i64(vst), out.data_ptr(), _i64(out.stride()),
         int(bool(is_causal)), int(scale is not None), float(scale or 0.0),
-        int(block_size_r), int(block_size_c), _stream(stream)))
+        int(block_size_r), int(block_size_c), wsp, _stream(stream)))
     return out
 
 
-def attention_forward(q, k, v, is_causal, q_offset=0, scale=None, out=None, stream=None):
+def attention_forward(q, k, v, is_causal, q_offset=0, scale=None, out=None, stream=None,
+                      workspace=None):
     """GQA-capable attention: q [B, Hq, Tq, d], k/v [B, Hkv, Tk, d], Hkv | Hq.
 
     Query head hq reads KV head hq // (Hq // Hkv) (src/models/llama.rs:256-266);
-    with is_causal, key c is visible to row r iff c <= r + q_offset."""
+    with is_causal, key c is visible to row r iff c <= r + q_offset.
+    ``workspace``: a Workspace the call uses instead of the library's
+    per-stream one."""
     import torch
     qs, qst = _shape4(q, "Q")
     ks, kst = _shape4(k, "K")
@@ -202,11 +299,15 @@ def attention_forward(q, k, v, is_causal, q_offset=0, scale=None, out=None, stre
     _require_f32_cuda(q, k, v)
     if out is None:
         out = torch.empty(tuple(qs), dtype=torch.float32, device=q.device)
-    check(lib().nne_attention_forward(
+    wsp, keep = None, None
+    if workspace is not None:
+        wsp, keep = _ws_arg(workspace, attention_workspace_size(qs, ks, is_causal, q_offset),
+                            stream)
+    check(lib().nne_attention_forward_ws(
         q.data_ptr(), _i64(qs), _i64(qst), k.data_ptr(), _i64(ks), _i64(kst),
         v.data_ptr(), _i64(vs), _i64(vst), out.data_ptr(), _i64(out.stride()),
         int(bool(is_causal)), int(q_offset), int(scale is not None), float(scale or 0.0),
-        _stream(stream)))
+        wsp, _stream(stream)))
     return out
 
 
@@ -227,7 +328,7 @@ class KVCache:
         self.lens_dev = [torch.zeros(self.batch, dtype=torch.int32, device=device)
                          for _ in range(num_layers)]
         self.lens_host = [np.zeros(self.batch, dtype=np.int32) for _ in range(num_layers)]
-        self._ws = None
+        self._ws = Workspace(device)
 
     # kv_cache.rs:25-29
     def reset(self):
@@ -278,14 +379,17 @@ class KVCache:
         L = int(lh.max()) if self.batch else 0
         return self.k[layer_idx][:, :, :L], self.v[layer_idx][:, :, :L]
 
-    def workspace(self, num_heads):
-        """Decode workspace sized for full sequences (allocated once)."""
-        import torch
-        need = lib().nne_decode_workspace_bytes(self.batch, num_heads, self.num_kv_heads,
-                                                self.head_dim, self.capacity)
-        if need and (self._ws is None or self._ws.numel() < need):
-            self._ws = torch.empty(int(need), dtype=torch.uint8, device=self.k[0].device)
-        return self._ws
+    def workspace(self, num_heads, stream=None):
+        """The cache's own decode workspace (records and zeroed counters),
+        grown to what num_heads query heads need: (pointer argument,
+        keep-alive).  The library allocates nothing for these calls."""
+        size = NneWorkspaceSize()
+        rc = lib().nne_decode_workspace_size(self.batch, num_heads, self.num_kv_heads,
+                                             self.head_dim, ctypes.byref(size))
+        if rc != NNE_OK:
+            return None, None      # the call itself reports the geometry error
+        self._ws.reserve(size, stream)
+        return self._ws.struct()
 
     def attend(self, layer_idx, q, out=None, scale=None, stream=None):
         """Decode attention of q [B, Hq, 1, d] over the cached rows."""
@@ -295,15 +399,13 @@ class KVCache:
         hq = q.shape[1]
         if out is None:
             out = torch.empty(q.shape, dtype=torch.float32, device=q.device)
-        ws = self.workspace(hq)
+        wsp, keep = self.workspace(hq, stream)
         check(lib().nne_decode_attention(
             q.data_ptr(), _i64(q.stride()), self.k[layer_idx].data_ptr(),
             self.v[layer_idx].data_ptr(), self.lens_dev[layer_idx].data_ptr(),
             self.lens_host[layer_idx].ctypes.data_as(_i32p), out.data_ptr(), _i64(out.stride()),
             self.batch, hq, self.num_kv_heads, self.capacity, self.head_dim,
-            int(scale is not None), float(scale or 0.0),
-            ws.data_ptr() if ws is not None else None, ws.numel() if ws is not None else 0,
-            _stream(stream)))
+            int(scale is not None), float(scale or 0.0), wsp, _stream(stream)))
         return out
 
     def decode_step(self, layer_idx, q, k_new, v_new, out=None, scale=None, stream=None):
@@ -321,16 +423,14 @@ class KVCache:
             out = torch.empty(q.shape, dtype=torch.float32, device=q.device)
         if not decode_kernel_fits(self.batch, hq, self.num_kv_heads, self.head_dim):
             return self._append_then_attend(layer_idx, q, k_new, v_new, out, scale, stream)
-        ws = self.workspace(hq)
+        wsp, keep = self.workspace(hq, stream)
         check(lib().nne_decode_step(
             q.data_ptr(), _i64(q.stride()), self.k[layer_idx].data_ptr(),
             self.v[layer_idx].data_ptr(), self.lens_dev[layer_idx].data_ptr(),
             self.lens_host[layer_idx].ctypes.data_as(_i32p), k_new.data_ptr(),
             _i64(k_new.stride()), v_new.data_ptr(), _i64(v_new.stride()), out.data_ptr(),
             _i64(out.stride()), self.batch, hq, self.num_kv_heads, self.capacity, self.head_dim,
-            int(scale is not None), float(scale or 0.0),
-            ws.data_ptr() if ws is not None else None, ws.numel() if ws is not None else 0,
-            _stream(stream)))
+            int(scale is not None), float(scale or 0.0), wsp, _stream(stream)))
         return out
 
     def _append_then_attend(self, layer_idx, q, k_new, v_new, out, scale, stream):
@@ -344,12 +444,13 @@ class KVCache:
             idx = np.nonzero(lens == L)[0]
             if len(idx) == self.batch:
                 attention_forward(q, kl[:, :, :L], vl[:, :, :L], False, scale=scale, out=out,
-                                  stream=stream)
+                                  stream=stream, workspace=self._ws)
                 break
             for bi in idx:
                 bi = int(bi)
                 attention_forward(q[bi:bi + 1], kl[bi:bi + 1, :, :L], vl[bi:bi + 1, :, :L], False,
-                                  scale=scale, out=out[bi:bi + 1], stream=stream)
+                                  scale=scale, out=out[bi:bi + 1], stream=stream,
+                                  workspace=self._ws)
         return out
 
 
@@ -357,7 +458,7 @@ def decode_kernel_fits(batch, num_heads, num_kv_heads, head_dim):
     """True when the fused append + attend kernel takes this geometry (the
     library reports a workspace size for it)."""
     return lib().nne_decode_workspace_bytes(max(int(batch), 1), int(num_heads),
-                                            int(num_kv_heads), int(head_dim), 1) > 0
+                                            int(num_kv_heads), int(head_dim), 0) > 0
 
 
 class FlashAttention:
@@ -466,12 +567,14 @@ def qkv_pack(wq, wk, wv, num_heads, num_kv_heads, stream=None):
 
 
 def qkv_rope(x, w_packed, bq, bk, bv, rope, pos_dev, pos_host, num_heads, num_kv_heads,
-             q_out=None, k_out=None, v_out=None, stream=None, head_dim=None):
+             q_out=None, k_out=None, v_out=None, stream=None, head_dim=None, workspace=None):
     """Fused decode prologue: x [B, C] (or [B, 1, C]) -> q [B, Hq, 1, d] and
     k, v [B, Hkv, 1, d] with q = RoPE(x Wq^T + bq), k = RoPE(x Wk^T + bk),
     v = x Wv^T + bv at positions pos (int32, device and host copies);
     ``w_packed`` comes from ``qkv_pack``.  With rope=None nothing is rotated
-    (the MultiHeadAttention projections) and ``head_dim`` gives d."""
+    (the MultiHeadAttention projections) and ``head_dim`` gives d.
+    ``workspace``: a Workspace the call uses instead of the library's
+    per-stream one."""
     import torch
     x2 = x.reshape(x.shape[0], x.shape[-1]) if x.dim() == 3 else x
     _require_f32_cuda(x2, w_packed)
@@ -496,10 +599,15 @@ def qkv_rope(x, w_packed, bq, bk, bv, rope, pos_dev, pos_host, num_heads, num_kv
                   pos_dev.data_ptr(), pos_host.ctypes.data_as(_i32p))
     else:
         tables = (None, None, 0, d, None, None)
-    check(lib().nne_qkv_rope(
+    wsp, keep = None, None
+    if workspace is not None:
+        size = NneWorkspaceSize()
+        check(lib().nne_qkv_workspace_size(c, num_heads, num_kv_heads, d, ctypes.byref(size)))
+        wsp, keep = _ws_arg(workspace, size, stream)
+    check(lib().nne_qkv_rope_ws(
         x2.data_ptr(), x2.stride(0), w_packed.data_ptr(), ptr(bq), ptr(bk), ptr(bv), *tables,
         q_out.data_ptr(), k_out.data_ptr(), v_out.data_ptr(), b, c, num_heads, num_kv_heads, d,
-        _stream(stream)))
+        wsp, _stream(stream)))
     return q_out, k_out, v_out
 
 
@@ -560,7 +668,8 @@ class GroupedQueryAttention:
         if cache is not None and t == 1:
             if self.w_packed is not None:
                 q, k_new, v_new = qkv_rope(x, self.w_packed, None, None, None, self.rope,
-                                           cache.lens_dev[layer_idx], sp, hq, hkv, stream=stream)
+                                           cache.lens_dev[layer_idx], sp, hq, hkv, stream=stream,
+                                           workspace=cache._ws)
             else:
                 q = torch.nn.functional.linear(x, self.wq).view(b, 1, hq, d).transpose(1, 2)
                 k_new = torch.nn.functional.linear(x, self.wk).view(b, 1, hkv, d).transpose(1, 2)
@@ -644,7 +753,7 @@ class MultiHeadAttention:
             if self.w_packed is not None:
                 q, k_new, v_new = qkv_rope(x, self.w_packed, self.q_proj[1], self.k_proj[1],
                                            self.v_proj[1], None, None, None, h, h, stream=stream,
-                                           head_dim=d)
+                                           head_dim=d, workspace=cache._ws)
             else:
                 q = self._heads(torch.nn.functional.linear(x, *self.q_proj), b, 1)
                 k_new = self._heads(torch.nn.functional.linear(x, *self.k_proj), b, 1).contiguous()

@@ -83,6 +83,7 @@ struct StreamResources {
     void* ws;
     uint64_t ws_bytes;
     std::vector<void*> retired;
+    uint64_t retired_bytes;
 };
 std::mutex g_res_mu;
 std::vector<StreamResources> g_res;
@@ -100,7 +101,7 @@ hipError_t stream_resources(int64_t n, uint64_t ws_bytes, hipStream_t s, uint32_
     for (auto& x : g_res)
         if (x.dev == dev && x.stream == s && x.thread == th) r = &x;
     if (!r) {
-        g_res.push_back(StreamResources{dev, s, th, nullptr, 0, nullptr, 0, {}});
+        g_res.push_back(StreamResources{dev, s, th, nullptr, 0, nullptr, 0, {}, 0});
         r = &g_res.back();
     }
     if (r->n_counters < n) {
@@ -111,7 +112,10 @@ hipError_t stream_resources(int64_t n, uint64_t ws_bytes, hipStream_t s, uint32_
         if (e != hipSuccess) return e;
         e = nne::zero_counters(p, cap, s);
         if (e != hipSuccess) return e;
-        if (r->counters) r->retired.push_back(r->counters);
+        if (r->counters) {
+            r->retired.push_back(r->counters);
+            r->retired_bytes += (uint64_t)r->n_counters * 4;
+        }
         r->counters = p;
         r->n_counters = cap;
     }
@@ -123,13 +127,39 @@ hipError_t stream_resources(int64_t n, uint64_t ws_bytes, hipStream_t s, uint32_
             void* p = nullptr;
             e = hipMallocAsync(&p, cap, s);
             if (e != hipSuccess) return e;
-            if (r->ws) r->retired.push_back(r->ws);
+            if (r->ws) {
+                r->retired.push_back(r->ws);
+                r->retired_bytes += r->ws_bytes;
+            }
             r->ws = p;
             r->ws_bytes = cap;
         }
         *ws = r->ws;
     }
     return hipSuccess;
+}
+
+// Records and counters of one call: the caller's workspace, checked against
+// what the call needs, or (ws == NULL) the stream's library-side ones.
+int call_workspace(const nne_workspace_t* ws, uint64_t need_bytes, int64_t need_counters,
+                   hipStream_t s, void** records, uint32_t** counters, const char* what) {
+    if (ws) {
+        if (need_bytes > 0 && (!ws->records || ws->records_bytes < need_bytes))
+            return fail(NNE_EINVAL, "Invalid configuration or argument: %s workspace holds %llu "
+                                    "record bytes, the call needs %llu", what,
+                        (unsigned long long)(ws->records ? ws->records_bytes : 0),
+                        (unsigned long long)need_bytes);
+        if (need_counters > 0 && (!ws->counters || ws->n_counters < (uint64_t)need_counters))
+            return fail(NNE_EINVAL, "Invalid configuration or argument: %s workspace holds %llu "
+                                    "counters, the call needs %lld", what,
+                        (unsigned long long)(ws->counters ? ws->n_counters : 0),
+                        (long long)need_counters);
+        *records = ws->records;
+        *counters = ws->counters;
+        return NNE_OK;
+    }
+    const hipError_t e = stream_resources(need_counters, need_bytes, s, counters, records);
+    return e == hipSuccess ? NNE_OK : hip_fail(e, what);
 }
 
 // 16-byte vector access is valid for this view: unit dim stride and every
@@ -161,7 +191,7 @@ float softmax_scale(int has_scale, float scale, int64_t d) {
 int run_attention(const float* q, const int64_t* qs_, const int64_t* qst, const float* k,
                   const int64_t* ks_, const int64_t* kst, const float* v, const int64_t* vst,
                   float* o, const int64_t* ost, bool causal, int64_t q_offset, float scale,
-                  hipStream_t stream) {
+                  const nne_workspace_t* wsp, hipStream_t stream) {
     const int B = (int)qs_[0], Hq = (int)qs_[1], Tq = (int)qs_[2], d = (int)qs_[3];
     const int Hkv = (int)ks_[1], Tk = (int)ks_[2];
     if ((int64_t)B * Hq * Tq == 0 || d == 0) return NNE_OK;
@@ -201,9 +231,11 @@ int run_attention(const float* q, const int64_t* qs_, const int64_t* qst, const 
         const nne::SplitKWorkspace w = nne::splitk_workspace_layout(B, Hkv, (int)rows, d);
         uint32_t* counters = nullptr;
         void* ws = nullptr;
-        hipError_t e = stream_resources((int64_t)B * Hkv, w.total_bytes, stream, &counters, &ws);
-        if (e != hipSuccess) return hip_fail(e, "split-K workspace");
-        e = nne::launch_splitk(p, (int64_t)B * Hkv * tk, (int)tk, ws, stream, nullptr, counters);
+        const int rc = call_workspace(wsp, w.total_bytes, (int64_t)B * Hkv, stream, &ws, &counters,
+                                      "few-query attention");
+        if (rc != NNE_OK) return rc;
+        hipError_t e = nne::launch_splitk(p, (int64_t)B * Hkv * tk, (int)tk, ws, stream, nullptr,
+                                          counters);
         if (e != hipSuccess) return hip_fail(e, "split-K attention launch");
         return NNE_OK;
     }
@@ -222,14 +254,42 @@ int run_attention(const float* q, const int64_t* qs_, const int64_t* qst, const 
     if (p.n_chunks > 1) {
         uint32_t* counters = nullptr;
         void* ws = nullptr;
-        hipError_t e = stream_resources(plan.n_counters, plan.ws_bytes, stream, &counters, &ws);
-        if (e != hipSuccess) return hip_fail(e, "prefill split workspace");
+        const int rc = call_workspace(wsp, plan.ws_bytes, plan.n_counters, stream, &ws, &counters,
+                                      "prefill key split");
+        if (rc != NNE_OK) return rc;
         p.ws = static_cast<float*>(ws);
         p.cnt = counters;
     }
     hipError_t e = nne::launch_prefill(p, causal, vec, stream);
     if (e != hipSuccess) return hip_fail(e, "prefill attention launch");
     return NNE_OK;
+}
+
+// Upper bound on the workspace of a prefill call: the few-query layout and
+// the key-split plan of the same shapes (which one runs depends on strides).
+nne_workspace_size_t attention_workspace(const int64_t* qs_, const int64_t* ks_, bool causal,
+                                         int64_t q_offset) {
+    nne_workspace_size_t r{0, 0};
+    const int B = (int)qs_[0], Hq = (int)qs_[1], Tq = (int)qs_[2], d = (int)qs_[3];
+    const int Hkv = (int)ks_[1], Tk = (int)ks_[2];
+    if ((int64_t)B * Hq * Tq == 0 || d == 0 || Hkv == 0 || nne::prefill_padded_dim(d) == 0) return r;
+    const int qoff = (int)std::max<int64_t>(-(1 << 30), std::min<int64_t>(q_offset, 1 << 30));
+    const int64_t rows = (int64_t)(Hq / Hkv) * Tq;
+    const int64_t tk = causal ? std::min<int64_t>(Tk, (int64_t)qoff + Tq) : Tk;
+    if (rows <= nne::splitk_max_rows() && tk > 0 && B <= nne::splitk_max_seqs() && d % 4 == 0) {
+        const nne::SplitKWorkspace w = nne::splitk_workspace_layout(B, Hkv, (int)rows, d);
+        r.records_bytes = w.total_bytes;
+        r.n_counters = (uint64_t)B * Hkv;
+    }
+    nne::PrefillParams p{};
+    p.B = B; p.Hq = Hq; p.Hkv = Hkv; p.Tq = Tq; p.Tk = Tk; p.d = d;
+    p.q_offset = qoff;
+    const nne::PrefillSplit plan = nne::prefill_split_plan(p, causal, true);
+    if (p.n_chunks > 1) {
+        r.records_bytes = std::max<uint64_t>(r.records_bytes, plan.ws_bytes);
+        r.n_counters = std::max<uint64_t>(r.n_counters, (uint64_t)plan.n_counters);
+    }
+    return r;
 }
 
 struct Resolved {
@@ -343,12 +403,10 @@ int nne_stream_release(void* stream) {
     return NNE_OK;
 }
 
-int nne_flash_attention_forward(const float* q, const int64_t q_shape[4], const int64_t q_strides[4],
-                                const float* k, const int64_t k_shape[4], const int64_t k_strides[4],
-                                const float* v, const int64_t v_shape[4], const int64_t v_strides[4],
-                                float* o, const int64_t o_strides[4], int is_causal, int has_scale,
-                                float scale, int64_t block_size_r, int64_t block_size_c,
-                                void* stream) {
+namespace {
+
+// flash_attention_forward's checks (flash_attention.rs:32-48).
+int check_flash_shapes(const int64_t* q_shape, const int64_t* k_shape, const int64_t* v_shape) {
     if (!q_shape || !k_shape || !v_shape)
         return fail(NNE_EINVAL, "Invalid configuration or argument: FlashAttention expects 4D "
                                 "tensors [Batch, Heads, SeqLen, Dim]");
@@ -356,7 +414,6 @@ int nne_flash_attention_forward(const float* q, const int64_t q_shape[4], const 
         return fail(NNE_EINVAL, "Invalid configuration or argument: FlashAttention dims out of "
                                 "range, got Q:%s, K:%s, V:%s", shape_str(q_shape).c_str(),
                     shape_str(k_shape).c_str(), shape_str(v_shape).c_str());
-    // flash_attention.rs:39-48
     const int64_t b = q_shape[0], h = q_shape[1], d = q_shape[3];
     const int64_t kb = k_shape[0], kh = k_shape[1], tk = k_shape[2], kd = k_shape[3];
     const int64_t vb = v_shape[0], vh = v_shape[1], vt = v_shape[2], vd = v_shape[3];
@@ -366,21 +423,12 @@ int nne_flash_attention_forward(const float* q, const int64_t q_shape[4], const 
         return fail(NNE_ESHAPE, "Shape mismatch error: expected shape %s, got %s",
                     shape_str(expected).c_str(), shape_str(actual).c_str());
     }
-    (void)block_size_r;   // br, bc = max(arg, 16) (:51-52) only order the reference's loops
-    (void)block_size_c;
-    if (b * h * q_shape[2] > 0 && (!q || !k || !v || !o) && tk > 0)
-        return fail(NNE_EINVAL, "Invalid configuration or argument: null tensor pointer");
-    Resolved r;
-    resolve_strides(r, q_shape, q_strides, k_shape, k_strides, v_shape, v_strides, o_strides);
-    return run_attention(q, q_shape, r.q, k, k_shape, r.k, v, r.v, o, r.o, is_causal != 0, 0,
-                         softmax_scale(has_scale, scale, d), as_stream(stream));
+    return NNE_OK;
 }
 
-int nne_attention_forward(const float* q, const int64_t q_shape[4], const int64_t q_strides[4],
-                          const float* k, const int64_t k_shape[4], const int64_t k_strides[4],
-                          const float* v, const int64_t v_shape[4], const int64_t v_strides[4],
-                          float* o, const int64_t o_strides[4], int is_causal, int64_t q_offset,
-                          int has_scale, float scale, void* stream) {
+// The grouped-query entry's checks: K/V agree with each other and with Q in
+// batch and head dim, and Hkv divides Hq.
+int check_attention_shapes(const int64_t* q_shape, const int64_t* k_shape, const int64_t* v_shape) {
     if (!q_shape || !k_shape || !v_shape)
         return fail(NNE_EINVAL, "Invalid configuration or argument: attention expects 4D "
                                 "tensors [Batch, Heads, SeqLen, Dim]");
@@ -397,12 +445,100 @@ int nne_attention_forward(const float* q, const int64_t q_shape[4], const int64_
         return fail(NNE_ESHAPE, "Shape mismatch error: expected shape %s, got %s",
                     shape_str(expected).c_str(), shape_str(actual).c_str());
     }
-    if (b * hq * q_shape[2] > 0 && (!q || !k || !v || !o) && tk > 0)
+    return NNE_OK;
+}
+
+int attention_entry(const float* q, const int64_t* q_shape, const int64_t* q_strides, const float* k,
+                    const int64_t* k_shape, const int64_t* k_strides, const float* v,
+                    const int64_t* v_shape, const int64_t* v_strides, float* o,
+                    const int64_t* o_strides, bool causal, int64_t q_offset, int has_scale,
+                    float scale, const nne_workspace_t* ws, hipStream_t stream) {
+    if (q_shape[0] * q_shape[1] * q_shape[2] > 0 && k_shape[2] > 0 && (!q || !k || !v || !o))
         return fail(NNE_EINVAL, "Invalid configuration or argument: null tensor pointer");
     Resolved r;
     resolve_strides(r, q_shape, q_strides, k_shape, k_strides, v_shape, v_strides, o_strides);
-    return run_attention(q, q_shape, r.q, k, k_shape, r.k, v, r.v, o, r.o, is_causal != 0,
-                         q_offset, softmax_scale(has_scale, scale, d), as_stream(stream));
+    return run_attention(q, q_shape, r.q, k, k_shape, r.k, v, r.v, o, r.o, causal, q_offset,
+                         softmax_scale(has_scale, scale, q_shape[3]), ws, stream);
+}
+
+}  // namespace
+
+int nne_flash_attention_forward_ws(const float* q, const int64_t q_shape[4], const int64_t q_strides[4],
+                                   const float* k, const int64_t k_shape[4], const int64_t k_strides[4],
+                                   const float* v, const int64_t v_shape[4], const int64_t v_strides[4],
+                                   float* o, const int64_t o_strides[4], int is_causal, int has_scale,
+                                   float scale, int64_t block_size_r, int64_t block_size_c,
+                                   const nne_workspace_t* ws, void* stream) {
+    const int rc = check_flash_shapes(q_shape, k_shape, v_shape);
+    if (rc != NNE_OK) return rc;
+    (void)block_size_r;   // br, bc = max(arg, 16) (:51-52) only order the reference's loops
+    (void)block_size_c;
+    return attention_entry(q, q_shape, q_strides, k, k_shape, k_strides, v, v_shape, v_strides, o,
+                           o_strides, is_causal != 0, 0, has_scale, scale, ws, as_stream(stream));
+}
+
+int nne_flash_attention_forward(const float* q, const int64_t q_shape[4], const int64_t q_strides[4],
+                                const float* k, const int64_t k_shape[4], const int64_t k_strides[4],
+                                const float* v, const int64_t v_shape[4], const int64_t v_strides[4],
+                                float* o, const int64_t o_strides[4], int is_causal, int has_scale,
+                                float scale, int64_t block_size_r, int64_t block_size_c,
+                                void* stream) {
+    return nne_flash_attention_forward_ws(q, q_shape, q_strides, k, k_shape, k_strides, v, v_shape,
+                                          v_strides, o, o_strides, is_causal, has_scale, scale,
+                                          block_size_r, block_size_c, nullptr, stream);
+}
+
+int nne_attention_forward_ws(const float* q, const int64_t q_shape[4], const int64_t q_strides[4],
+                             const float* k, const int64_t k_shape[4], const int64_t k_strides[4],
+                             const float* v, const int64_t v_shape[4], const int64_t v_strides[4],
+                             float* o, const int64_t o_strides[4], int is_causal, int64_t q_offset,
+                             int has_scale, float scale, const nne_workspace_t* ws, void* stream) {
+    const int rc = check_attention_shapes(q_shape, k_shape, v_shape);
+    if (rc != NNE_OK) return rc;
+    return attention_entry(q, q_shape, q_strides, k, k_shape, k_strides, v, v_shape, v_strides, o,
+                           o_strides, is_causal != 0, q_offset, has_scale, scale, ws,
+                           as_stream(stream));
+}
+
+int nne_attention_forward(const float* q, const int64_t q_shape[4], const int64_t q_strides[4],
+                          const float* k, const int64_t k_shape[4], const int64_t k_strides[4],
+                          const float* v, const int64_t v_shape[4], const int64_t v_strides[4],
+                          float* o, const int64_t o_strides[4], int is_causal, int64_t q_offset,
+                          int has_scale, float scale, void* stream) {
+    return nne_attention_forward_ws(q, q_shape, q_strides, k, k_shape, k_strides, v, v_shape,
+                                    v_strides, o, o_strides, is_causal, q_offset, has_scale, scale,
+                                    nullptr, stream);
+}
+
+int nne_attention_workspace_size(const int64_t q_shape[4], const int64_t k_shape[4], int is_causal,
+                                 int64_t q_offset, nne_workspace_size_t* out) {
+    if (!out) return fail(NNE_EINVAL, "Invalid configuration or argument: null output pointer");
+    *out = nne_workspace_size_t{0, 0};
+    const int rc = check_attention_shapes(q_shape, k_shape, k_shape);
+    if (rc != NNE_OK) return rc;
+    *out = attention_workspace(q_shape, k_shape, is_causal != 0, q_offset);
+    return NNE_OK;
+}
+
+int nne_counters_init(uint32_t* counters, uint64_t n, void* stream) {
+    if (n == 0) return NNE_OK;
+    if (!counters) return fail(NNE_EINVAL, "Invalid configuration or argument: null counters");
+    const hipError_t e = nne::zero_counters(counters, (int64_t)n, as_stream(stream));
+    return e == hipSuccess ? NNE_OK : hip_fail(e, "counter fill");
+}
+
+uint64_t nne_stream_resource_bytes(void* stream) {
+    const hipStream_t s = as_stream(stream);
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return 0;
+    const std::thread::id th =
+        s == hipStreamPerThread ? std::this_thread::get_id() : std::thread::id();
+    std::lock_guard<std::mutex> lock(g_res_mu);
+    uint64_t total = 0;
+    for (const auto& r : g_res)
+        if (r.dev == dev && r.stream == s && r.thread == th)
+            total += (uint64_t)r.n_counters * 4 + r.ws_bytes + r.retired_bytes;
+    return total;
 }
 
 int nne_kv_append(float* k_cache, float* v_cache, int32_t* lens_dev, int32_t* lens_host,
@@ -454,8 +590,7 @@ int run_decode(const float* q, const int64_t* q_strides, const float* k_cache, c
                const int32_t* lens_dev, int32_t* lens_dev_w, int32_t* lens_host, const float* k_new,
                const int64_t* kn_strides, const float* v_new, const int64_t* vn_strides, float* o,
                const int64_t* o_strides, int64_t B, int64_t Hq, int64_t Hkv, int64_t capacity,
-               int64_t d, int has_scale, float scale, void* workspace, uint64_t workspace_bytes,
-               uint32_t* caller_counters, hipStream_t s) {
+               int64_t d, int has_scale, float scale, const nne_workspace_t* wsp, hipStream_t s) {
     int rc = check_kv_cache_args(B, Hq, Hkv, capacity, d, true);
     if (rc) return rc;
     if (Hq / Hkv > nne::splitk_max_rows())
@@ -537,20 +672,11 @@ int run_decode(const float* q, const int64_t* q_strides, const float* k_cache, c
     }
     const nne::SplitKWorkspace w =
         nne::splitk_workspace_layout((int)B, (int)Hkv, (int)(Hq / Hkv), (int)d);
-    void* ws = workspace;
-    if (ws && w.total_bytes > workspace_bytes)
-        return fail(NNE_EINVAL, "Invalid configuration or argument: decode workspace of %llu bytes "
-                                "is smaller than the %llu required",
-                    (unsigned long long)workspace_bytes, (unsigned long long)w.total_bytes);
-    uint32_t* counters = caller_counters;
-    hipError_t e = hipSuccess;
-    if (!counters || !ws) {
-        uint32_t* lib_counters = nullptr;
-        e = stream_resources(counters ? 0 : B * Hkv, ws ? 0 : w.total_bytes, s, &lib_counters, &ws);
-        if (e != hipSuccess) return hip_fail(e, "decode workspace");
-        if (!counters) counters = lib_counters;
-    }
-    e = nne::launch_splitk(p, total_keys, max_len, ws, s, seq_lens.data(), counters);
+    void* ws = nullptr;
+    uint32_t* counters = nullptr;
+    rc = call_workspace(wsp, w.total_bytes, B * Hkv, s, &ws, &counters, "decode");
+    if (rc != NNE_OK) return rc;
+    hipError_t e = nne::launch_splitk(p, total_keys, max_len, ws, s, seq_lens.data(), counters);
     if (e != hipSuccess) return hip_fail(e, "decode attention launch");
     if (append)
         for (int64_t b = 0; b < B; ++b) lens_host[b] += 1;
@@ -562,15 +688,29 @@ int run_decode(const float* q, const int64_t* q_strides, const float* k_cache, c
 extern "C" {
 
 
+int nne_decode_workspace_size(int64_t B, int64_t Hq, int64_t Hkv, int64_t d,
+                              nne_workspace_size_t* out) {
+    if (!out) return fail(NNE_EINVAL, "Invalid configuration or argument: null output pointer");
+    *out = nne_workspace_size_t{0, 0};
+    const uint64_t bytes = nne_decode_workspace_bytes(B, Hq, Hkv, d, 0);
+    if (bytes == 0)
+        return fail(NNE_EINVAL, "Invalid configuration or argument: no decode kernel for B=%lld "
+                                "Hq=%lld Hkv=%lld d=%lld", (long long)B, (long long)Hq,
+                    (long long)Hkv, (long long)d);
+    out->records_bytes = bytes;
+    out->n_counters = (uint64_t)B * (uint64_t)Hkv;
+    return NNE_OK;
+}
+
 int nne_decode_attention(const float* q, const int64_t q_strides[4], const float* k_cache,
                          const float* v_cache, const int32_t* lens_dev, const int32_t* lens_host,
                          float* o, const int64_t o_strides[4], int64_t B, int64_t Hq, int64_t Hkv,
-                         int64_t capacity, int64_t d, int has_scale, float scale, void* workspace,
-                         uint64_t workspace_bytes, void* stream) {
+                         int64_t capacity, int64_t d, int has_scale, float scale,
+                         const nne_workspace_t* ws, void* stream) {
     return nne::run_decode(q, q_strides, k_cache, v_cache, lens_dev, nullptr,
-                      const_cast<int32_t*>(lens_host), nullptr, nullptr, nullptr, nullptr, o,
-                      o_strides, B, Hq, Hkv, capacity, d, has_scale, scale, workspace,
-                      workspace_bytes, nullptr, as_stream(stream));
+                           const_cast<int32_t*>(lens_host), nullptr, nullptr, nullptr, nullptr, o,
+                           o_strides, B, Hq, Hkv, capacity, d, has_scale, scale, ws,
+                           as_stream(stream));
 }
 
 int nne_decode_step(const float* q, const int64_t q_strides[4], float* k_cache, float* v_cache,
@@ -578,13 +718,12 @@ int nne_decode_step(const float* q, const int64_t q_strides[4], float* k_cache, 
                     const int64_t k_new_strides[4], const float* v_new,
                     const int64_t v_new_strides[4], float* o, const int64_t o_strides[4],
                     int64_t B, int64_t Hq, int64_t Hkv, int64_t capacity, int64_t d,
-                    int has_scale, float scale, void* workspace, uint64_t workspace_bytes,
-                    void* stream) {
+                    int has_scale, float scale, const nne_workspace_t* ws, void* stream) {
     if (!k_new || !v_new)
         return fail(NNE_EINVAL, "Invalid configuration or argument: decode step needs k_new and v_new");
     return nne::run_decode(q, q_strides, k_cache, v_cache, lens_dev, lens_dev, lens_host, k_new,
-                      k_new_strides, v_new, v_new_strides, o, o_strides, B, Hq, Hkv, capacity, d,
-                      has_scale, scale, workspace, workspace_bytes, nullptr, as_stream(stream));
+                           k_new_strides, v_new, v_new_strides, o, o_strides, B, Hq, Hkv, capacity,
+                           d, has_scale, scale, ws, as_stream(stream));
 }
 
 // ---- decode prologue: projections and rotary position embedding ----------
@@ -705,11 +844,33 @@ int nne_qkv_pack(const float* wq, const float* wk, const float* wv, float* packe
     return e == hipSuccess ? NNE_OK : hip_fail(e, "weight packing launch");
 }
 
+int nne_qkv_workspace_size(int64_t C, int64_t Hq, int64_t Hkv, int64_t d, nne_workspace_size_t* out) {
+    if (!out) return fail(NNE_EINVAL, "Invalid configuration or argument: null output pointer");
+    *out = nne_workspace_size_t{0, 0};
+    const int rc = check_qkv_geometry(C, Hq, Hkv, d);
+    if (rc) return rc;
+    const nne::QkvWorkspace w = nne::qkv_workspace((int)C, (int)Hq, (int)Hkv, (int)d, device_cus());
+    out->records_bytes = w.floats * 4;
+    out->n_counters = (uint64_t)w.n_tiles;
+    return NNE_OK;
+}
+
 int nne_qkv_rope(const float* x, int64_t x_row_stride, const float* w_packed, const float* bq,
                  const float* bk, const float* bv, const float* cos_table, const float* sin_table,
                  int64_t max_seq_len, int64_t table_head_dim, const int32_t* pos_dev,
                  const int32_t* pos_host, float* q_out, float* k_out, float* v_out, int64_t B,
                  int64_t C, int64_t Hq, int64_t Hkv, int64_t d, void* stream) {
+    return nne_qkv_rope_ws(x, x_row_stride, w_packed, bq, bk, bv, cos_table, sin_table, max_seq_len,
+                           table_head_dim, pos_dev, pos_host, q_out, k_out, v_out, B, C, Hq, Hkv, d,
+                           nullptr, stream);
+}
+
+int nne_qkv_rope_ws(const float* x, int64_t x_row_stride, const float* w_packed, const float* bq,
+                    const float* bk, const float* bv, const float* cos_table, const float* sin_table,
+                    int64_t max_seq_len, int64_t table_head_dim, const int32_t* pos_dev,
+                    const int32_t* pos_host, float* q_out, float* k_out, float* v_out, int64_t B,
+                    int64_t C, int64_t Hq, int64_t Hkv, int64_t d, const nne_workspace_t* wsp,
+                    void* stream) {
     if (B < 0 || B > INT32_MAX)
         return fail(NNE_EINVAL, "Invalid configuration or argument: batch %lld", (long long)B);
     const bool rope = cos_table || sin_table;
@@ -732,8 +893,9 @@ int nne_qkv_rope(const float* x, int64_t x_row_stride, const float* w_packed, co
     const nne::QkvWorkspace w = nne::qkv_workspace((int)C, (int)Hq, (int)Hkv, (int)d, device_cus());
     uint32_t* counters = nullptr;
     void* ws = nullptr;
-    hipError_t e = stream_resources(w.n_tiles, w.floats * 4, as_stream(stream), &counters, &ws);
-    if (e != hipSuccess) return hip_fail(e, "projection workspace");
+    rc = call_workspace(wsp, w.floats * 4, w.n_tiles, as_stream(stream), &ws, &counters,
+                        "projection");
+    if (rc != NNE_OK) return rc;
     nne::QkvParams p{};
     p.x = x;
     p.x_rs = x_row_stride;
@@ -750,7 +912,7 @@ int nne_qkv_rope(const float* x, int64_t x_row_stride, const float* w_packed, co
     p.n_tiles = w.n_tiles; p.S = w.S; p.kc_per_slice = w.kc_per_slice;
     p.ws = static_cast<float*>(ws);
     p.cnt = counters;
-    e = nne::launch_qkv_rope(p, as_stream(stream));
+    const hipError_t e = nne::launch_qkv_rope(p, as_stream(stream));
     return e == hipSuccess ? NNE_OK : hip_fail(e, "q/k/v projection launch");
 }
 

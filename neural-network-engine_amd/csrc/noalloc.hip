@@ -95,7 +95,9 @@ extern "C" int nne_decode_step_noalloc(const float* q, const int64_t q_strides[4
         const hipError_t e = nne::zero_counters(counters, B * Hkv, s);
         if (e != hipSuccess) return nne::fail_hip(e, "no-allocation counter clear");
     }
+    const nne_workspace_t scratch_ws{ws, kScratchBytes - cnt_bytes, counters,
+                                     (uint64_t)(cnt_bytes / 4)};
     return nne::run_decode(q, q_strides, k_cache, v_cache, lens_dev, lens_dev, lens_host, k_new,
                            k_new_strides, v_new, v_new_strides, o, o_strides, B, Hq, Hkv, capacity,
-                           d, has_scale, scale, ws, kScratchBytes - cnt_bytes, counters, s);
+                           d, has_scale, scale, &scratch_ws, s);
 }

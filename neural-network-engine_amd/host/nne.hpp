@@ -48,6 +48,8 @@
 #include <variant>
 #include <vector>
 
+#include "nne_attn.h"
+
 namespace nne {
 
 // src/error.rs:8-52: the variants this path produces, with the same messages.
@@ -208,7 +210,9 @@ class KVCache {
 
   private:
     Result<bool> check_layer(size_t layer_idx) const;
-    void* workspace(size_t num_heads);
+    // The cache's own decode workspace (records + zeroed counters), grown to
+    // what num_heads query heads need; the library allocates nothing.
+    const ::nne_workspace_t* workspace(size_t num_heads);
 
     struct Layer {
         std::shared_ptr<float> k, v;
@@ -217,7 +221,8 @@ class KVCache {
     };
     std::vector<Layer> layers_;
     std::shared_ptr<void> ws_;
-    uint64_t ws_bytes_ = 0;
+    std::shared_ptr<uint32_t> counters_;
+    std::shared_ptr<::nne_workspace_t> ws_desc_;
 };
 
 // src/models/llama.rs:64-158.  Tables are built on the host in f32 exactly as

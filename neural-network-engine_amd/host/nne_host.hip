@@ -512,15 +512,27 @@ Result<std::pair<RawTensor, RawTensor>> KVCache::update(size_t layer_idx, const 
     return std::make_pair(kv.value(), vv.value());
 }
 
-void* KVCache::workspace(size_t num_heads) {
-    const uint64_t need = nne_decode_workspace_bytes((int64_t)batch, (int64_t)num_heads, (int64_t)num_kv_heads,
-                                                     (int64_t)head_dim, (int64_t)capacity);
-    if (need > ws_bytes_) {
-        auto buf = device_alloc<char>(need);
+const nne_workspace_t* KVCache::workspace(size_t num_heads) {
+    nne_workspace_size_t need{0, 0};
+    if (nne_decode_workspace_size((int64_t)batch, (int64_t)num_heads, (int64_t)num_kv_heads, (int64_t)head_dim,
+                                  &need) != NNE_OK)
+        return nullptr;   // the call itself reports the geometry error
+    if (!ws_desc_) ws_desc_ = std::make_shared<nne_workspace_t>(nne_workspace_t{nullptr, 0, nullptr, 0});
+    nne_workspace_t& w = *ws_desc_;
+    if (need.records_bytes > w.records_bytes) {
+        auto buf = device_alloc<char>(need.records_bytes);
         ws_ = std::shared_ptr<void>(buf, buf.get());
-        ws_bytes_ = need;
+        w.records = ws_.get();
+        w.records_bytes = need.records_bytes;
     }
-    return ws_.get();
+    if (need.n_counters > w.n_counters) {
+        counters_ = device_alloc<uint32_t>(need.n_counters);
+        if (nne_counters_init(counters_.get(), need.n_counters, nullptr) != NNE_OK)
+            throw std::runtime_error(from_status(NNE_EHIP).to_string());
+        w.counters = counters_.get();
+        w.n_counters = need.n_counters;
+    }
+    return ws_desc_.get();
 }
 
 Result<RawTensor> KVCache::attend(size_t layer_idx, const RawTensor& q, std::optional<float> scale) {
@@ -531,12 +543,11 @@ Result<RawTensor> KVCache::attend(size_t layer_idx, const RawTensor& q, std::opt
     Layer& l = layers_[layer_idx];
     RawTensor out = RawTensor::zeros(q.shape());
     const auto qst = as_i64(q.strides()), ost = as_i64(out.strides());
-    void* ws = workspace(q.shape()[1]);
+    const nne_workspace_t* ws = workspace(q.shape()[1]);
     const int rc = nne_decode_attention(q.data(), qst.data(), l.k.get(), l.v.get(), l.lens_dev.get(),
                                         l.lens_host.data(), out.data(), ost.data(), (int64_t)batch,
                                         (int64_t)q.shape()[1], (int64_t)num_kv_heads, (int64_t)capacity,
-                                        (int64_t)head_dim, scale ? 1 : 0, scale.value_or(0.f), ws, ws_bytes_,
-                                        nullptr);
+                                        (int64_t)head_dim, scale ? 1 : 0, scale.value_or(0.f), ws, nullptr);
     if (rc != NNE_OK) return from_status(rc);
     return out;
 }
@@ -555,7 +566,7 @@ Result<RawTensor> KVCache::decode_step(size_t layer_idx, const RawTensor& q, con
     const auto qst = as_i64(q.strides()), ost = as_i64(out.strides());
     const int64_t hq = (int64_t)q.shape()[1];
     if (nne_decode_workspace_bytes(std::max<int64_t>((int64_t)batch, 1), hq, (int64_t)num_kv_heads,
-                                   (int64_t)head_dim, 1) == 0) {
+                                   (int64_t)head_dim, 0) == 0) {
         // Geometry the fused kernel does not take (head dim not a multiple of
         // 4): append, then attend every sequence to its own first lens[b]
         // rows, no mask (llama.rs:239-296 with t = 1), on the general kernel.
@@ -576,12 +587,12 @@ Result<RawTensor> KVCache::decode_step(size_t layer_idx, const RawTensor& q, con
         return out;
     }
     const auto kst = as_i64(k_new.strides()), vst = as_i64(v_new.strides());
-    void* ws = workspace(q.shape()[1]);
+    const nne_workspace_t* ws = workspace(q.shape()[1]);
     const int rc = nne_decode_step(q.data(), qst.data(), l.k.get(), l.v.get(), l.lens_dev.get(),
                                    l.lens_host.data(), k_new.data(), kst.data(), v_new.data(), vst.data(),
                                    out.data(), ost.data(), (int64_t)batch, (int64_t)q.shape()[1],
                                    (int64_t)num_kv_heads, (int64_t)capacity, (int64_t)head_dim, scale ? 1 : 0,
-                                   scale.value_or(0.f), ws, ws_bytes_, nullptr);
+                                   scale.value_or(0.f), ws, nullptr);
     if (rc != NNE_OK) return from_status(rc);
     return out;
 }

@@ -22,7 +22,7 @@ def test_library_exports_header_symbols(nne):
     for name in declared:
         assert hasattr(lib, name), name
         assert name in nne.SIGNATURES, name
-    assert lib.nne_abi_version() == 3
+    assert lib.nne_abi_version() == 4
 
 
 def test_flash_shape_mismatch_is_shape_error(nne):
@@ -75,20 +75,20 @@ def test_decode_rejects_bad_geometry(nne):
     lp = lens.ctypes.data_as(ctypes.POINTER(ctypes.c_int32))
     # Hq not divisible by Hkv
     rc = lib.nne_decode_attention(FAKE, None, FAKE, FAKE, FAKE, lp, FAKE, None, 1, 6, 4, 8, 16,
-                                  0, 0.0, None, 0, None)
+                                  0, 0.0, None, None)
     assert rc == nne.NNE_EINVAL
     # head dim not a multiple of 4
     rc = lib.nne_decode_attention(FAKE, None, FAKE, FAKE, FAKE, lp, FAKE, None, 1, 4, 4, 8, 18,
-                                  0, 0.0, None, 0, None)
+                                  0, 0.0, None, None)
     assert rc == nne.NNE_EINVAL
     # more than 16 query rows per KV head
     rc = lib.nne_decode_attention(FAKE, None, FAKE, FAKE, FAKE, lp, FAKE, None, 1, 32, 1, 8, 16,
-                                  0, 0.0, None, 0, None)
+                                  0, 0.0, None, None)
     assert rc == nne.NNE_EINVAL
     # length beyond capacity
     lens[0] = 9
     rc = lib.nne_decode_attention(FAKE, None, FAKE, FAKE, FAKE, lp, FAKE, None, 1, 4, 4, 8, 16,
-                                  0, 0.0, None, 0, None)
+                                  0, 0.0, None, None)
     assert rc == nne.NNE_EINVAL
 
 
@@ -112,7 +112,7 @@ def test_decode_step_capacity_error_leaves_lengths(nne):
     lens = np.array([3, 8], np.int32)
     lp = lens.ctypes.data_as(ctypes.POINTER(ctypes.c_int32))
     rc = lib.nne_decode_step(FAKE, None, FAKE, FAKE, FAKE, lp, FAKE, None, FAKE, None, FAKE, None,
-                             2, 4, 2, 8, 16, 0, 0.0, None, 0, None)
+                             2, 4, 2, 8, 16, 0, 0.0, None, None)
     assert rc == nne.NNE_ECAPACITY
     assert list(lens) == [3, 8]
 
@@ -211,7 +211,7 @@ def test_decode_and_append_reject_null_device_pointers(nne):
         ptrs[bad] = None
         q, kc, vc, ld, kn, vn, o = ptrs
         rc = lib.nne_decode_step(q, None, kc, vc, ld, lp, kn, None, vn, None, o, None, 2, 4, 2,
-                                 16, 16, 0, 0.0, None, 0, None)
+                                 16, 16, 0, 0.0, None, None)
         assert rc == nne.NNE_EINVAL, bad
     assert list(lens) == [3, 4]
     # attention only: q, caches, lengths and output
@@ -220,7 +220,7 @@ def test_decode_and_append_reject_null_device_pointers(nne):
         ptrs[bad] = None
         q, kc, vc, ld, o = ptrs
         rc = lib.nne_decode_attention(q, None, kc, vc, ld, lp, o, None, 2, 4, 2, 16, 16, 0, 0.0,
-                                      None, 0, None)
+                                      None, None)
         assert rc == nne.NNE_EINVAL, bad
 
 
@@ -232,10 +232,55 @@ def test_decode_16_row_tile_needs_vector_q(nne):
     lp = lens.ctypes.data_as(ctypes.POINTER(ctypes.c_int32))
     misaligned = ctypes.c_void_p(4096 + 4)
     rc = lib.nne_decode_attention(misaligned, None, FAKE, FAKE, FAKE, lp, FAKE, None, 1, 8, 1, 16,
-                                  16, 0, 0.0, None, 0, None)
+                                  16, 0, 0.0, None, None)
     assert rc == nne.NNE_EINVAL
     assert "16-byte alignment" in lib.nne_last_error().decode()
     odd = i64(8 * 16, 18, 16, 1)       # head stride 18 floats
     rc = lib.nne_decode_attention(FAKE, odd, FAKE, FAKE, FAKE, lp, FAKE, None, 1, 8, 1, 16, 16, 0,
-                                  0.0, None, 0, None)
+                                  0.0, None, None)
     assert rc == nne.NNE_EINVAL
+
+
+def test_workspace_size_queries(nne):
+    """What each split computation needs from a caller workspace."""
+    lib = nne.lib()
+    size = nne.NneWorkspaceSize()
+    # config 1 (4 work items on 256 CUs): key split, records and counters
+    assert lib.nne_attention_workspace_size(i64(1, 4, 256, 64), i64(1, 4, 256, 64), 1, 0,
+                                            ctypes.byref(size)) == nne.NNE_OK
+    assert size.records_bytes > 0 and size.n_counters > 0
+    # config 2 fills the device: no workspace
+    assert lib.nne_attention_workspace_size(i64(4, 32, 2048, 128), i64(4, 8, 2048, 128), 1, 0,
+                                            ctypes.byref(size)) == nne.NNE_OK
+    assert (size.records_bytes, size.n_counters) == (0, 0)
+    # few-query cross-attention: one counter per (sequence, KV head)
+    assert lib.nne_attention_workspace_size(i64(8, 20, 8, 64), i64(8, 20, 1500, 64), 0, 0,
+                                            ctypes.byref(size)) == nne.NNE_OK
+    assert size.records_bytes > 0 and size.n_counters >= 8 * 20
+    # shapes the call would refuse
+    assert lib.nne_attention_workspace_size(i64(1, 6, 8, 16), i64(1, 4, 8, 16), 1, 0,
+                                            ctypes.byref(size)) == nne.NNE_ESHAPE
+    assert lib.nne_decode_workspace_size(32, 32, 8, 128, ctypes.byref(size)) == nne.NNE_OK
+    assert size.n_counters == 32 * 8
+    assert size.records_bytes == lib.nne_decode_workspace_bytes(32, 32, 8, 128, 4160)
+    assert lib.nne_decode_workspace_size(1, 4, 4, 30, ctypes.byref(size)) == nne.NNE_EINVAL
+    assert lib.nne_qkv_workspace_size(4096, 32, 8, 128, ctypes.byref(size)) == nne.NNE_OK
+    assert size.records_bytes > 0 and size.n_counters == 48 * 128 // 64
+    assert lib.nne_qkv_workspace_size(100, 4, 2, 64, ctypes.byref(size)) == nne.NNE_EINVAL
+
+
+def test_undersized_caller_workspace_is_refused_before_launch(nne):
+    lib = nne.lib()
+    lens = np.array([3, 5], np.int32)
+    lp = lens.ctypes.data_as(ctypes.POINTER(ctypes.c_int32))
+    small = nne.NneWorkspace(records=4096, records_bytes=64, counters=4096, n_counters=16)
+    rc = lib.nne_decode_step(FAKE, None, FAKE, FAKE, FAKE, lp, FAKE, None, FAKE, None, FAKE, None,
+                             2, 4, 2, 16, 16, 0, 0.0, ctypes.byref(small), None)
+    assert rc == nne.NNE_EINVAL
+    assert "record bytes" in lib.nne_last_error().decode()
+    assert list(lens) == [3, 5]
+    few = nne.NneWorkspace(records=4096, records_bytes=1 << 30, counters=4096, n_counters=1)
+    rc = lib.nne_decode_attention(FAKE, None, FAKE, FAKE, FAKE, lp, FAKE, None, 2, 4, 2, 16, 16,
+                                  0, 0.0, ctypes.byref(few), None)
+    assert rc == nne.NNE_EINVAL
+    assert "counters" in lib.nne_last_error().decode()

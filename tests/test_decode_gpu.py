@@ -147,7 +147,8 @@ def test_decode_matches_last_row_of_gpu_prefill(nne, cuda):
 
 
 def test_workspace_argument_paths(nne, cuda):
-    """Caller workspace, library-allocated workspace, and a too-small one."""
+    """Library workspace (NULL), a caller workspace (records + zeroed
+    counters), and undersized caller workspaces, which are refused."""
     import ctypes
     import torch
     rng = np.random.default_rng(11)
@@ -158,23 +159,30 @@ def test_workspace_argument_paths(nne, cuda):
     ref = T.ref_decode_attend(host(q), kc, vc, lens)
     lib = nne.lib()
     i32p = ctypes.POINTER(ctypes.c_int32)
-    for ws in (None, "small"):
+    size = nne.NneWorkspaceSize()
+    assert lib.nne_decode_workspace_size(b, hq, hkv, d, ctypes.byref(size)) == nne.NNE_OK
+    caller = nne.Workspace(cuda).reserve(size)
+    buf = torch.zeros(16, dtype=torch.int32, device=cuda)
+    short_records = nne.NneWorkspace(buf.data_ptr(), 16, buf.data_ptr(), 16)
+    short_counters = nne.NneWorkspace(caller.records.data_ptr(), caller.records.numel(),
+                                      buf.data_ptr(), 1)
+    outs = {}
+    for name, ws in (("library", None), ("caller", caller.struct()[0]),
+                     ("short records", ctypes.byref(short_records)),
+                     ("short counters", ctypes.byref(short_counters))):
+        print("case workspace", name, flush=True)
         out = torch.empty_like(q)
-        if ws is None:
-            ptr, nbytes = None, 0
-        else:
-            buf = torch.empty(16, dtype=torch.uint8, device=cuda)
-            ptr, nbytes = buf.data_ptr(), 16
         rc = lib.nne_decode_attention(q.data_ptr(), None, cache.k[0].data_ptr(),
                                       cache.v[0].data_ptr(), cache.lens_dev[0].data_ptr(),
                                       cache.lens_host[0].ctypes.data_as(i32p), out.data_ptr(),
-                                      None, b, hq, hkv, cap, d, 0, 0.0, ptr, nbytes,
-                                      nne._stream())
-        if ws is None:
-            assert rc == 0
-            T.assert_close(host(out), ref, what="library workspace")
-        else:
+                                      None, b, hq, hkv, cap, d, 0, 0.0, ws, nne._stream())
+        if name.startswith("short"):
             assert rc == nne.NNE_EINVAL
+        else:
+            assert rc == 0
+            outs[name] = host(out)
+            T.assert_close(outs[name], ref, what=name + " workspace")
+    assert np.array_equal(outs["library"], outs["caller"])
 
 
 def test_split_head_handoff_alternating_inputs(nne, cuda):

@@ -1,5 +1,6 @@
 """nne_decode_step_noalloc (the decode step on the library's static device
-scratch) against nne_decode_step (caller workspace), both through the C ABI.
+scratch) against nne_decode_step (caller workspace: records and counters),
+both through the C ABI.
 
 Two calls in a row on the same scratch, the second with a smaller input
 (fewer sequences, fewer heads, a smaller head dim), so a call that read the
@@ -42,8 +43,10 @@ def _step(nne, fn, lens, kc, vc, q, kn, vn, cuda, workspace=None):
     args = [q.data_ptr(), None, kc.data_ptr(), vc.data_ptr(), lens_dev.data_ptr(),
             lens_host.ctypes.data_as(_i32p), kn.data_ptr(), None, vn.data_ptr(), None,
             o.data_ptr(), None, b, hq, hkv, cap, d, 0, 0.0]
+    keep = None
     if workspace is not None:
-        args += [workspace.data_ptr(), workspace.numel()]
+        wsp, keep = workspace.struct()
+        args += [wsp]
     rc = fn(*args, s)
     assert rc == nne.NNE_OK, nne.lib().nne_last_error()
     torch.cuda.synchronize()
@@ -65,9 +68,10 @@ def test_noalloc_decode_step_matches_decode_step(nne, cuda, order):
         base = _case(nne, cuda, c["seed"], c["b"], c["hq"], c["hkv"], c["d"], c["cap"], c["lo"],
                      c["hi"])
         lens, kc, vc, q, kn, vn = base
-        ws_bytes = lib.nne_decode_workspace_bytes(c["b"], c["hq"], c["hkv"], c["d"], c["cap"])
-        assert ws_bytes > 0
-        ws = torch.empty(int(ws_bytes), dtype=torch.uint8, device=cuda)
+        size = nne.NneWorkspaceSize()
+        assert lib.nne_decode_workspace_size(c["b"], c["hq"], c["hkv"], c["d"],
+                                             ctypes.byref(size)) == nne.NNE_OK
+        ws = nne.Workspace(cuda).reserve(size)
         runs = {}
         names = ["noalloc", "reference"] if order == "noalloc_first" else ["reference", "noalloc"]
         for name in names:
