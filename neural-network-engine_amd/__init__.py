@@ -311,12 +311,68 @@ def attention_forward(q, k, v, is_causal, q_offset=0, scale=None, out=None, stre
     return out
 
 
+class _LayerSlots:
+    """``KVCache.layers`` -- the reference's ``pub layers:
+    Vec<Option<(Tensor, Tensor)>>`` (kv_cache.rs:13) over the device cache.
+    Item i is None or (K, V) views [B, Hkv, L, d] of the filled rows
+    (L = the longest sequence), materialised when read, with no copy.
+    Assigning None empties the layer; assigning (k, v) [B, Hkv, L, d] makes
+    them its rows 0..L (zero-element k, v give an engaged, empty slot, as
+    llama.rs:501-503 sets up before the prompt)."""
+
+    def __init__(self, cache):
+        self._c = cache
+
+    def __len__(self):
+        return self._c.num_layers()
+
+    def _index(self, i):
+        n = len(self)
+        i = i + n if i < 0 else i
+        if not 0 <= i < n:
+            raise IndexError("KVCache layer index %d out of range (total layers: %d)" % (i, n))
+        return i
+
+    def __getitem__(self, i):
+        c = self._c
+        i = self._index(i)
+        if not c._engaged[i]:
+            return None
+        L = c.current_seq_len(i)
+        return c.k[i][:, :, :L], c.v[i][:, :, :L]
+
+    def __setitem__(self, i, kv):
+        c = self._c
+        i = self._index(i)
+        if kv is not None:
+            k, v = kv
+            if k.numel() or v.numel():
+                want = [c.batch, c.num_kv_heads, k.shape[2] if k.dim() == 4 else 0, c.head_dim]
+                if list(k.shape) != want or list(v.shape) != want:
+                    raise ShapeMismatch("Shape mismatch error: expected shape %s, got %s"
+                                        % (want, list(k.shape)))
+                if want[2] > c.capacity:
+                    raise CapacityError("GPU compute error: KV cache slot of %d rows exceeds "
+                                        "capacity %d" % (want[2], c.capacity))
+        c.lens_dev[i].zero_()
+        c.lens_host[i][:] = 0
+        c._engaged[i] = False
+        if kv is not None:
+            if kv[0].numel():
+                c.update(i, kv[0], kv[1])
+            c._engaged[i] = True
+
+    def __iter__(self):
+        return (self[i] for i in range(len(self)))
+
+
 class KVCache:
     """Device-resident KV cache (src/nn/kv_cache.rs:11-74).
 
     Per layer: K and V buffers [B, Hkv, capacity, d] (head-major, rows appended
     in place) and per-sequence lengths kept on the device (read by kernels) and
-    on the host (validation, launch sizing).  Sequences may be ragged."""
+    on the host (validation, launch sizing).  Sequences may be ragged.
+    ``layers`` is the reference's per-layer slot vector over these buffers."""
 
     def __init__(self, num_layers, batch, num_kv_heads, capacity, head_dim, device="cuda"):
         import torch
@@ -329,12 +385,18 @@ class KVCache:
                          for _ in range(num_layers)]
         self.lens_host = [np.zeros(self.batch, dtype=np.int32) for _ in range(num_layers)]
         self._ws = Workspace(device)
+        self._engaged = [False] * num_layers    # Some(..) in the reference's slot vector
+
+    @property
+    def layers(self):
+        return _LayerSlots(self)
 
     # kv_cache.rs:25-29
     def reset(self):
         for i in range(self.num_layers()):
             self.lens_dev[i].zero_()
             self.lens_host[i][:] = 0
+            self._engaged[i] = False
 
     # kv_cache.rs:32-34
     def num_layers(self):
@@ -355,6 +417,7 @@ class KVCache:
             raise InvalidArgument("Invalid configuration or argument: bad lengths")
         self.lens_host[layer_idx][:] = lens
         self.lens_dev[layer_idx].copy_(torch.from_numpy(lens))
+        self._engaged[layer_idx] = True
 
     def _check_layer(self, layer_idx):
         if layer_idx >= self.num_layers():
@@ -376,6 +439,7 @@ class KVCache:
             self.lens_dev[layer_idx].data_ptr(), lh.ctypes.data_as(_i32p),
             k_new.data_ptr(), _i64(k_new.stride()), v_new.data_ptr(), _i64(v_new.stride()),
             self.batch, self.num_kv_heads, self.capacity, self.head_dim, t, _stream(stream)))
+        self._engaged[layer_idx] = True
         L = int(lh.max()) if self.batch else 0
         return self.k[layer_idx][:, :, :L], self.v[layer_idx][:, :, :L]
 
@@ -431,6 +495,7 @@ class KVCache:
             _i64(k_new.stride()), v_new.data_ptr(), _i64(v_new.stride()), out.data_ptr(),
             _i64(out.stride()), self.batch, hq, self.num_kv_heads, self.capacity, self.head_dim,
             int(scale is not None), float(scale or 0.0), wsp, _stream(stream)))
+        self._engaged[layer_idx] = True
         return out
 
     def _append_then_attend(self, layer_idx, q, k_new, v_new, out, scale, stream):

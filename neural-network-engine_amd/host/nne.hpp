@@ -184,6 +184,68 @@ class KVCache {
   public:
     KVCache(size_t num_layers, size_t batch, size_t num_kv_heads, size_t capacity, size_t head_dim);
 
+    // One entry of the reference's `pub layers: Vec<Option<(Tensor, Tensor)>>`
+    // (kv_cache.rs:13), as a handle on layer i of the device cache.  Reading
+    // it materialises (K, V) views [B, Hkv, L, d] of the filled rows (L = the
+    // longest sequence) -- no copy; assigning to it writes the device cache,
+    // so the models' slot idioms keep their meaning:
+    //   for (auto slot : cache.layers()) slot = {RawTensor::zeros({0}), RawTensor::zeros({0})};
+    //                                  // llama.rs:501-503: an engaged, empty slot
+    //   auto s = cache.layers().get_mut(i);   // llama.rs:464-468 (Option<&mut (K, V)>)
+    //   slot = std::nullopt;                   // kv_cache.rs:25-29 (None)
+    class Slot {
+      public:
+        bool has_value() const;                          // Some(..)
+        explicit operator bool() const { return has_value(); }
+        // The (K, V) views; throws std::bad_optional_access for None.
+        std::pair<RawTensor, RawTensor> value() const;
+        // *slot = None: the layer holds nothing (lengths 0).
+        Slot& operator=(std::nullopt_t);
+        // *slot = Some((k, v)): k, v [B, Hkv, L, d] (any strides, L <= capacity)
+        // become the layer's rows 0..L; k of zero elements makes an empty,
+        // engaged slot.  set() reports shape / capacity errors; operator=
+        // throws them.
+        Result<bool> set(const RawTensor& k, const RawTensor& v);
+        Slot& operator=(const std::pair<RawTensor, RawTensor>& kv);
+        // Option::take: contiguous copies of the rows, and the slot becomes None.
+        std::optional<std::pair<RawTensor, RawTensor>> take();
+        KVCache& cache() const { return *cache_; }
+        size_t layer_idx() const { return layer_; }
+
+      private:
+        friend class KVCache;
+        Slot(KVCache* c, size_t i) : cache_(c), layer_(i) {}
+        KVCache* cache_;
+        size_t layer_;
+    };
+    // The slots as a Vec-like range (size, operator[], get_mut, iteration).
+    class Layers {
+      public:
+        class iterator {
+          public:
+            Slot operator*() const { return Slot(c_, i_); }
+            iterator& operator++() { ++i_; return *this; }
+            bool operator!=(const iterator& o) const { return i_ != o.i_; }
+
+          private:
+            friend class Layers;
+            iterator(KVCache* c, size_t i) : c_(c), i_(i) {}
+            KVCache* c_;
+            size_t i_;
+        };
+        size_t size() const { return c_->num_layers(); }
+        Slot operator[](size_t i) const;                 // throws std::out_of_range past the end
+        std::optional<Slot> get_mut(size_t i) const;     // None past the end
+        iterator begin() const { return iterator(c_, 0); }
+        iterator end() const { return iterator(c_, size()); }
+
+      private:
+        friend class KVCache;
+        explicit Layers(KVCache* c) : c_(c) {}
+        KVCache* c_;
+    };
+    Layers layers() { return Layers(this); }
+
     void reset();                                        // kv_cache.rs:25-29
     size_t num_layers() const;                           // kv_cache.rs:32-34
     size_t current_seq_len(size_t layer_idx) const;      // kv_cache.rs:37-44 (longest sequence)
@@ -218,6 +280,7 @@ class KVCache {
         std::shared_ptr<float> k, v;
         std::shared_ptr<int32_t> lens_dev;
         std::vector<int32_t> lens_host;
+        bool engaged = false;    // Some(..) in the reference's slot vector
     };
     std::vector<Layer> layers_;
     std::shared_ptr<void> ws_;
@@ -256,6 +319,10 @@ class GroupedQueryAttention {
     // cache length, :525).
     Result<RawTensor> forward_gqa_cached(const RawTensor& x, size_t start_pos, KVCache* cache = nullptr,
                                          size_t layer_idx = 0);
+    // The reference's call shape, forward_gqa_cached(x, start_pos, layer_slot)
+    // (llama.rs:463-471): an empty optional or a None slot runs uncached.
+    Result<RawTensor> forward_gqa_cached(const RawTensor& x, size_t start_pos,
+                                         std::optional<KVCache::Slot> layer_cache);
     Result<RawTensor> forward_gqa(const RawTensor& x, size_t start_pos) {   // :298-301
         return forward_gqa_cached(x, start_pos, nullptr);
     }
@@ -282,6 +349,8 @@ class MultiHeadAttention {
     Result<RawTensor> forward_attention(const RawTensor& x) { return forward_attention_cached(x, nullptr); }
     // :51-129.  x [B, T, C]; cache layer layer_idx holds this layer's rows.
     Result<RawTensor> forward_attention_cached(const RawTensor& x, KVCache* cache, size_t layer_idx = 0);
+    // forward_attention_cached(x, layer_slot) as GPT-2 calls it (gpt2.rs:141).
+    Result<RawTensor> forward_attention_cached(const RawTensor& x, std::optional<KVCache::Slot> layer_cache);
     // :132-210.  x [B, T_q, C], memory [B, T_kv, C]; slot (if given) caches the
     // projected memory K/V [B, H, T_kv, d] on its first use.
     Result<RawTensor> forward_cross_attention(const RawTensor& x, const RawTensor& memory) {

@@ -457,11 +457,84 @@ KVCache::KVCache(size_t num_layers, size_t batch_, size_t num_kv_heads_, size_t 
     }
 }
 
-void KVCache::reset() {
+void KVCache::reset() {                                             // kv_cache.rs:25-29
     for (auto& l : layers_) {
         std::fill(l.lens_host.begin(), l.lens_host.end(), 0);
         if (batch) hip_check(hipMemset(l.lens_dev.get(), 0, batch * 4), "hipMemset");
+        l.engaged = false;
     }
+}
+
+// ---- KVCache slots (kv_cache.rs:13) --------------------------------------------
+
+bool KVCache::Slot::has_value() const { return cache_->layers_.at(layer_).engaged; }
+
+std::pair<RawTensor, RawTensor> KVCache::Slot::value() const {
+    if (!has_value()) throw std::bad_optional_access();
+    const size_t L = cache_->current_seq_len(layer_);
+    return {cache_->k(layer_).slice(2, 0, L).value(), cache_->v(layer_).slice(2, 0, L).value()};
+}
+
+KVCache::Slot& KVCache::Slot::operator=(std::nullopt_t) {
+    KVCache& c = *cache_;
+    Layer& l = c.layers_.at(layer_);
+    std::fill(l.lens_host.begin(), l.lens_host.end(), 0);
+    if (c.batch) hip_check(hipMemset(l.lens_dev.get(), 0, c.batch * 4), "hipMemset");
+    l.engaged = false;
+    return *this;
+}
+
+Result<bool> KVCache::Slot::set(const RawTensor& k, const RawTensor& v) {
+    KVCache& c = *cache_;
+    if (k.numel() == 0 && v.numel() == 0) {          // Some((zeros[0], zeros[0])): engaged, empty
+        *this = std::nullopt;
+        c.layers_.at(layer_).engaged = true;
+        return true;
+    }
+    const std::vector<size_t> want{c.batch, c.num_kv_heads, k.ndim() == 4 ? k.shape()[2] : 0, c.head_dim};
+    if (k.shape() != want) return EngineError::shape_mismatch(want, k.shape());
+    if (v.shape() != want) return EngineError::shape_mismatch(want, v.shape());
+    if (want[2] > c.capacity)
+        return EngineError::gpu_error("KV cache slot of " + std::to_string(want[2]) + " rows exceeds capacity " +
+                                      std::to_string(c.capacity));
+    // Rows 0..L of every sequence: lengths to zero, then the append kernel.
+    *this = std::nullopt;
+    auto r = c.update(layer_, k, v);
+    if (r.is_err()) return r.error();
+    return true;
+}
+
+KVCache::Slot& KVCache::Slot::operator=(const std::pair<RawTensor, RawTensor>& kv) {
+    set(kv.first, kv.second).unwrap();
+    return *this;
+}
+
+std::optional<std::pair<RawTensor, RawTensor>> KVCache::Slot::take() {
+    if (!has_value()) return std::nullopt;
+    auto kv = value();
+    auto copy = [](const RawTensor& t) {
+        if (!t.is_contiguous()) return t.to_contiguous();
+        RawTensor out = RawTensor::zeros(t.shape());
+        if (t.numel() && nne_memcpy_d2d(out.data(), t.data(), t.numel() * 4, nullptr) != NNE_OK)
+            throw std::runtime_error(from_status(NNE_EHIP).to_string());
+        return out;
+    };
+    std::pair<RawTensor, RawTensor> out{copy(kv.first), copy(kv.second)};
+    if (nne_stream_sync(nullptr) != NNE_OK) throw std::runtime_error(from_status(NNE_EHIP).to_string());
+    *this = std::nullopt;
+    return out;
+}
+
+KVCache::Slot KVCache::Layers::operator[](size_t i) const {
+    if (i >= size())
+        throw std::out_of_range("KVCache layer index " + std::to_string(i) + " out of range (total layers: " +
+                                std::to_string(size()) + ")");
+    return Slot(c_, i);
+}
+
+std::optional<KVCache::Slot> KVCache::Layers::get_mut(size_t i) const {
+    if (i >= size()) return std::nullopt;
+    return Slot(c_, i);
 }
 
 size_t KVCache::num_layers() const { return layers_.size(); }
@@ -507,6 +580,7 @@ Result<std::pair<RawTensor, RawTensor>> KVCache::update(size_t layer_idx, const 
                                  v_new.data(), vst.data(), (int64_t)batch, (int64_t)num_kv_heads,
                                  (int64_t)capacity, (int64_t)head_dim, (int64_t)want[2], nullptr);
     if (rc != NNE_OK) return from_status(rc);
+    l.engaged = true;
     const size_t L = current_seq_len(layer_idx);
     auto kv = k(layer_idx).slice(2, 0, L), vv = v(layer_idx).slice(2, 0, L);
     return std::make_pair(kv.value(), vv.value());
@@ -594,6 +668,7 @@ Result<RawTensor> KVCache::decode_step(size_t layer_idx, const RawTensor& q, con
                                    (int64_t)num_kv_heads, (int64_t)capacity, (int64_t)head_dim, scale ? 1 : 0,
                                    scale.value_or(0.f), ws, nullptr);
     if (rc != NNE_OK) return from_status(rc);
+    l.engaged = true;
     return out;
 }
 
@@ -607,6 +682,7 @@ Result<bool> KVCache::set_lengths(size_t layer_idx, const std::vector<int32_t>& 
                                                  std::to_string(capacity) + "]");
     Layer& l = layers_[layer_idx];
     l.lens_host = lens;
+    l.engaged = true;
     if (batch && nne_memcpy_h2d(l.lens_dev.get(), lens.data(), batch * 4, nullptr) != NNE_OK)
         return from_status(NNE_EHIP);
     return true;
@@ -774,6 +850,12 @@ Result<RawTensor> GroupedQueryAttention::forward_gqa_cached(const RawTensor& x, 
     return o_proj.forward(merged);
 }
 
+Result<RawTensor> GroupedQueryAttention::forward_gqa_cached(const RawTensor& x, size_t start_pos,
+                                                            std::optional<KVCache::Slot> layer_cache) {
+    if (!layer_cache || !layer_cache->has_value()) return forward_gqa_cached(x, start_pos, nullptr, 0);
+    return forward_gqa_cached(x, start_pos, &layer_cache->cache(), layer_cache->layer_idx());
+}
+
 // ---- MultiHeadAttention -----------------------------------------------------------
 
 MultiHeadAttention::MultiHeadAttention(size_t d_model_, size_t num_heads_, bool is_causal_)
@@ -892,6 +974,12 @@ Result<RawTensor> MultiHeadAttention::forward_attention_cached(const RawTensor& 
     auto merged = attend_merged(q, k_all, v_all, is_causal && t > 1, (int64_t)(total - t));
     if (merged.is_err()) return merged.error();
     return out_proj.forward(merged.value());                         // :124-128
+}
+
+Result<RawTensor> MultiHeadAttention::forward_attention_cached(const RawTensor& x,
+                                                               std::optional<KVCache::Slot> layer_cache) {
+    if (!layer_cache || !layer_cache->has_value()) return forward_attention_cached(x, nullptr, 0);
+    return forward_attention_cached(x, &layer_cache->cache(), layer_cache->layer_idx());
 }
 
 Result<RawTensor> MultiHeadAttention::forward_cross_attention_cached(

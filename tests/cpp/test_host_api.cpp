@@ -435,6 +435,49 @@ TEST_GPU(test_mha_ragged_decode_step_matches_oracle) {
     }
 }
 
+// The reference's models walk and mutate `kv_cache.layers` (kv_cache.rs:13):
+// they engage every slot with empty tensors before the prompt
+// (llama.rs:501-503, gpt2.rs:280) and hand layer i its slot
+// (llama.rs:463-471).  The same idioms on the device cache.
+TEST_GPU(test_kv_cache_layers_slot_view) {
+    const size_t b = 2, hkv = 2, hq = 4, c = 128, d = c / hq, cap = 24, t0 = 6;
+    manual_seed(16);
+    GroupedQueryAttention attn(c, hq, hkv, 64);
+    KVCache cache(2, b, hkv, cap, d);
+    CHECK(cache.layers().size() == 2);
+    for (auto slot : cache.layers()) CHECK(!slot.has_value());            // KVCache::new: all None
+    for (auto slot : cache.layers()) slot = {RawTensor::zeros({0}), RawTensor::zeros({0})};
+    for (auto slot : cache.layers()) CHECK(slot.has_value() && slot.value().first.shape()[2] == 0);
+    RawTensor x = RawTensor::randn({b, t0 + 1, c}, 0.f, 1.f);
+    const auto full = attn.forward_gqa_cached(x, 0, std::nullopt).unwrap().to_vec();   // uncached
+    attn.forward_gqa_cached(x.slice(1, 0, t0).unwrap(), 0, cache.layers().get_mut(1)).unwrap();
+    const auto step =
+        attn.forward_gqa_cached(x.slice(1, t0, t0 + 1).unwrap(), t0, cache.layers().get_mut(1)).unwrap().to_vec();
+    std::vector<float> last;
+    for (size_t bi = 0; bi < b; ++bi)
+        last.insert(last.end(), full.begin() + (bi * (t0 + 1) + t0) * c, full.begin() + (bi * (t0 + 1) + t0 + 1) * c);
+    check_close(step, last, "decode through the slot vs full prefill");
+    // reading the slot materialises [B, Hkv, L, d] views of the filled rows
+    const auto kv = cache.layers()[1].value();
+    CHECK(kv.first.shape() == (std::vector<size_t>{b, hkv, t0 + 1, d}));
+    CHECK(cache.layers()[0].value().first.shape()[2] == 0);              // layer 0 untouched
+    // Option::take moves the rows out; *slot = Some((k, v)) writes them back
+    auto taken = cache.layers()[1].take();
+    CHECK(taken.has_value() && !cache.layers()[1].has_value());
+    cache.layers()[0] = *taken;
+    CHECK(cache.layers()[0].value().first.to_vec() == taken->first.to_vec());
+    CHECK(cache.layers()[0].value().second.to_vec() == taken->second.to_vec());
+    CHECK(cache.current_seq_len(0) == t0 + 1);
+    // a None slot runs uncached (llama.rs:464-468 passes None on)
+    const auto none = attn.forward_gqa_cached(x, 0, cache.layers().get_mut(1)).unwrap().to_vec();
+    check_close(none, full, "None slot runs uncached");
+    CHECK(!cache.layers().get_mut(2).has_value());                        // Vec::get_mut past the end
+    auto bad = cache.layers()[0].set(RawTensor::zeros({b, hkv, cap + 1, d}), RawTensor::zeros({b, hkv, cap + 1, d}));
+    CHECK(bad.is_err() && cache.current_seq_len(0) == t0 + 1);            // refused, slot unchanged
+    cache.reset();                                                         // kv_cache.rs:25-29
+    for (auto slot : cache.layers()) CHECK(!slot.has_value());
+}
+
 TEST_GPU(test_cross_attention_cached_slot) {                              // attention.rs:139-210
     const size_t b = 2, c = 128, h = 2, tkv = 70;
     manual_seed(14);

@@ -241,3 +241,38 @@ def test_large_batch_uses_combine_kernel(nne, cuda):
     ref, kc, vc, lens = T.ref_decode_step(q, kc, vc, lens, kn, vn)
     T.assert_close(out, ref, what="B=150 step")
     assert list(host(cache.lens_dev[0])) == list(lens)
+
+
+def test_kv_cache_layers_slot_view(nne, cuda):
+    """KVCache.layers (kv_cache.rs:13) with the models' idioms: engage every
+    slot with empty tensors (llama.rs:501-503), fill through the cache, read
+    the slot back as [B, Hkv, L, d] views, assign Some((k, v)), None, reset."""
+    import torch
+    rng = np.random.default_rng(41)
+    b, hkv, cap, d = 2, 2, 32, 16
+    cache = nne.KVCache(2, b, hkv, cap, d, device=cuda)
+    assert len(cache.layers) == 2 and list(cache.layers) == [None, None]
+    for i in range(len(cache.layers)):
+        cache.layers[i] = (torch.zeros(0, device=cuda), torch.zeros(0, device=cuda))
+    assert all(kv is not None and kv[0].shape[2] == 0 for kv in cache.layers)
+    k1, v1 = rnd(rng, b, hkv, 5, d), rnd(rng, b, hkv, 5, d)
+    cache.update(1, dev(k1, cuda), dev(v1, cuda))
+    k_view, v_view = cache.layers[1]
+    assert k_view.shape == (b, hkv, 5, d) and k_view.data_ptr() == cache.k[1].data_ptr()
+    assert np.array_equal(host(k_view), k1) and np.array_equal(host(v_view), v1)
+    cache.layers[0] = (dev(k1, cuda), dev(v1, cuda))            # *slot = Some((k, v))
+    assert cache.current_seq_len(0) == 5 and np.array_equal(host(cache.layers[0][0]), k1)
+    q = rnd(rng, b, 4, 1, d)
+    out = host(cache.attend(0, dev(q, cuda)))
+    T.assert_close(out, T.ref_decode_attend(q, np.pad(k1, ((0, 0), (0, 0), (0, cap - 5), (0, 0))),
+                                            np.pad(v1, ((0, 0), (0, 0), (0, cap - 5), (0, 0))),
+                                            [5, 5]), what="attend after slot assignment")
+    with pytest.raises(nne.ShapeMismatch):
+        cache.layers[0] = (dev(k1[:, :1], cuda), dev(v1[:, :1], cuda))
+    assert cache.current_seq_len(0) == 5                       # refused, slot unchanged
+    cache.layers[1] = None
+    assert cache.layers[1] is None and cache.current_seq_len(1) == 0
+    cache.reset()
+    assert list(cache.layers) == [None, None]
+    with pytest.raises(IndexError):
+        cache.layers[2]
