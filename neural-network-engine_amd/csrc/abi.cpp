@@ -322,7 +322,7 @@ int check_kv_cache_args(int64_t B, int64_t Hq, int64_t Hkv, int64_t capacity, in
                     (long long)Hq, (long long)Hkv);
     if (decode && (d % 4 != 0 || nne::splitk_padded_dim((int)d) == 0))
         return fail(NNE_EINVAL, "Invalid configuration or argument: KV cache head dim %lld must be "
-                                "a multiple of 4 and at most 128", (long long)d);
+                                "a multiple of 4 and at most 256", (long long)d);
     return NNE_OK;
 }
 
@@ -574,10 +574,13 @@ int nne_kv_append(float* k_cache, float* v_cache, int32_t* lens_dev, int32_t* le
 
 uint64_t nne_decode_workspace_bytes(int64_t B, int64_t Hq, int64_t Hkv, int64_t d, int64_t max_len) {
     if (B <= 0 || Hkv <= 0 || Hq <= 0 || Hq % Hkv != 0 || d <= 0 || d % 4 != 0 || max_len < 0 ||
-        nne::splitk_padded_dim((int)d) == 0 || Hq / Hkv > nne::splitk_max_rows() ||
-        B > nne::splitk_max_seqs())
+        B > INT32_MAX || Hq > INT32_MAX || nne::splitk_padded_dim((int)d) == 0)
         return 0;
-    return nne::splitk_workspace_layout((int)B, (int)Hkv, (int)(Hq / Hkv), (int)d).total_bytes;
+    // One launch's worth: batches and rows beyond one launch run as several.
+    const int Bl = (int)std::min<int64_t>(B, nne::splitk_max_seqs());
+    const int Rl = (int)std::min<int64_t>(Hq / Hkv, nne::splitk_rows_per_launch((int)d));
+    if ((int64_t)Bl * Hkv > INT32_MAX) return 0;
+    return nne::splitk_workspace_layout(Bl, (int)Hkv, Rl, (int)d).total_bytes;
 }
 
 }  // extern "C"
@@ -593,16 +596,9 @@ int run_decode(const float* q, const int64_t* q_strides, const float* k_cache, c
                int64_t d, int has_scale, float scale, const nne_workspace_t* wsp, hipStream_t s) {
     int rc = check_kv_cache_args(B, Hq, Hkv, capacity, d, true);
     if (rc) return rc;
-    if (Hq / Hkv > nne::splitk_max_rows())
-        return fail(NNE_EINVAL, "Invalid configuration or argument: %lld query heads per KV head "
-                                "exceeds the decode kernel's %d", (long long)(Hq / Hkv),
-                    nne::splitk_max_rows());
     if (B == 0 || Hq == 0) return NNE_OK;
     if (!lens_host)
         return fail(NNE_EINVAL, "Invalid configuration or argument: lens_host is null");
-    if (B > nne::splitk_max_seqs())
-        return fail(NNE_EINVAL, "Invalid configuration or argument: decode batch of %lld sequences "
-                                "exceeds %d", (long long)B, nne::splitk_max_seqs());
     const bool append = k_new != nullptr;
     if (!q || !o || !k_cache || !v_cache || !lens_dev || (append && !v_new))
         return fail(NNE_EINVAL, "Invalid configuration or argument: null tensor pointer");
@@ -642,9 +638,9 @@ int run_decode(const float* q, const int64_t* q_strides, const float* k_cache, c
     const int64_t* vnst = vn_strides ? vn_strides : ckv;
     if (qst[3] != 1 || ost[3] != 1)
         return fail(NNE_EINVAL, "Invalid configuration or argument: decode q/o need unit dim stride");
-    // The 16-row tile (more than 4 query heads per KV head) reads q rows as
-    // 16-byte vectors.
-    if (Hq / Hkv > 4 && !vec_view(q, qst))
+    // The 16-row tiles (more than 4 query heads per KV head, or d > 128) read
+    // q rows as 16-byte vectors.
+    if ((Hq / Hkv > 4 || d > 128) && !vec_view(q, qst))
         return fail(NNE_EINVAL, "Invalid configuration or argument: decode q needs 16-byte alignment "
                                 "and strides that are multiples of 4");
     if (!aligned16(k_cache) || !aligned16(v_cache))
@@ -670,11 +666,13 @@ int run_decode(const float* q, const int64_t* q_strides, const float* k_cache, c
         p.vn_sb = vnst[0]; p.vn_sh = vnst[1];
         p.lens_w = lens_dev_w;
     }
-    const nne::SplitKWorkspace w =
-        nne::splitk_workspace_layout((int)B, (int)Hkv, (int)(Hq / Hkv), (int)d);
+    nne_workspace_size_t need{0, 0};
+    rc = nne_decode_workspace_size(B, Hq, Hkv, d, &need);
+    if (rc != NNE_OK) return rc;
     void* ws = nullptr;
     uint32_t* counters = nullptr;
-    rc = call_workspace(wsp, w.total_bytes, B * Hkv, s, &ws, &counters, "decode");
+    rc = call_workspace(wsp, need.records_bytes, (int64_t)need.n_counters, s, &ws, &counters,
+                        "decode");
     if (rc != NNE_OK) return rc;
     hipError_t e = nne::launch_splitk(p, total_keys, max_len, ws, s, seq_lens.data(), counters);
     if (e != hipSuccess) return hip_fail(e, "decode attention launch");
@@ -698,7 +696,7 @@ int nne_decode_workspace_size(int64_t B, int64_t Hq, int64_t Hkv, int64_t d,
                                 "Hq=%lld Hkv=%lld d=%lld", (long long)B, (long long)Hq,
                     (long long)Hkv, (long long)d);
     out->records_bytes = bytes;
-    out->n_counters = (uint64_t)B * (uint64_t)Hkv;
+    out->n_counters = (uint64_t)std::min<int64_t>(B, nne::splitk_max_seqs()) * (uint64_t)Hkv;
     return NNE_OK;
 }
 

@@ -100,8 +100,9 @@ struct QkvParams {
 };
 
 // Split-K few-query kernel parameters (decode and cross-attention).  Each KV
-// head serves R = G * Tq query rows; row rr maps to query head kvh*G + rr/Tq
-// and query position rr % Tq.  Every row sees every key of its sequence.
+// head serves G * Tq query rows; a launch takes R of them starting at row0,
+// and its row rr maps to query head kvh*G + (row0+rr)/Tq and query position
+// (row0+rr) % Tq.  Every row sees every key of its sequence.
 // Sequences whose flattened prefix travels in the kernel arguments.
 constexpr int kArgSeqs = 128;
 
@@ -116,6 +117,7 @@ struct SplitKParams {
     int max_keys;            // host-validated upper bound on every key count
     OutView4 o;
     int B, Hq, Hkv, G, Tq, d, R;
+    int row0;                // first of this launch's rows (row passes of many-row heads)
     float qscale;            // softmax scale * log2(e)
     // Causal rows (masked != 0): query t sees keys c <= q_off + t only.
     int masked;

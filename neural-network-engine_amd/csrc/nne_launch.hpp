@@ -8,10 +8,14 @@
 
 namespace nne {
 
-// Head dims are padded to the next of {32, 64, 128}; 0 = unsupported.
+// Head dims are padded to the next of {32, 64, 128} (prefill) or
+// {64, 128, 256} (split-K); 0 = unsupported.
 int prefill_padded_dim(int d);
 int splitk_padded_dim(int d);
+// Query rows per KV head the few-query prefill routes to the split-K kernel.
 int splitk_max_rows();
+// Query rows per KV head one split-K launch serves (more go in further launches).
+int splitk_rows_per_launch(int d);
 
 // `vec` selects 16-byte loads/stores: requires dim stride 1, d % 4 == 0,
 // 16-byte aligned base pointers and row/head/batch strides that are multiples of 4.
@@ -26,8 +30,9 @@ struct PrefillSplit {
 };
 PrefillSplit prefill_split_plan(PrefillParams& p, bool causal, bool vec);
 
-// Split-K workspace: per-sequence prefix (B+1 ints) and partial records for
-// up to splitk_max_workgroups() + B*Hkv (workgroup, head) pairs.
+// Split-K workspace of one launch (at most splitk_max_seqs() sequences and
+// splitk_rows_per_launch() rows): per-sequence prefix (B+1 ints) and partial
+// records for up to (workgroups of a launch) + B*Hkv (workgroup, head) pairs.
 // Workspace: [prefix (B+1) int32][partial (max, sum)][partial O].
 struct SplitKWorkspace {
     uint64_t ml_offset;
@@ -41,6 +46,9 @@ SplitKWorkspace splitk_workspace_layout(int B, int Hkv, int R, int d);
 // rows.  With counters (B*Hkv zeroed arrival counters, left zeroed) and at
 // most kArgSeqs sequences, the last workgroup of each split head merges it;
 // otherwise the per-head combine kernel follows.  max_len bounds every sequence.
+// Batches beyond splitk_max_seqs() and rows beyond splitk_rows_per_launch()
+// take several launches in stream order, with the workspace and counters of
+// one.
 // seq_lens (host) are this launch's key counts per sequence (including a
 // decode step's new row), or null when every sequence has p.tk keys.
 hipError_t launch_splitk(SplitKParams p, int64_t total_keys, int max_len, void* workspace,

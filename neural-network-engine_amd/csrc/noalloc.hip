@@ -75,8 +75,10 @@ extern "C" int nne_decode_step_noalloc(const float* q, const int64_t q_strides[4
     // [arrival counters (B * Hkv, 256-byte aligned)][split-K workspace].
     // Geometry the decode kernel does not take reports 0 bytes and is
     // refused by the validation in run_decode.
-    const uint64_t ws_bytes = nne_decode_workspace_bytes(B, Hq, Hkv, d, 0);
-    const uint64_t cnt_bytes = ws_bytes ? ((uint64_t)B * (uint64_t)Hkv * 4 + 255) / 256 * 256 : 0;
+    nne_workspace_size_t need{0, 0};
+    const uint64_t ws_bytes =
+        nne_decode_workspace_size(B, Hq, Hkv, d, &need) == NNE_OK ? need.records_bytes : 0;
+    const uint64_t cnt_bytes = ws_bytes ? (need.n_counters * 4 + 255) / 256 * 256 : 0;
     if (cnt_bytes + ws_bytes > kScratchBytes) {
         char msg[256];
         snprintf(msg, sizeof(msg),
@@ -91,8 +93,8 @@ extern "C" int nne_decode_step_noalloc(const float* q, const int64_t q_strides[4
     uint32_t* counters = static_cast<uint32_t*>(base);
     void* ws = static_cast<char*>(base) + cnt_bytes;
     const hipStream_t s = static_cast<hipStream_t>(stream);
-    if (ws_bytes > 0 && B * Hkv > 0) {
-        const hipError_t e = nne::zero_counters(counters, B * Hkv, s);
+    if (ws_bytes > 0 && need.n_counters > 0) {
+        const hipError_t e = nne::zero_counters(counters, (int64_t)need.n_counters, s);
         if (e != hipSuccess) return nne::fail_hip(e, "no-allocation counter clear");
     }
     const nne_workspace_t scratch_ws{ws, kScratchBytes - cnt_bytes, counters,

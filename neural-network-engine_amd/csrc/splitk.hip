@@ -58,7 +58,8 @@ typedef float floatx4 __attribute__((ext_vector_type(4)));
 
 constexpr int KB = 16;            // keys per block (one 16x16x4 MFMA tile of keys)
 constexpr int MAX_SEQS = 2048;    // sequences per launch (prefix array in LDS)
-constexpr int MAX_PARTS = 512;    // workgroups sharing one head (combine weights in LDS)
+constexpr int MAX_PARTS = 512;    // workgroups sharing one head
+constexpr int COMBINE_ML = 8192;  // (record, row) pairs the combine kernel holds in LDS
 constexpr int MAX_WG = 2048;      // workgroups of one split launch
 
 __device__ __forceinline__ int clamp_len(int L, int max_keys) {
@@ -127,6 +128,13 @@ __device__ __forceinline__ float float_unorder(unsigned k) {
     return __uint_as_float((k & 0x80000000u) ? (k & 0x7fffffffu) : ~k);
 }
 
+// 16-byte load, non-temporal when each byte is read by one wave only.
+template <bool NT>
+__device__ __forceinline__ vf4 load4(const float* p) {
+    if constexpr (NT) return __builtin_nontemporal_load(reinterpret_cast<const vf4*>(p));
+    else return *reinterpret_cast<const vf4*>(p);
+}
+
 // Orders this wave's LDS accesses on both sides of a cross-lane exchange.
 __device__ __forceinline__ void wave_lds_sync() {
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -174,9 +182,10 @@ __device__ __forceinline__ void build_prefix(const SplitKParams& p, int* pref, i
 }
 
 // Merges the n partial records (slots s0 .. s0+n-1) of one head into its
-// output, then clears the head's arrival counter.  n * R <= 1024 (the host
-// bounds the workgroups per head), so each thread holds at most 4 (max, sum)
-// pairs; the O rows are read NPRE records per round trip.
+// output, then clears the head's arrival counter.  R <= ROWS <= 64 and
+// n * R <= 1024 (the host bounds the workgroups per head), so each thread
+// holds at most 4 (max, sum) pairs; the O rows are read NPRE records per
+// round trip.
 template <int D, int ROWS>
 __device__ __forceinline__ void merge_head_records(const SplitKParams& p, int b, int kvh, int head,
                                                    int64_t s0, int n, float* w_s, unsigned* red_m,
@@ -223,8 +232,9 @@ __device__ __forceinline__ void merge_head_records(const SplitKParams& p, int b,
     // Denominators in a fixed order: 16 lanes per row (record c to lane
     // c % 16), then a butterfly over the 16, so repeated calls give the same
     // bits whichever workgroup merges and however its waves are scheduled.
-    {
-        const int rr = tid >> 4, part = tid & 15;
+#pragma unroll
+    for (int r0 = 0; r0 < ROWS; r0 += 16) {
+        const int rr = r0 + (tid >> 4), part = tid & 15;
         float l = 0.f;
         if (rr < p.R)
             for (int c = part; c < n; c += 16) l += w_s[1024 + c * p.R + rr];
@@ -268,7 +278,7 @@ __device__ __forceinline__ void merge_head_records(const SplitKParams& p, int b,
         const int rr = e / D, dd = e % D;
         if (dd < p.d) {
             const float den = red_l[rr];
-            const int hq = kvh * p.G + rr / p.Tq, t = rr % p.Tq;
+            const int gr = p.row0 + rr, hq = kvh * p.G + gr / p.Tq, t = gr % p.Tq;
             p.o.p[b * p.o.sb + hq * p.o.sh + t * p.o.st + dd] = den > 0.f ? acc[j] / den : 0.f;
         }
     }
@@ -277,6 +287,10 @@ __device__ __forceinline__ void merge_head_records(const SplitKParams& p, int b,
 }
 
 // ROWS = 16: R <= 16 query rows per KV head on v_mfma_f32_16x16x4_f32 (above).
+// ROWS = 32 / 64: 2 / 4 row groups of 16 rows; the waves split into the row
+// groups (2 / 1 waves each), and the waves of a group interleave the blocks,
+// so every K/V byte of the chunk is read from HBM once for all the rows (the
+// row groups' loads of one block meet in L1 / L2, so they use ordinary loads).
 // ROWS = 4: R <= 4 rows (single-token decode with G <= 4) on
 // v_mfma_f32_4x4x1_16b_f32, which wastes no MFMA work on padding rows:
 //   S = Q K^T: lane l scores key l % 16 over dim group l / 16 (D/4 dims); Q is
@@ -287,9 +301,15 @@ __device__ __forceinline__ void merge_head_records(const SplitKParams& p, int b,
 //     holds the 16 keys' probabilities, regrouped through LDS); each key group
 //     accumulates its own partial O, summed once per segment.
 // MASK: causal rows (p.masked), compiled only into the variants that serve them.
+// A split launch places at most one workgroup on a CU (its chunks are cut
+// for that), so the 16-row tiles at d >= 128 may take the whole register
+// file (AGPRs included) instead of spilling.
 template <int D, bool APPEND, int ROWS, bool MASK = false>
-__global__ __launch_bounds__(256, 2) void splitk_kernel(const SplitKParams p) {
+__global__ __launch_bounds__(256, (D >= 128 && ROWS >= 16) ? 1 : 2) void splitk_kernel(const SplitKParams p) {
     constexpr bool NARROW = ROWS == 4;
+    constexpr int RG = NARROW ? 1 : ROWS / 16;   // row groups of 16 rows
+    constexpr int WPR = 4 / RG;                  // waves per row group
+    constexpr bool NT = RG == 1;                 // each block read by one wave only
     constexpr int KS = D + 4;            // LDS row stride (16-byte reads conflict-free)
     constexpr int LPR = D / 4;           // lanes per K row in the coalesced load
     constexpr int RPI = 64 / LPR;        // K rows per load instruction
@@ -300,17 +320,20 @@ __global__ __launch_bounds__(256, 2) void splitk_kernel(const SplitKParams p) {
     constexpr int OS = D + 4;            // merge-buffer row stride (rows start 4 banks apart)
     constexpr int NQN = D / 16;          // narrow: Q registers per lane
     constexpr int CBV = D == 128 ? 3 : 2;  // narrow: PV broadcast group (LPR / 4 blocks)
-    constexpr int DEPTH = 2;             // K/V blocks held in registers per wave
-    static_assert(ROWS == 16 || ROWS == 4, "row tile");
-    static_assert(4 * ROWS * OS <= 4 * KB * KS, "merge buffer must fit in the K slices");
+    // K/V blocks held in registers per wave (at d = 256 one 16-key block is
+    // 32 KB of K and V per wave, and the other waves cover its latency)
+    constexpr int DEPTH = D >= 256 ? 1 : 2;
+    static_assert(ROWS == 4 || ROWS == 16 || ROWS == 32 || ROWS == 64, "row tile");
+    static_assert(!NARROW || D <= 128, "4-row tile up to d = 128");
+    static_assert(4 * (NARROW ? 4 : 16) * OS <= 4 * KB * KS, "merge buffer must fit in the K slices");
     static_assert(2048 <= 4 * KB * KS, "merge weights (2 x 1024) must fit in the K slices");
     static_assert(NK == 4 * NH, "K and V loads per block");
 
     __shared__ __attribute__((aligned(16))) float lds[4 * KB * KS];
     __shared__ float ml_s[4][16][2];
     __shared__ vf4 p_s[4][16];           // narrow: P of a wave's 16 keys
-    __shared__ unsigned red_m[16];       // fused combine: per-row max (ordered)
-    __shared__ float red_l[16];          // fused combine: per-row denominator
+    __shared__ unsigned red_m[64];       // fused combine: per-row max (ordered)
+    __shared__ float red_l[64];          // fused combine: per-row denominator
     __shared__ int pend_s[2][3];         // fused combine: heads this workgroup merges
     __shared__ int n_pend_s;
     __shared__ int pref[MAX_SEQS + 1];
@@ -320,6 +343,9 @@ __global__ __launch_bounds__(256, 2) void splitk_kernel(const SplitKParams p) {
     // compiler neither masks it nor drains the prefetched loads at its head.
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int col = lane & 15, grp = lane >> 4;
+    // row group of this wave and its place among the group's waves
+    const int rgw = wave / WPR, kw = wave % WPR;
+    const int my_row = 16 * rgw + col;    // 16-row tiles: this lane's query row
     // narrow lane roles: QK broadcast block within the dim group, A row, and
     // the P element supplied to PV (key RPI * block + key group, row).
     const int na = (lane >> 2) & 3, ni = lane & 3;
@@ -338,7 +364,7 @@ __global__ __launch_bounds__(256, 2) void splitk_kernel(const SplitKParams p) {
             if (pref[bb + 1] != pref[bb]) continue;
             for (int e = tid; e < p.Hkv * p.R * p.d; e += 256) {
                 const int dd = e % p.d, rest = e / p.d, rr = rest % p.R, kv = rest / p.R;
-                const int hq = kv * p.G + rr / p.Tq, t = rr % p.Tq;
+                const int gr = p.row0 + rr, hq = kv * p.G + gr / p.Tq, t = gr % p.Tq;
                 p.o.p[bb * p.o.sb + hq * p.o.sh + t * p.o.st + dd] = 0.f;
             }
         }
@@ -408,7 +434,8 @@ __global__ __launch_bounds__(256, 2) void splitk_kernel(const SplitKParams p) {
         float qf[NARROW ? NQN : NQ];
         if constexpr (NARROW) {
             const bool rok = ni < p.R;
-            const int hq = kvh * p.G + (rok ? ni / p.Tq : 0), t = rok ? ni % p.Tq : 0;
+            const int gr = p.row0 + (rok ? ni : 0);
+            const int hq = kvh * p.G + gr / p.Tq, t = gr % p.Tq;
             const float* qp = p.q.p + b * p.q.sb + hq * p.q.sh + t * p.q.st;
 #pragma unroll
             for (int t4 = 0; t4 < NQN; ++t4) {   // clamped loads, then select: no waits between them
@@ -417,8 +444,9 @@ __global__ __launch_bounds__(256, 2) void splitk_kernel(const SplitKParams p) {
                 qf[t4] = (rok && c < p.d) ? x * p.qscale : 0.f;
             }
         } else {
-            const bool rok = col < p.R;
-            const int hq = kvh * p.G + (rok ? col / p.Tq : 0), t = rok ? col % p.Tq : 0;
+            const bool rok = my_row < p.R;
+            const int gr = p.row0 + (rok ? my_row : 0);
+            const int hq = kvh * p.G + gr / p.Tq, t = gr % p.Tq;
             const float* qp = p.q.p + b * p.q.sb + hq * p.q.sh + t * p.q.st;
 #pragma unroll
             for (int s4 = 0; s4 < NQ / 4; ++s4) {   // clamped loads, then select
@@ -444,13 +472,13 @@ __global__ __launch_bounds__(256, 2) void splitk_kernel(const SplitKParams p) {
 #pragma unroll
             for (int i = 0; i < NK; ++i) {
                 const int key = min(kb0 + lane / LPR + RPI * i, key_end - 1);
-                kr[i] = __builtin_nontemporal_load(reinterpret_cast<const vf4*>(kb + key * kst + kc_col));
+                kr[i] = load4<NT>(kb + key * kst + kc_col);
             }
             if constexpr (NARROW) {
 #pragma unroll
                 for (int i = 0; i < NK; ++i) {
                     const int key = min(kb0 + lane / LPR + RPI * i, key_end - 1);
-                    vr[i] = __builtin_nontemporal_load(reinterpret_cast<const vf4*>(vb + key * vst + kc_col));
+                    vr[i] = load4<NT>(vb + key * vst + kc_col);
                 }
             } else {
 #pragma unroll
@@ -458,7 +486,7 @@ __global__ __launch_bounds__(256, 2) void splitk_kernel(const SplitKParams p) {
                     const int key = min(kb0 + 4 * grp + st, key_end - 1);
 #pragma unroll
                     for (int h = 0; h < NH; ++h)
-                        vr[st * NH + h] = __builtin_nontemporal_load(reinterpret_cast<const vf4*>(vb + key * vst + v_col[h]));
+                        vr[st * NH + h] = load4<NT>(vb + key * vst + v_col[h]);
                 }
             }
         };
@@ -509,7 +537,7 @@ __global__ __launch_bounds__(256, 2) void splitk_kernel(const SplitKParams p) {
             if (MASK && kb0 + KB - 1 > p.q_off) {   // causal rows: key <= q_off + t
 #pragma unroll
                 for (int r = 0; r < 4; ++r)
-                    s[r] = kb0 + col <= p.q_off + r % p.Tq ? s[r] : kNegInf;
+                    s[r] = kb0 + col <= p.q_off + (p.row0 + r) % p.Tq ? s[r] : kNegInf;
             }
             // Lazy rescale: keep each row's reference max until a score exceeds
             // it by 8 (a factor 256 in exp2), so most blocks skip the row max.
@@ -561,7 +589,7 @@ __global__ __launch_bounds__(256, 2) void splitk_kernel(const SplitKParams p) {
                 for (int r = 0; r < 4; ++r) s[r] = (kb0 + 4 * grp + r < key_end) ? s[r] : kNegInf;
             }
             if (MASK && kb0 + KB - 1 > p.q_off) {   // causal rows: key <= q_off + t
-                const int last = p.q_off + col % p.Tq;
+                const int last = p.q_off + (p.row0 + my_row) % p.Tq;
 #pragma unroll
                 for (int r = 0; r < 4; ++r) s[r] = (kb0 + 4 * grp + r <= last) ? s[r] : kNegInf;
             }
@@ -596,8 +624,8 @@ __global__ __launch_bounds__(256, 2) void splitk_kernel(const SplitKParams p) {
           }
         };
 
-        // Ring of DEPTH register buffers over this wave's blocks (wave,
-        // wave+4, ...): while one block computes, the next DEPTH-1 blocks'
+        // Ring of DEPTH register buffers over this wave's blocks (kw,
+        // kw+WPR, ...): while one block computes, the next DEPTH-1 blocks'
         // loads are in flight.  The loop has a single exit at its end, which
         // lets the next blocks' loads issue before the wait for the current
         // block's data.  At d = 64 (8 KB of K/V per 16-key block) 3 and 4
@@ -605,23 +633,23 @@ __global__ __launch_bounds__(256, 2) void splitk_kernel(const SplitKParams p) {
         // 29.6 and 30.5 against 28.9 us, GPT-2 decode attend 35.0 and 35.3
         // against 32.5 us.
         const int n_blocks = (key_end - key_begin + KB - 1) / KB;
-        const int n_mine = wave < n_blocks ? (n_blocks - wave + 3) / 4 : 0;
+        const int n_mine = kw < n_blocks ? (n_blocks - kw + WPR - 1) / WPR : 0;
         vf4 kq[DEPTH][NK], vq[DEPTH][4 * NH];
-        int kb0 = key_begin + wave * KB;
+        int kb0 = key_begin + kw * KB;
 #pragma unroll
-        for (int s = 0; s + 1 < DEPTH; ++s) load_block(kq[s], vq[s], kb0 + 4 * KB * s);
+        for (int s = 0; s + 1 < DEPTH; ++s) load_block(kq[s], vq[s], kb0 + WPR * KB * s);
         int done = 0;
-        for (; done + DEPTH <= n_mine; done += DEPTH, kb0 += 4 * KB * DEPTH) {
+        for (; done + DEPTH <= n_mine; done += DEPTH, kb0 += WPR * KB * DEPTH) {
 #pragma unroll
             for (int s = 0; s < DEPTH; ++s) {
                 load_block(kq[(s + DEPTH - 1) % DEPTH], vq[(s + DEPTH - 1) % DEPTH],
-                           kb0 + 4 * KB * (s + DEPTH - 1));
-                block(kq[s], vq[s], kb0 + 4 * KB * s);
+                           kb0 + WPR * KB * (s + DEPTH - 1));
+                block(kq[s], vq[s], kb0 + WPR * KB * s);
             }
         }
 #pragma unroll
         for (int s = 0; s + 1 < DEPTH; ++s)
-            if (done + s < n_mine) block(kq[s], vq[s], kb0 + 4 * KB * s);
+            if (done + s < n_mine) block(kq[s], vq[s], kb0 + WPR * KB * s);
         if (NARROW && has_new && wave == 0 && lane < LPR && 4 * lane < p.d) {
             const int row = Lb - 1;
             *reinterpret_cast<vf4*>(const_cast<float*>(kb) + row * kst + 4 * lane) = nk;
@@ -664,23 +692,27 @@ __global__ __launch_bounds__(256, 2) void splitk_kernel(const SplitKParams p) {
         }
         __syncthreads();
 
+        // Rows of the 16-row tiles sit at ob[(wave * 16 + row % 16) * OS];
+        // row rr is the row group rr / 16, whose WPR waves are merged.
+        constexpr int RPW = NARROW ? 4 : 16;
         const int64_t slot = (int64_t)wg + head;    // unique per (workgroup, head)
         for (int e = tid; e < p.R * D; e += 256) {
             const int rr = e / D, dd = e % D;
+            const int w0 = (rr / RPW) * WPR, lr = rr % RPW;
             float M = kNegInf;
 #pragma unroll
-            for (int w = 0; w < 4; ++w) M = fmaxf(M, ml_s[w][rr][0]);
+            for (int j = 0; j < WPR; ++j) M = fmaxf(M, ml_s[w0 + j][lr][0]);
             const float M_use = M == kNegInf ? 0.f : M;
             float l = 0.f, acc = 0.f;
 #pragma unroll
-            for (int w = 0; w < 4; ++w) {
-                const float f = fast_exp2(ml_s[w][rr][0] - M_use);
-                l += f * ml_s[w][rr][1];
-                acc += f * ob[(w * ROWS + rr) * OS + dd];
+            for (int j = 0; j < WPR; ++j) {
+                const float f = fast_exp2(ml_s[w0 + j][lr][0] - M_use);
+                l += f * ml_s[w0 + j][lr][1];
+                acc += f * ob[((w0 + j) * RPW + lr) * OS + dd];
             }
             if (whole) {
                 if (dd < p.d) {
-                    const int hq = kvh * p.G + rr / p.Tq, t = rr % p.Tq;
+                    const int gr = p.row0 + rr, hq = kvh * p.G + gr / p.Tq, t = gr % p.Tq;
                     p.o.p[b * p.o.sb + hq * p.o.sh + t * p.o.st + dd] = l > 0.f ? acc / l : 0.f;
                 }
             } else {
@@ -718,7 +750,7 @@ __global__ __launch_bounds__(256, 2) void splitk_kernel(const SplitKParams p) {
         const int L = (pref[bb + 1] - pref[bb]) / p.Hkv;
         const int h0 = pref[bb] + kv * L;
         const int n = (h0 + L - 1) / p.chunk - w_first + 1;
-        if (tid < 16) { red_m[tid] = float_order(kNegInf); red_l[tid] = 0.f; }
+        if (tid < 64) { red_m[tid] = float_order(kNegInf); red_l[tid] = 0.f; }
         __syncthreads();
         merge_head_records<D, ROWS>(p, bb, kv, bb * p.Hkv + kv, (int64_t)w_first + bb * p.Hkv + kv, n,
                               lds, red_m, red_l, tid);
@@ -731,11 +763,11 @@ __global__ __launch_bounds__(256, 2) void splitk_kernel(const SplitKParams p) {
 // publish the sequence's new length.  Every global load is issued before the
 // first barrier (partial O rows into registers, (max, sum) pairs into LDS), so
 // the kernel costs one memory round trip.
-template <int D>
+template <int D, int ROWS>
 __global__ __launch_bounds__(256) void splitk_combine_kernel(const SplitKParams p) {
-    constexpr int EPT = 16 * D / 256;     // output elements per thread (R <= 16)
-    constexpr int NPRE = 4;               // partials per element held in registers
-    __shared__ float2 ml_s[MAX_PARTS][16];
+    constexpr int EPT = ROWS * D / 256;   // output elements per thread (R <= ROWS)
+    constexpr int NPRE = EPT >= 16 ? 2 : 4;   // partials per element held in registers
+    __shared__ float2 ml_s[COMBINE_ML];   // [n records][R rows], n * R <= COMBINE_ML
     const int head = blockIdx.x;
     const int b = head / p.Hkv, kvh = head % p.Hkv;
     const int tid = threadIdx.x;
@@ -744,7 +776,7 @@ __global__ __launch_bounds__(256) void splitk_combine_kernel(const SplitKParams 
     const int Lb = (p1 - p0) / p.Hkv;
     if (p.lens_w && kvh == 0 && tid == 0) p.lens_w[b] = Lb;
     auto out_ptr = [&](int rr) {
-        const int hq = kvh * p.G + rr / p.Tq, t = rr % p.Tq;
+        const int gr = p.row0 + rr, hq = kvh * p.G + gr / p.Tq, t = gr % p.Tq;
         return p.o.p + b * p.o.sb + hq * p.o.sh + t * p.o.st;
     };
     if (Lb == 0) {
@@ -767,19 +799,17 @@ __global__ __launch_bounds__(256) void splitk_combine_kernel(const SplitKParams 
         for (int c = 0; c < NPRE; ++c)
             pre[j][c] = (e < RD && c < n) ? o_src[(int64_t)c * RD + e] : 0.f;
     }
-    for (int e = tid; e < n * p.R; e += 256) {
-        const int c = e / p.R, rr = e % p.R;
-        ml_s[c][rr] = *reinterpret_cast<const float2*>(p.ws_ml + ((s0 + c) * p.R + rr) * 2);
-    }
+    for (int e = tid; e < n * p.R; e += 256)
+        ml_s[e] = *reinterpret_cast<const float2*>(p.ws_ml + ((s0 + e / p.R) * p.R + e % p.R) * 2);
     __syncthreads();
     if (tid < p.R) {                      // weights: exp2(m_c - M) / sum_c exp2(m_c - M) l_c
         float M = kNegInf;
-        for (int c = 0; c < n; ++c) M = fmaxf(M, ml_s[c][tid].x);
+        for (int c = 0; c < n; ++c) M = fmaxf(M, ml_s[c * p.R + tid].x);
         const float M_use = M == kNegInf ? 0.f : M;
         float den = 0.f;
-        for (int c = 0; c < n; ++c) den += fast_exp2(ml_s[c][tid].x - M_use) * ml_s[c][tid].y;
+        for (int c = 0; c < n; ++c) den += fast_exp2(ml_s[c * p.R + tid].x - M_use) * ml_s[c * p.R + tid].y;
         const float inv = den > 0.f ? 1.f / den : 0.f;
-        for (int c = 0; c < n; ++c) ml_s[c][tid].x = fast_exp2(ml_s[c][tid].x - M_use) * inv;
+        for (int c = 0; c < n; ++c) ml_s[c * p.R + tid].x = fast_exp2(ml_s[c * p.R + tid].x - M_use) * inv;
     }
     __syncthreads();
 #pragma unroll
@@ -790,34 +820,44 @@ __global__ __launch_bounds__(256) void splitk_combine_kernel(const SplitKParams 
         float acc = 0.f;
 #pragma unroll
         for (int c = 0; c < NPRE; ++c)
-            if (c < n) acc += ml_s[c][rr].x * pre[j][c];
-        for (int c = NPRE; c < n; ++c) acc += ml_s[c][rr].x * o_src[(int64_t)c * RD + e];
+            if (c < n) acc += ml_s[c * p.R + rr].x * pre[j][c];
+        for (int c = NPRE; c < n; ++c) acc += ml_s[c * p.R + rr].x * o_src[(int64_t)c * RD + e];
         if (dd < p.d) out_ptr(rr)[dd] = acc;
     }
 }
 
-template <int D>
-hipError_t launch_splitk_d(const SplitKParams& p, hipStream_t stream) {
+template <int D, int ROWS>
+hipError_t launch_rows(const SplitKParams& p, hipStream_t stream) {
     if (p.n_wg > 0) {
-        const bool narrow = p.R <= 4;
-        if (p.k_new && narrow)
-            hipLaunchKernelGGL((splitk_kernel<D, true, 4>), dim3(p.n_wg), dim3(256), 0, stream, p);
-        else if (p.k_new)
-            hipLaunchKernelGGL((splitk_kernel<D, true, 16>), dim3(p.n_wg), dim3(256), 0, stream, p);
-        else if (narrow && p.masked)
-            hipLaunchKernelGGL((splitk_kernel<D, false, 4, true>), dim3(p.n_wg), dim3(256), 0, stream, p);
-        else if (narrow)
-            hipLaunchKernelGGL((splitk_kernel<D, false, 4>), dim3(p.n_wg), dim3(256), 0, stream, p);
-        else if (p.masked)
-            hipLaunchKernelGGL((splitk_kernel<D, false, 16, true>), dim3(p.n_wg), dim3(256), 0, stream, p);
+        // Causal rows come only from few-query prefill steps (<= 16 rows).
+        bool masked = false;
+        if constexpr (ROWS <= 16) masked = p.masked != 0;
+        if (p.k_new)
+            hipLaunchKernelGGL((splitk_kernel<D, true, ROWS>), dim3(p.n_wg), dim3(256), 0, stream, p);
+        else if (masked)
+            hipLaunchKernelGGL((splitk_kernel<D, false, ROWS <= 16 ? ROWS : 16, true>), dim3(p.n_wg),
+                               dim3(256), 0, stream, p);
         else
-            hipLaunchKernelGGL((splitk_kernel<D, false, 16>), dim3(p.n_wg), dim3(256), 0, stream, p);
+            hipLaunchKernelGGL((splitk_kernel<D, false, ROWS>), dim3(p.n_wg), dim3(256), 0, stream, p);
         hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;
     }
     if (p.fused) return hipSuccess;
-    hipLaunchKernelGGL((splitk_combine_kernel<D>), dim3(p.B * p.Hkv), dim3(256), 0, stream, p);
+    hipLaunchKernelGGL((splitk_combine_kernel<D, ROWS>), dim3(p.B * p.Hkv), dim3(256), 0, stream, p);
     return hipGetLastError();
+}
+
+// Row tile of a launch: 4 rows (single-token decode with G <= 4, d <= 128),
+// else the smallest of 16 / 32 / 64 that holds the launch's rows.
+template <int D>
+hipError_t launch_splitk_d(const SplitKParams& p, hipStream_t stream) {
+    if (D <= 128 && p.R <= 4) {
+        if constexpr (D <= 128) return launch_rows<D, 4>(p, stream);
+    }
+    if (p.R <= 16) return launch_rows<D, 16>(p, stream);
+    if (p.R <= 32) return launch_rows<D, 32>(p, stream);
+    if constexpr (D <= 128) return launch_rows<D, 64>(p, stream);
+    return hipErrorInvalidValue;
 }
 
 // ---- KV append (prefill-style, many rows) ---------------------------------
@@ -883,10 +923,12 @@ int split_workgroups() {
 int splitk_padded_dim(int d) {
     if (d <= 64) return 64;
     if (d <= 128) return 128;
+    if (d <= 256) return 256;
     return 0;
 }
 
 int splitk_max_rows() { return 16; }
+int splitk_rows_per_launch(int d) { return splitk_padded_dim(d) >= 256 ? 32 : 64; }
 int splitk_max_seqs() { return MAX_SEQS; }
 int splitk_max_workgroups() { return MAX_WG; }
 
@@ -927,8 +969,12 @@ hipError_t launch_flat(SplitKParams p, int64_t total_keys, int max_len, hipStrea
 
 }  // namespace
 
-hipError_t launch_splitk(SplitKParams p, int64_t total_keys, int max_len, void* workspace,
-                         hipStream_t stream, const int32_t* seq_lens, uint32_t* counters) {
+namespace {
+
+// One launch (plus, without the fused merge, its combine kernel) over at most
+// MAX_SEQS sequences and one tile of rows.
+hipError_t launch_one(SplitKParams p, int64_t total_keys, int max_len, void* workspace,
+                      hipStream_t stream, const int32_t* seq_lens, uint32_t* counters) {
     // Small batches carry the flattened prefix in the arguments, which saves
     // every workgroup the scan over lens.
     p.arg_pref_valid = p.B <= kArgSeqs ? 1 : 0;
@@ -937,12 +983,10 @@ hipError_t launch_splitk(SplitKParams p, int64_t total_keys, int max_len, void* 
         for (int b = 0; b < p.B; ++b)
             p.arg_pref[b + 1] = p.arg_pref[b] + p.Hkv * (seq_lens ? seq_lens[b] : p.tk);
     }
-    p.G = p.Hq / p.Hkv;
-    p.R = p.G * p.Tq;
     // Fused combine needs the prefix in the arguments (no workgroup reads
     // lens, so the lens bump can happen inside the launch) and n * R <= 1024.
     p.fused = p.arg_pref_valid && counters != nullptr;
-    p.max_parts = p.fused ? std::min(MAX_PARTS, 1024 / p.R) : MAX_PARTS;
+    p.max_parts = std::min(MAX_PARTS, (p.fused ? 1024 : COMBINE_ML) / p.R);
     const SplitKWorkspace w = splitk_workspace_layout(p.B, p.Hkv, p.R, p.d);
     char* base = static_cast<char*>(workspace);
     p.ws_pref = reinterpret_cast<int32_t*>(base);
@@ -952,8 +996,57 @@ hipError_t launch_splitk(SplitKParams p, int64_t total_keys, int max_len, void* 
     switch (splitk_padded_dim(p.d)) {
         case 64: return launch_flat<64>(p, total_keys, max_len, stream);
         case 128: return launch_flat<128>(p, total_keys, max_len, stream);
+        case 256: return launch_flat<256>(p, total_keys, max_len, stream);
         default: return hipErrorInvalidValue;
     }
+}
+
+}  // namespace
+
+hipError_t launch_splitk(SplitKParams p, int64_t total_keys, int max_len, void* workspace,
+                         hipStream_t stream, const int32_t* seq_lens, uint32_t* counters) {
+    p.G = p.Hq / p.Hkv;
+    // Batches beyond MAX_SEQS sequences: one launch per block of sequences,
+    // in stream order, sharing the workspace and counters.
+    if (p.B > MAX_SEQS) {
+        for (int b0 = 0; b0 < p.B; b0 += MAX_SEQS) {
+            SplitKParams c = p;
+            c.B = std::min(MAX_SEQS, p.B - b0);
+            c.q.p += b0 * p.q.sb;
+            c.o.p += b0 * p.o.sb;
+            c.k += b0 * p.ksb;
+            c.v += b0 * p.vsb;
+            if (c.lens) c.lens += b0;
+            if (c.lens_w) c.lens_w += b0;
+            if (c.k_new) {
+                c.k_new += b0 * p.kn_sb;
+                c.v_new += b0 * p.vn_sb;
+            }
+            int64_t keys = 0;
+            for (int b = 0; b < c.B; ++b) keys += (int64_t)p.Hkv * (seq_lens ? seq_lens[b0 + b] : p.tk);
+            const hipError_t e = launch_splitk(c, keys, max_len, workspace, stream,
+                                               seq_lens ? seq_lens + b0 : nullptr, counters);
+            if (e != hipSuccess) return e;
+        }
+        return hipSuccess;
+    }
+    // More query rows per KV head than one tile holds: one launch per range
+    // of rows.  A decode step appends in the first; the later launches read
+    // the stored row from the cache (lens has advanced by then).
+    const int rows = p.G * p.Tq, rpl = splitk_rows_per_launch(p.d);
+    for (int r0 = 0; r0 < rows; r0 += rpl) {
+        SplitKParams c = p;
+        c.row0 = r0;
+        c.R = std::min(rpl, rows - r0);
+        if (r0 > 0 && p.k_new) {
+            c.k_new = nullptr;
+            c.v_new = nullptr;
+            c.lens_w = nullptr;
+        }
+        const hipError_t e = launch_one(c, total_keys, max_len, workspace, stream, seq_lens, counters);
+        if (e != hipSuccess) return e;
+    }
+    return hipSuccess;
 }
 
 hipError_t zero_counters(uint32_t* counters, int64_t n, hipStream_t stream) {

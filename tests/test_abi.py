@@ -81,8 +81,8 @@ def test_decode_rejects_bad_geometry(nne):
     rc = lib.nne_decode_attention(FAKE, None, FAKE, FAKE, FAKE, lp, FAKE, None, 1, 4, 4, 8, 18,
                                   0, 0.0, None, None)
     assert rc == nne.NNE_EINVAL
-    # more than 16 query rows per KV head
-    rc = lib.nne_decode_attention(FAKE, None, FAKE, FAKE, FAKE, lp, FAKE, None, 1, 32, 1, 8, 16,
+    # head dim beyond 256
+    rc = lib.nne_decode_attention(FAKE, None, FAKE, FAKE, FAKE, lp, FAKE, None, 1, 4, 4, 8, 260,
                                   0, 0.0, None, None)
     assert rc == nne.NNE_EINVAL
     # length beyond capacity
@@ -95,9 +95,16 @@ def test_decode_rejects_bad_geometry(nne):
 def test_decode_workspace_size(nne):
     lib = nne.lib()
     assert lib.nne_decode_workspace_bytes(1, 4, 3, 64, 100) == 0   # 3 does not divide 4
-    assert lib.nne_decode_workspace_bytes(1, 4, 4, 256, 100) == 0  # head dim > 128
+    assert lib.nne_decode_workspace_bytes(1, 4, 4, 260, 100) == 0  # head dim > 256
     assert lib.nne_decode_workspace_bytes(1, 4, 4, 30, 100) == 0   # head dim not a multiple of 4
-    assert lib.nne_decode_workspace_bytes(1, 32, 1, 64, 100) == 0  # 32 rows per KV head > 16
+    assert lib.nne_decode_workspace_bytes(1, 4, 4, 256, 100) > 0
+    # any group size: rows beyond one launch's 64 go in further launches that
+    # reuse the workspace, so 128 rows need what 64 need
+    g64 = lib.nne_decode_workspace_bytes(1, 64, 1, 64, 100)
+    assert g64 > 0 and lib.nne_decode_workspace_bytes(1, 128, 1, 64, 100) == g64
+    # batches beyond 2048 sequences run 2048 at a time
+    assert lib.nne_decode_workspace_bytes(5000, 8, 8, 64, 10) == \
+        lib.nne_decode_workspace_bytes(2048, 8, 8, 64, 10)
     small = lib.nne_decode_workspace_bytes(2, 4, 2, 64, 4160)
     big = lib.nne_decode_workspace_bytes(32, 32, 8, 128, 4160)
     assert 0 < small < big
