@@ -115,7 +115,10 @@ int nne_counters_init(uint32_t *counters, uint64_t n, void *stream);
  * has_scale = 0 means scale = 1/sqrt(d) (:50); block sizes are accepted and
  * only validated (they change the reference's rounding order, not the result).
  * Causal masking is top-left: key c is visible to query row r iff c <= r
- * (:113).  Rows that see no key are zero (:186-194).  `o` has Q's shape. */
+ * (:113).  Rows that see no key are zero (:186-194).  `o` has Q's shape.
+ * Head dims up to 256; above 128 the tensors must be 16-byte vector views
+ * (d % 4 == 0, unit dim stride, other strides multiples of 4, 16-byte
+ * aligned) -- NNE_EINVAL otherwise. */
 int nne_flash_attention_forward(const float *q, const int64_t q_shape[4], const int64_t q_strides[4],
                                 const float *k, const int64_t k_shape[4], const int64_t k_strides[4],
                                 const float *v, const int64_t v_shape[4], const int64_t v_strides[4],
@@ -190,7 +193,10 @@ int nne_decode_workspace_size(int64_t B, int64_t Hq, int64_t Hkv, int64_t d,
 
 /* Single-token decode attention over the cache: q [B, Hq, 1, d] attends to
  * the first lens[b] rows of its sequence, no mask (llama.rs:239-296 with
- * t = 1).  Ragged lengths are allowed; Hq / Hkv <= 16.  ws: the caller's
+ * t = 1).  Ragged lengths, any Hq / Hkv, any batch, head dims up to 256
+ * (multiples of 4).  With more than 4 query heads per KV head or d > 128, q
+ * must be a 16-byte vector view (strides multiples of 4, 16-byte aligned).
+ * ws: the caller's
  * workspace of at least nne_decode_workspace_size, or NULL for the library's
  * per-stream one. */
 int nne_decode_attention(const float *q, const int64_t q_strides[4], const float *k_cache,

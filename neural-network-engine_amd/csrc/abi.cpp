@@ -187,6 +187,12 @@ float softmax_scale(int has_scale, float scale, int64_t d) {
     return has_scale ? scale : 1.0f / std::sqrt((float)d);
 }
 
+// Query rows per launch when the split-K kernel serves a prefill of head
+// dim above 128: causal steps take the 16-row tile with per-row masks.
+int wide_rows_per_launch(int d, bool causal) {
+    return causal ? 16 : nne::splitk_rows_per_launch(d);
+}
+
 // Shared body of the two prefill entry points.  Shapes were validated.
 int run_attention(const float* q, const int64_t* qs_, const int64_t* qst, const float* k,
                   const int64_t* ks_, const int64_t* kst, const float* v, const int64_t* vst,
@@ -195,13 +201,20 @@ int run_attention(const float* q, const int64_t* qs_, const int64_t* qst, const 
     const int B = (int)qs_[0], Hq = (int)qs_[1], Tq = (int)qs_[2], d = (int)qs_[3];
     const int Hkv = (int)ks_[1], Tk = (int)ks_[2];
     if ((int64_t)B * Hq * Tq == 0 || d == 0) return NNE_OK;
-    if (nne::prefill_padded_dim(d) == 0)
-        return fail(NNE_EINVAL, "Invalid configuration or argument: head dim %d > 128 is not "
+    // Head dims above 128 run on the split-K kernel (d <= 256); the MFMA
+    // prefill kernel holds Q^T and O^T of up to 128 dims in registers.
+    const bool wide = nne::prefill_padded_dim(d) == 0;
+    if (wide && nne::splitk_padded_dim(d) == 0)
+        return fail(NNE_EINVAL, "Invalid configuration or argument: head dim %d > 256 is not "
                                 "supported by the gfx950 attention kernels", d);
     // Offsets beyond +-2^30 cannot change visibility for int32 lengths.
     const int qoff = (int)std::max<int64_t>(-(1 << 30), std::min<int64_t>(q_offset, 1 << 30));
     const bool vec = d % 4 == 0 && vec_view(q, qst) && vec_view(k, kst) && vec_view(v, vst) &&
                      vec_view(o, ost);
+    if (wide && !vec)
+        return fail(NNE_EINVAL, "Invalid configuration or argument: head dim %d > 128 needs a "
+                                "multiple of 4, unit dim strides, strides that are multiples of 4 "
+                                "and 16-byte aligned tensors", d);
     const int G = Hq / Hkv;
     const int64_t rows = (int64_t)G * Tq;
     // Few query rows per KV head (decode-like steps, cross-attention, a few
@@ -209,34 +222,56 @@ int run_attention(const float* q, const int64_t* qs_, const int64_t* qst, const 
     // only the first tk keys are visible to any row (the last row sees keys
     // <= qoff + Tq - 1), and rows see different prefixes of them when
     // qoff < tk - 1.
-    const int64_t tk = causal ? std::min<int64_t>(Tk, (int64_t)qoff + Tq) : Tk;
+    const int64_t tk = causal ? std::max<int64_t>(0, std::min<int64_t>(Tk, (int64_t)qoff + Tq)) : Tk;
     const bool masked = causal && (int64_t)qoff < tk - 1;
+    const bool fits32 = (int64_t)B * Hkv * Tk < INT32_MAX && (int64_t)Tk * kst[2] < INT32_MAX &&
+                        (int64_t)Tk * vst[2] < INT32_MAX;
+    if (wide && (!fits32 || rows > INT32_MAX))
+        return fail(NNE_EINVAL, "Invalid configuration or argument: head dim %d > 128 with %lld "
+                                "keys per call exceeds the split-K kernel's 2^31 limit", d,
+                    (long long)((int64_t)B * Hkv * Tk));
 
-    if (vec && rows <= nne::splitk_max_rows() && tk > 0 &&
-        B <= nne::splitk_max_seqs() && (int64_t)B * Hkv * tk < INT32_MAX &&
-        tk * kst[2] < INT32_MAX && tk * vst[2] < INT32_MAX) {
+    if (vec && fits32 && (wide || (rows <= nne::splitk_max_rows() && tk > 0))) {
         nne::SplitKParams p{};
         p.q = make_view(q, qst);
         p.k = k; p.v = v;
         p.ksb = kst[0]; p.ksh = kst[1]; p.kst = kst[2];
         p.vsb = vst[0]; p.vsh = vst[1]; p.vst = vst[2];
         p.lens = nullptr;
-        p.tk = (int)tk;
-        p.max_keys = (int)tk;
         p.o = make_out(o, ost);
         p.B = B; p.Hq = Hq; p.Hkv = Hkv; p.Tq = Tq; p.d = d;
         p.qscale = scale * nne::kLog2e;
-        p.masked = masked ? 1 : 0;
         p.q_off = qoff;
-        const nne::SplitKWorkspace w = nne::splitk_workspace_layout(B, Hkv, (int)rows, d);
+        const int rp = wide ? wide_rows_per_launch(d, causal) : (int)rows;
+        const nne::SplitKWorkspace w = nne::splitk_workspace_layout(
+            std::min(B, nne::splitk_max_seqs()), Hkv, (int)std::min<int64_t>(rows, rp), d);
         uint32_t* counters = nullptr;
         void* ws = nullptr;
-        const int rc = call_workspace(wsp, w.total_bytes, (int64_t)B * Hkv, stream, &ws, &counters,
-                                      "few-query attention");
+        const int rc = call_workspace(wsp, w.total_bytes,
+                                      (int64_t)std::min(B, nne::splitk_max_seqs()) * Hkv, stream,
+                                      &ws, &counters, "few-query attention");
         if (rc != NNE_OK) return rc;
-        hipError_t e = nne::launch_splitk(p, (int64_t)B * Hkv * tk, (int)tk, ws, stream, nullptr,
-                                          counters);
-        if (e != hipSuccess) return hip_fail(e, "split-K attention launch");
+        // One launch per range of rp rows, each over the keys its rows can see.
+        for (int64_t r0 = 0; r0 < rows; r0 += rp) {
+            const int R = (int)std::min<int64_t>(rp, rows - r0);
+            int64_t tkp = tk;
+            bool maskp = masked;
+            if (wide && causal) {
+                int tmin = Tq, tmax = -1;
+                for (int64_t rr = r0; rr < r0 + R; ++rr) {
+                    tmin = std::min(tmin, (int)(rr % Tq));
+                    tmax = std::max(tmax, (int)(rr % Tq));
+                }
+                tkp = std::max<int64_t>(0, std::min<int64_t>(Tk, (int64_t)qoff + tmax + 1));
+                maskp = (int64_t)qoff + tmin < tkp - 1;
+            }
+            p.tk = (int)tkp;
+            p.max_keys = (int)tkp;
+            p.masked = maskp ? 1 : 0;
+            hipError_t e = nne::launch_splitk(p, (int64_t)B * Hkv * tkp, (int)tkp, ws, stream,
+                                              nullptr, counters, (int)r0, R);
+            if (e != hipSuccess) return hip_fail(e, "split-K attention launch");
+        }
         return NNE_OK;
     }
 
@@ -272,15 +307,20 @@ nne_workspace_size_t attention_workspace(const int64_t* qs_, const int64_t* ks_,
     nne_workspace_size_t r{0, 0};
     const int B = (int)qs_[0], Hq = (int)qs_[1], Tq = (int)qs_[2], d = (int)qs_[3];
     const int Hkv = (int)ks_[1], Tk = (int)ks_[2];
-    if ((int64_t)B * Hq * Tq == 0 || d == 0 || Hkv == 0 || nne::prefill_padded_dim(d) == 0) return r;
+    if ((int64_t)B * Hq * Tq == 0 || d == 0 || Hkv == 0 || nne::splitk_padded_dim(d) == 0) return r;
+    const bool wide = nne::prefill_padded_dim(d) == 0;
     const int qoff = (int)std::max<int64_t>(-(1 << 30), std::min<int64_t>(q_offset, 1 << 30));
     const int64_t rows = (int64_t)(Hq / Hkv) * Tq;
     const int64_t tk = causal ? std::min<int64_t>(Tk, (int64_t)qoff + Tq) : Tk;
-    if (rows <= nne::splitk_max_rows() && tk > 0 && B <= nne::splitk_max_seqs() && d % 4 == 0) {
-        const nne::SplitKWorkspace w = nne::splitk_workspace_layout(B, Hkv, (int)rows, d);
+    if (d % 4 == 0 && (wide || (rows <= nne::splitk_max_rows() && tk > 0))) {
+        const int rp = wide ? wide_rows_per_launch(d, causal) : (int)rows;
+        const int Bl = std::min(B, nne::splitk_max_seqs());
+        const nne::SplitKWorkspace w =
+            nne::splitk_workspace_layout(Bl, Hkv, (int)std::min<int64_t>(rows, rp), d);
         r.records_bytes = w.total_bytes;
-        r.n_counters = (uint64_t)B * Hkv;
+        r.n_counters = (uint64_t)Bl * Hkv;
     }
+    if (wide) return r;
     nne::PrefillParams p{};
     p.B = B; p.Hq = Hq; p.Hkv = Hkv; p.Tq = Tq; p.Tk = Tk; p.d = d;
     p.q_offset = qoff;

@@ -51,8 +51,11 @@ SplitKWorkspace splitk_workspace_layout(int B, int Hkv, int R, int d);
 // one.
 // seq_lens (host) are this launch's key counts per sequence (including a
 // decode step's new row), or null when every sequence has p.tk keys.
+// row_begin / row_count restrict the launch to a range of each KV head's
+// G * Tq rows (row_count < 0: all of them).
 hipError_t launch_splitk(SplitKParams p, int64_t total_keys, int max_len, void* workspace,
-                         hipStream_t stream, const int32_t* seq_lens, uint32_t* counters);
+                         hipStream_t stream, const int32_t* seq_lens, uint32_t* counters,
+                         int row_begin = 0, int row_count = -1);
 
 // Zeroes n counters with a fill kernel on the stream.
 hipError_t zero_counters(uint32_t* counters, int64_t n, hipStream_t stream);

@@ -125,11 +125,12 @@ __device__ __forceinline__ int item_at(const PrefillParams& p, int j, int x, int
     return 1;
 }
 
-// Two workgroups per CU for the persistent schedule; the key-split variant
-// (small problems, one short chunk per workgroup) may take the whole register
-// file at d = 128 instead of spilling.
+// Two workgroups per CU for the persistent schedule.  At d = 128 the
+// key-split variant (small problems, one short chunk per workgroup) and the
+// scalar-load variant (views that are not 16-byte vectors) take the whole
+// register file instead of spilling.
 template <int D, bool CAUSAL, bool VEC, bool SPLIT>
-__global__ __launch_bounds__(256, (SPLIT && D >= 128) ? 1 : 2) void prefill_mfma_kernel(const PrefillParams p) {
+__global__ __launch_bounds__(256, (D >= 128 && (SPLIT || !VEC)) ? 1 : 2) void prefill_mfma_kernel(const PrefillParams p) {
     constexpr int KS = D + 4;          // K row stride in LDS (16-byte reads conflict-free)
     constexpr int VS = D + 8;          // V row stride in LDS (lane halves on disjoint banks)
     constexpr int STAGE = 32 * KS + 32 * VS;

@@ -1004,7 +1004,8 @@ hipError_t launch_one(SplitKParams p, int64_t total_keys, int max_len, void* wor
 }  // namespace
 
 hipError_t launch_splitk(SplitKParams p, int64_t total_keys, int max_len, void* workspace,
-                         hipStream_t stream, const int32_t* seq_lens, uint32_t* counters) {
+                         hipStream_t stream, const int32_t* seq_lens, uint32_t* counters,
+                         int row_begin, int row_count) {
     p.G = p.Hq / p.Hkv;
     // Batches beyond MAX_SEQS sequences: one launch per block of sequences,
     // in stream order, sharing the workspace and counters.
@@ -1025,7 +1026,8 @@ hipError_t launch_splitk(SplitKParams p, int64_t total_keys, int max_len, void* 
             int64_t keys = 0;
             for (int b = 0; b < c.B; ++b) keys += (int64_t)p.Hkv * (seq_lens ? seq_lens[b0 + b] : p.tk);
             const hipError_t e = launch_splitk(c, keys, max_len, workspace, stream,
-                                               seq_lens ? seq_lens + b0 : nullptr, counters);
+                                               seq_lens ? seq_lens + b0 : nullptr, counters,
+                                               row_begin, row_count);
             if (e != hipSuccess) return e;
         }
         return hipSuccess;
@@ -1033,12 +1035,13 @@ hipError_t launch_splitk(SplitKParams p, int64_t total_keys, int max_len, void* 
     // More query rows per KV head than one tile holds: one launch per range
     // of rows.  A decode step appends in the first; the later launches read
     // the stored row from the cache (lens has advanced by then).
-    const int rows = p.G * p.Tq, rpl = splitk_rows_per_launch(p.d);
-    for (int r0 = 0; r0 < rows; r0 += rpl) {
+    const int rows_end = row_count < 0 ? p.G * p.Tq : row_begin + row_count;
+    const int rpl = splitk_rows_per_launch(p.d);
+    for (int r0 = row_begin; r0 < rows_end; r0 += rpl) {
         SplitKParams c = p;
         c.row0 = r0;
-        c.R = std::min(rpl, rows - r0);
-        if (r0 > 0 && p.k_new) {
+        c.R = std::min(rpl, rows_end - r0);
+        if (r0 > row_begin && p.k_new) {
             c.k_new = nullptr;
             c.v_new = nullptr;
             c.lens_w = nullptr;

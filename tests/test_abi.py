@@ -53,11 +53,17 @@ def test_value_length_mismatch(nne):
 
 def test_head_dim_too_large_is_invalid_argument(nne):
     lib = nne.lib()
-    s = i64(1, 1, 4, 256)
+    s = i64(1, 1, 4, 260)
     rc = lib.nne_flash_attention_forward(FAKE, s, None, FAKE, s, None, FAKE, s, None, FAKE, None,
                                          0, 0, 0.0, 64, 64, None)
     assert rc == nne.NNE_EINVAL
-    assert "head dim" in lib.nne_last_error().decode()
+    assert "head dim 260 > 256" in lib.nne_last_error().decode()
+    # above 128 the split-K kernel serves the call: 16-byte vector rows only
+    s = i64(1, 1, 4, 130)
+    rc = lib.nne_flash_attention_forward(FAKE, s, None, FAKE, s, None, FAKE, s, None, FAKE, None,
+                                         0, 0, 0.0, 64, 64, None)
+    assert rc == nne.NNE_EINVAL
+    assert "multiple of 4" in lib.nne_last_error().decode()
 
 
 def test_kv_append_capacity_error_leaves_lengths(nne):

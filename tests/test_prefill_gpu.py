@@ -313,3 +313,28 @@ def test_stream_release_frees_and_reallocates(nne, cuda):
     s.synchronize()
     assert np.array_equal(host(a), host(b))
     T.assert_close(host(b), T.ref_flash(host(q), host(k), host(v), True), what="after release")
+
+
+@pytest.mark.parametrize("b,hq,hkv,tq,tk,d,causal,q_off", [
+    (1, 2, 2, 200, 200, 256, True, 0),      # flash causal, d = 256
+    (1, 1, 1, 300, 300, 256, False, 0),     # non-causal
+    (2, 4, 2, 70, 90, 192, True, 20),       # GQA, bottom-right offset, padded dim
+    (1, 3, 3, 33, 33, 160, True, 0),        # rows of one launch span two heads' positions
+    (2, 8, 2, 8, 500, 256, False, 0),       # few-query cross-attention, d = 256
+    (1, 2, 1, 40, 64, 256, True, -10),      # rows that see no key
+])
+def test_head_dims_above_128(nne, cuda, b, hq, hkv, tq, tk, d, causal, q_off):
+    """flash_attention_forward takes any head dim (flash_attention.rs:39-48):
+    d in (128, 256] runs on the split-K kernel, 16 causal (32 other) rows per
+    launch, each launch over the keys its rows can see."""
+    print("case wide head dim", b, hq, hkv, tq, tk, d, causal, q_off, flush=True)
+    s = 17 * tq + d
+    q, k, v = rnd(s, b, hq, tq, d), rnd(s + 1, b, hkv, tk, d), rnd(s + 2, b, hkv, tk, d)
+    got = host(nne.attention_forward(dev(q, cuda), dev(k, cuda), dev(v, cuda), causal,
+                                     q_offset=q_off))
+    r0 = max(0, -q_off) if causal else 0
+    assert not got[:, :, :r0].any()
+    ref = T.ref_standard(q[:, :, r0:], k, v, causal, start_pos=q_off + r0)
+    T.assert_close(got[:, :, r0:], ref, what="d=%d" % d)
+    if hq == hkv and tq == tk and q_off == 0:
+        T.assert_close(got, T.ref_flash(q, k, v, causal), what="d=%d flash" % d)
