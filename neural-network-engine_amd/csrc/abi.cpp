@@ -62,6 +62,8 @@ bool dims_ok(const int64_t* s) {
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
+int device_cus();   // CUs of the current device (cached per device)
+
 // Per-stream resources of the split-K kernel, one set per (device, stream) --
 // per calling thread for the per-thread default stream.  Launches on one
 // stream run in order, so they share the set:
@@ -283,8 +285,15 @@ int run_attention(const float* q, const int64_t* qs_, const int64_t* qst, const 
     p.B = B; p.Hq = Hq; p.Hkv = Hkv; p.Tq = Tq; p.Tk = Tk; p.d = d;
     p.q_offset = qoff;
     p.qscale = scale * nne::kLog2e;
-    // Problems too small to fill the device split their key range across
-    // workgroups, with partial records in the stream's workspace.
+    // Small problems: one workgroup per 16-row block, waves over its key
+    // tiles, merged in LDS.
+    if (nne::small_prefill_fits(p, vec, device_cus())) {
+        hipError_t e = nne::launch_small_prefill(p, causal, stream);
+        if (e != hipSuccess) return hip_fail(e, "small prefill launch");
+        return NNE_OK;
+    }
+    // Other problems too small to fill the device split their key range
+    // across workgroups, with partial records in the workspace.
     const nne::PrefillSplit plan = nne::prefill_split_plan(p, causal, vec);
     if (p.n_chunks > 1) {
         uint32_t* counters = nullptr;

@@ -30,6 +30,14 @@ struct PrefillSplit {
 };
 PrefillSplit prefill_split_plan(PrefillParams& p, bool causal, bool vec);
 
+// Prefill of a problem too small to fill the device (small.hip): one
+// workgroup per (sequence, query head, 16-row block), whose waves split the
+// block's key tiles and merge in LDS (no workspace).  small_prefill_fits says
+// whether the problem is one (16-byte vector views, d <= 128, at most one
+// workgroup per CU, at most two key tiles per wave).
+bool small_prefill_fits(const PrefillParams& p, bool vec, int cus);
+hipError_t launch_small_prefill(PrefillParams p, bool causal, hipStream_t stream);
+
 // Split-K workspace of one launch (at most splitk_max_seqs() sequences and
 // splitk_rows_per_launch() rows): per-sequence prefix (B+1 ints) and partial
 // records for up to (workgroups of a launch) + B*Hkv (workgroup, head) pairs.

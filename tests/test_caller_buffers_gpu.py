@@ -27,8 +27,8 @@ def test_every_entry_point_on_caller_buffers_allocates_nothing(nne, cuda):
     ws = nne.Workspace(cuda)
     got, ref = {}, {}
 
-    # prefill: key split (config 1), persistent (no workspace), few-query cross
-    q1, k1, v1 = (dev(rnd(900 + i, 1, 4, 256, 64)) for i in range(3))
+    # prefill: key split, persistent (no workspace), few-query cross
+    q1, k1, v1 = (dev(rnd(900 + i, 1, 4, 600, 64)) for i in range(3))
     q2, k2, v2 = dev(rnd(903, 2, 8, 300, 64)), dev(rnd(904, 2, 4, 300, 64)), dev(rnd(905, 2, 4, 300, 64))
     qx, kx, vx = dev(rnd(906, 2, 6, 8, 64)), dev(rnd(907, 2, 6, 500, 64)), dev(rnd(908, 2, 6, 500, 64))
     # decode prologue + step over a ragged cache
@@ -87,7 +87,7 @@ def test_library_workspace_is_reported_and_released(nne, cuda):
     until nne_stream_release."""
     import torch
     s = torch.cuda.Stream(device=cuda)
-    q, k, v = (torch.randn(1, 4, 256, 64, device=cuda) for _ in range(3))
+    q, k, v = (torch.randn(1, 4, 600, 64, device=cuda) for _ in range(3))   # key split
     torch.cuda.synchronize()
     with torch.cuda.stream(s):
         nne.flash_attention_forward(q, k, v, True, stream=s)

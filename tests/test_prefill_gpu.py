@@ -218,14 +218,15 @@ def test_few_query_causal_rows(nne, cuda, g, tq, tk, q_off, d):
 
 
 # Problems with fewer work items (4 row blocks of 32 rows) than CUs and at
-# least 4 key tiles split every item's key tiles into chunks, one workgroup
-# each; the last workgroup of an item merges the partial (max, sum, O)
-# records.  Cases: config 1 (4 and 8 one-tile chunks), one item of 16 chunks (cached
-# multi-token step), the 16-chunk cap with an odd number of records to fold,
-# GQA through strided [B, T, H, d] views on the scalar path, a negative
-# offset (rows without keys), a padded head dim.
+# least 4 key tiles, too long for the small prefill kernel, split every
+# item's key tiles into chunks, one workgroup each; the last workgroup of an
+# item merges the partial (max, sum, O) records.  Cases: 4 heads of 600
+# (chunks of 2 tiles), one item of 16 chunks (cached multi-token step), the
+# 16-chunk cap with an odd number of records to fold, GQA through strided
+# [B, T, H, d] views on the scalar path, a negative offset (rows without
+# keys), a padded head dim.
 @pytest.mark.parametrize("b,hq,hkv,tq,tk,d,causal,q_off,strided", [
-    (1, 4, 4, 256, 256, 64, True, 0, False),
+    (1, 4, 4, 600, 600, 64, True, 0, False),
     (1, 2, 1, 9, 1000, 128, True, 991, False),
     (1, 1, 1, 32, 4096, 64, False, 0, False),
     (2, 8, 2, 160, 700, 32, True, 540, True),
@@ -254,7 +255,7 @@ def test_key_split_workspace_reuse_is_deterministic(nne, cuda):
     """Back-to-back split launches of different shapes share the stream's
     workspace and arrival counters; every call leaves the counters at zero,
     so repeating a call reproduces its output bit for bit."""
-    qa, ka, va = (dev(rnd(90 + i, 1, 4, 256, 64), cuda) for i in range(3))
+    qa, ka, va = (dev(rnd(90 + i, 1, 4, 600, 64), cuda) for i in range(3))
     qb = dev(rnd(93, 1, 2, 9, 128), cuda)
     kb, vb = (dev(rnd(94 + i, 1, 1, 1000, 128), cuda) for i in range(2))
     first = host(nne.attention_forward(qa, ka, va, True))
@@ -302,7 +303,7 @@ def test_stream_release_frees_and_reallocates(nne, cuda):
     call on the stream allocates them again and gives the same result."""
     import torch
     s = torch.cuda.Stream(device=cuda)
-    q, k, v = (dev(rnd(400 + i, 1, 4, 256, 64), cuda) for i in range(3))   # key-split path
+    q, k, v = (dev(rnd(400 + i, 1, 4, 600, 64), cuda) for i in range(3))   # key-split path
     torch.cuda.synchronize()
     with torch.cuda.stream(s):
         a = nne.attention_forward(q, k, v, True, stream=s)
@@ -338,3 +339,34 @@ def test_head_dims_above_128(nne, cuda, b, hq, hkv, tq, tk, d, causal, q_off):
     T.assert_close(got[:, :, r0:], ref, what="d=%d" % d)
     if hq == hkv and tq == tk and q_off == 0:
         T.assert_close(got, T.ref_flash(q, k, v, causal), what="d=%d flash" % d)
+
+
+# Problems of at most one workgroup per CU (one per sequence, query head and
+# 16-row block) with at most two 16-key tiles per wave run on the small
+# prefill kernel: the waves of a workgroup take one row block's key tiles and
+# merge in LDS.  Row counts that are not multiples of 16, GQA, offsets of both
+# signs (rows that see no key), Tk < Tq and Tk > Tq, padded head dims.
+@pytest.mark.parametrize("b,hq,hkv,tq,tk,d,causal,q_off", [
+    (1, 4, 4, 256, 256, 64, True, 0),      # config 1
+    (2, 6, 2, 37, 37, 64, True, 0),
+    (1, 8, 1, 100, 300, 32, True, 200),
+    (1, 2, 2, 90, 60, 48, True, -20),
+    (1, 3, 3, 70, 450, 64, False, 0),
+    (2, 4, 4, 64, 64, 128, True, 0),
+    (1, 2, 1, 130, 250, 96, False, 0),
+    (1, 5, 5, 17, 200, 128, True, 183),
+])
+def test_small_prefill_kernel_shapes(nne, cuda, b, hq, hkv, tq, tk, d, causal, q_off):
+    print("case small prefill", b, hq, hkv, tq, tk, d, causal, q_off, flush=True)
+    s = 53 * tq + tk + d
+    q, k, v = rnd(s, b, hq, tq, d), rnd(s + 1, b, hkv, tk, d), rnd(s + 2, b, hkv, tk, d)
+    got = host(nne.attention_forward(dev(q, cuda), dev(k, cuda), dev(v, cuda), causal,
+                                     q_offset=q_off))
+    r0 = max(0, -q_off) if causal else 0
+    assert not got[:, :, :r0].any()
+    ref = T.ref_standard(q[:, :, r0:], k, v, causal, start_pos=q_off + r0)
+    T.assert_close(got[:, :, r0:], ref, what="small prefill")
+    # the same call again gives the same bits (no state between calls)
+    again = host(nne.attention_forward(dev(q, cuda), dev(k, cuda), dev(v, cuda), causal,
+                                       q_offset=q_off))
+    assert np.array_equal(again, got)

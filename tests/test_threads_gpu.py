@@ -21,11 +21,12 @@ import nne_testlib as T
 
 pytestmark = pytest.mark.gpu
 
-# (b, hq, hkv, tq, tk, d, causal, q_off): small-problem key split (config 1),
-# few-query split-K with the causal row mask, a cached 9-token GQA step (key
-# split, 16 chunks), and a larger key split that needs a bigger workspace.
+# (b, hq, hkv, tq, tk, d, causal, q_off): small-problem key split (4 heads
+# of 600), few-query split-K with the causal row mask, a cached 9-token GQA
+# step (key split, 16 chunks), and a larger key split that needs a bigger
+# workspace.
 CASES = [
-    (1, 4, 4, 256, 256, 64, True, 0),
+    (1, 4, 4, 600, 600, 64, True, 0),
     (2, 8, 2, 4, 1000, 128, True, 996),
     (1, 12, 3, 9, 1000, 64, True, 991),
     (1, 12, 12, 1024, 1024, 64, True, 0),
