@@ -12,10 +12,9 @@
 // MI355X mapping.  A small problem's time is a chain of latencies, not
 // arithmetic: a launch, the first loads, the tiles one wave must run in
 // sequence, and any hand-off between workgroups.  Here the waves of one
-// workgroup take the tiles of one row block side by side (up to 16 waves,
-// 4 per SIMD, at d <= 64; 8 at d = 128), so the heaviest causal block of a
-// T = 256 head runs one tile per wave, and the partial results never leave
-// the CU: no global records, no arrival counters, no second round trip.
+// workgroup take the tiles of one row block side by side (8 waves, at most
+// two tiles each, loaded at once), and the partial results never leave the
+// CU: no global records, no arrival counters, no second round trip.
 // Per tile, on v_mfma_f32_16x16x4_f32 (the layout of the split-K kernel's
 // 16-row tile):
 //   S^T = K Q^T  (Q^T in registers, pre-scaled by scale * log2(e); K staged
@@ -59,10 +58,17 @@ __device__ __forceinline__ void wave_lds_fence() {
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
-// Waves per workgroup: 4 per SIMD at d <= 64 (<= 128 registers each), 2 at
-// d = 128.
+// Waves per workgroup; each takes at most two tiles, both loaded at once.
+// Measured at config 1 (B=1, H=4, T=256, d=64, causal), queued calls on
+// MI355X: 16 waves of one tile each 7.0 us, 8 waves of two tiles 6.5 us --
+// the LDS merge of twice as many partial O cost more than the second tile.
+// The heaviest causal block (16 tiles) keeps its CU's four MFMA pipes busy
+// for ~1.7 us; with the ~1.6 us launch and ~1.5 us first loads that is most
+// of the call.
+constexpr int SMALL_WAVES = 8;
+constexpr int SMALL_TILES_PER_WAVE = 2;
 template <int D>
-constexpr int small_waves() { return D <= 64 ? 16 : 8; }
+constexpr int small_waves() { return SMALL_WAVES; }
 
 template <int D, bool CAUSAL>
 __global__ __launch_bounds__(64 * small_waves<D>(), 1) void small_prefill_kernel(const PrefillParams p) {
@@ -78,16 +84,24 @@ __global__ __launch_bounds__(64 * small_waves<D>(), 1) void small_prefill_kernel
 
     // K slices of the waves during the tile loop, then the waves' partial O.
     __shared__ __attribute__((aligned(16))) float lds[NW * SKB * KS];
+    __shared__ __attribute__((aligned(16))) float q_s[SKB * KS];   // the block's Q rows
     __shared__ float ml_s[NW][SKB][2];
+    __shared__ float wgt_s[NW][SKB];     // merge weight of wave w for row r
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int col = lane & 15, grp = lane >> 4;
 
-    // Workgroup -> (sequence, query head, row block); in causal problems the
-    // blocks with the most keys go first.
+    // Workgroup -> (sequence, query head, row block).  The hardware deals
+    // consecutive workgroup ids to the 8 XCDs in turn; XCD x takes the x-th
+    // eighth of the block list, so the blocks of one head -- which read the
+    // same K/V tiles -- share an L2.  In causal problems the blocks with the
+    // most keys come first.
     const int n_rb = (p.Tq + SKB - 1) / SKB;
-    const int idx = blockIdx.x;
+    const int n_items = p.B * p.Hq * n_rb;
+    const int per_xcd = (n_items + 7) >> 3;
+    const int idx = (blockIdx.x & 7) * per_xcd + (blockIdx.x >> 3);
+    if (idx >= n_items) return;          // whole workgroup: no barrier is skipped
     const int rb_i = idx % n_rb, bh = idx / n_rb;
     const int rb = CAUSAL ? n_rb - 1 - rb_i : rb_i;
     const int bi = bh / p.Hq, hq = bh % p.Hq, kvh = hq / p.G;
@@ -98,22 +112,6 @@ __global__ __launch_bounds__(64 * small_waves<D>(), 1) void small_prefill_kernel
     if (CAUSAL) n_keys = min(p.Tk, min(p.Tq - 1, r0 + SKB - 1) + p.q_offset + 1);
     const int n_tiles = n_keys > 0 ? (n_keys + SKB - 1) / SKB : 0;
 
-    // Q^T fragment: lane holds row `col`, dims grp*NQ .. +NQ, pre-scaled.
-    float qf[NQ];
-    {
-        const bool rok = row < p.Tq;
-        const float* qp = p.q.p + bi * p.q.sb + hq * p.q.sh + (int64_t)(rok ? row : 0) * p.q.st;
-#pragma unroll
-        for (int s4 = 0; s4 < NQ / 4; ++s4) {
-            const int c = grp * NQ + 4 * s4;
-            const vf4 x = *reinterpret_cast<const vf4*>(qp + min(c, p.d - 4));
-            const bool ok = rok && c < p.d;
-            qf[4 * s4 + 0] = ok ? x.x * p.qscale : 0.f;
-            qf[4 * s4 + 1] = ok ? x.y * p.qscale : 0.f;
-            qf[4 * s4 + 2] = ok ? x.z * p.qscale : 0.f;
-            qf[4 * s4 + 3] = ok ? x.w * p.qscale : 0.f;
-        }
-    }
     const float* kb = p.k.p + bi * p.k.sb + kvh * p.k.sh;
     const float* vb = p.v.p + bi * p.v.sb + kvh * p.v.sh;
     const int kst = (int)p.k.st, vst = (int)p.v.st;
@@ -123,6 +121,49 @@ __global__ __launch_bounds__(64 * small_waves<D>(), 1) void small_prefill_kernel
     for (int h = 0; h < NH; ++h) v_col[h] = min(64 * h + 4 * col, p.d - 4);
     float* Kw = lds + wave * SKB * KS;
 
+    // The block's 16 Q rows, loaded once for all waves (scaled by
+    // scale * log2(e); rows past T_q and columns past d are zero).  Their
+    // loads go first, so staging them waits for nothing else.
+    static_assert(SKB * (D / 4) <= 64 * NW, "one Q vector per thread");
+    const int qe = tid, q_r = qe / (D / 4), q_c = 4 * (qe % (D / 4));
+    const bool q_ok = qe < SKB * (D / 4) && r0 + q_r < p.Tq && q_c < p.d;
+    vf4 qx = vf4{0.f, 0.f, 0.f, 0.f};
+    if (q_ok)
+        qx = *reinterpret_cast<const vf4*>(p.q.p + bi * p.q.sb + hq * p.q.sh +
+                                          (int64_t)(r0 + q_r) * p.q.st + q_c);
+    // Both tiles of this wave (wave and wave + NW) in flight at once.  Loads
+    // clamp to the last key (masked below) and to the row's last 4 floats
+    // past d (their Q columns are zero), so none is out of bounds.
+    vf4 kr[SMALL_TILES_PER_WAVE][NK], vr[SMALL_TILES_PER_WAVE][4 * NH];
+    auto load_tile = [&](vf4 (&kt)[NK], vf4 (&vt)[4 * NH], int kb0) __attribute__((always_inline)) {
+#pragma unroll
+        for (int i = 0; i < NK; ++i) {
+            const int key = min(kb0 + lane / LPR + RPI * i, n_keys - 1);
+            kt[i] = *reinterpret_cast<const vf4*>(kb + key * kst + kc_col);
+        }
+#pragma unroll
+        for (int st = 0; st < 4; ++st) {
+            const int key = min(kb0 + 4 * grp + st, n_keys - 1);
+#pragma unroll
+            for (int h = 0; h < NH; ++h)
+                vt[st * NH + h] = *reinterpret_cast<const vf4*>(vb + key * vst + v_col[h]);
+        }
+    };
+#pragma unroll
+    for (int j = 0; j < SMALL_TILES_PER_WAVE; ++j)
+        if (wave + j * NW < n_tiles) load_tile(kr[j], vr[j], (wave + j * NW) * SKB);
+    if (qe < SKB * (D / 4)) *reinterpret_cast<vf4*>(q_s + q_r * KS + q_c) = qx * p.qscale;
+    __syncthreads();
+    float qf[NQ];
+#pragma unroll
+    for (int s4 = 0; s4 < NQ / 4; ++s4) {
+        const vf4 x = *reinterpret_cast<const vf4*>(q_s + col * KS + grp * NQ + 4 * s4);
+        qf[4 * s4 + 0] = x.x;
+        qf[4 * s4 + 1] = x.y;
+        qf[4 * s4 + 2] = x.z;
+        qf[4 * s4 + 3] = x.w;
+    }
+
     floatx4 o[NB];
 #pragma unroll
     for (int b = 0; b < NB; ++b) o[b] = floatx4{0.f, 0.f, 0.f, 0.f};
@@ -130,27 +171,15 @@ __global__ __launch_bounds__(64 * small_waves<D>(), 1) void small_prefill_kernel
     // last key this lane's row may see (tile masks only where a tile reaches past it)
     const int row_last = CAUSAL ? row + p.q_offset : p.Tk - 1;
 
-    for (int t = wave; t < n_tiles; t += NW) {
+#pragma unroll
+    for (int j = 0; j < SMALL_TILES_PER_WAVE; ++j) {
+        const int t = wave + j * NW;
+        if (t >= n_tiles) break;         // wave-uniform
         const int kb0 = t * SKB;
-        vf4 kr[NK], vr[4 * NH];
-        // Loads clamp to the last key (masked below) and to the row's last 4
-        // floats past d (their Q columns are zero), so none is out of bounds.
-#pragma unroll
-        for (int i = 0; i < NK; ++i) {
-            const int key = min(kb0 + lane / LPR + RPI * i, n_keys - 1);
-            kr[i] = *reinterpret_cast<const vf4*>(kb + key * kst + kc_col);
-        }
-#pragma unroll
-        for (int st = 0; st < 4; ++st) {
-            const int key = min(kb0 + 4 * grp + st, n_keys - 1);
-#pragma unroll
-            for (int h = 0; h < NH; ++h)
-                vr[st * NH + h] = *reinterpret_cast<const vf4*>(vb + key * vst + v_col[h]);
-        }
         wave_lds_fence();
 #pragma unroll
         for (int i = 0; i < NK; ++i)
-            *reinterpret_cast<vf4*>(Kw + (lane / LPR + RPI * i) * KS + 4 * (lane % LPR)) = kr[i];
+            *reinterpret_cast<vf4*>(Kw + (lane / LPR + RPI * i) * KS + 4 * (lane % LPR)) = kr[j][i];
         wave_lds_fence();
 
         // S^T = K Q^T: s[r] = score of key kb0 + 4*grp + r for row `col`.
@@ -192,7 +221,7 @@ __global__ __launch_bounds__(64 * small_waves<D>(), 1) void small_prefill_kernel
         for (int st = 0; st < 4; ++st)
 #pragma unroll
             for (int h = 0; h < NH; ++h) {
-                const vf4 vv = vr[st * NH + h];
+                const vf4 vv = vr[j][st * NH + h];
                 o[4 * h + 0] = __builtin_amdgcn_mfma_f32_16x16x4f32(vv.x, s[st], o[4 * h + 0], 0, 0, 0);
                 o[4 * h + 1] = __builtin_amdgcn_mfma_f32_16x16x4f32(vv.y, s[st], o[4 * h + 1], 0, 0, 0);
                 o[4 * h + 2] = __builtin_amdgcn_mfma_f32_16x16x4f32(vv.z, s[st], o[4 * h + 2], 0, 0, 0);
@@ -216,27 +245,40 @@ __global__ __launch_bounds__(64 * small_waves<D>(), 1) void small_prefill_kernel
         ml_s[wave][col][1] = l_tot;
     }
     __syncthreads();
+    // Weight of wave w for row r: 2^(m_w - M) / sum_w' 2^(m_w' - M) l_w'
+    // (0 for waves without a tile, and for rows that saw no key), computed
+    // once per (row, wave) by NW-lane groups, in a fixed order.
     const int n_active = min(NW, n_tiles);   // waves that ran a tile
-    for (int e = tid; e < SKB * D; e += 64 * NW) {
-        const int rr = e / D, dd = e % D;
-        if (r0 + rr >= p.Tq || dd >= p.d) continue;
-        float M = kNegInf;
-        for (int w = 0; w < n_active; ++w) M = fmaxf(M, ml_s[w][rr][0]);
-        const float M_use = M == kNegInf ? 0.f : M;
-        float l = 0.f, acc = 0.f;
-        for (int w = 0; w < n_active; ++w) {
-            const float f = fast_exp2(ml_s[w][rr][0] - M_use);
-            l += f * ml_s[w][rr][1];
-            acc += f * ob[(w * SKB + rr) * KS + dd];
-        }
-        p.o.p[bi * p.o.sb + hq * p.o.sh + (int64_t)(r0 + rr) * p.o.st + dd] = l > 0.f ? acc / l : 0.f;
+    if (tid < SKB * NW) {
+        const int rr = tid / NW, w = tid % NW;
+        const float m = w < n_active ? ml_s[w][rr][0] : kNegInf;
+        float M = m;
+#pragma unroll
+        for (int off = 1; off < NW; off <<= 1) M = fmaxf(M, __shfl_xor(M, off, NW));
+        const float f = w < n_active ? fast_exp2(m - (M == kNegInf ? 0.f : M)) : 0.f;
+        float L = f * (w < n_active ? ml_s[w][rr][1] : 0.f);
+#pragma unroll
+        for (int off = 1; off < NW; off <<= 1) L += __shfl_xor(L, off, NW);
+        wgt_s[w][rr] = L > 0.f ? f / L : 0.f;
+    }
+    __syncthreads();
+    // 16-byte output vectors (d % 4 == 0 and 16-byte views on this path).
+    for (int e = tid; e < SKB * (D / 4); e += 64 * NW) {
+        const int rr = e / (D / 4), c = 4 * (e % (D / 4));
+        vf4 acc = vf4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int w = 0; w < NW; ++w)
+            acc += wgt_s[w][rr] * *reinterpret_cast<const vf4*>(ob + (w * SKB + rr) * KS + c);
+        if (r0 + rr < p.Tq && c < p.d)
+            *reinterpret_cast<vf4*>(p.o.p + bi * p.o.sb + hq * p.o.sh + (int64_t)(r0 + rr) * p.o.st + c) = acc;
     }
 }
 
 template <int D>
 hipError_t launch_small_d(const PrefillParams& p, bool causal, hipStream_t stream) {
     const int n_rb = (p.Tq + SKB - 1) / SKB;
-    const dim3 grid((unsigned)(p.B * p.Hq * n_rb)), block(64 * small_waves<D>());
+    const int n_items = p.B * p.Hq * n_rb;
+    const dim3 grid((unsigned)(8 * ((n_items + 7) / 8))), block(64 * small_waves<D>());
     if (causal)
         hipLaunchKernelGGL((small_prefill_kernel<D, true>), grid, block, 0, stream, p);
     else
@@ -253,8 +295,7 @@ bool small_prefill_fits(const PrefillParams& p, bool vec, int cus) {
     const int64_t wgs = (int64_t)p.B * p.Hq * ((p.Tq + SKB - 1) / SKB);
     // Tiles of the heaviest row block: at most two per wave.
     const int64_t tiles = ((int64_t)p.Tk + SKB - 1) / SKB;
-    const int nw = p.d <= 64 ? small_waves<64>() : small_waves<128>();
-    return wgs > 0 && wgs <= cus && tiles <= 2 * nw;
+    return wgs > 0 && wgs <= cus && tiles <= SMALL_TILES_PER_WAVE * SMALL_WAVES;
 }
 
 hipError_t launch_small_prefill(PrefillParams p, bool causal, hipStream_t stream) {
