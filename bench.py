@@ -152,10 +152,15 @@ def time_prefill(nne, torch, q, k, v, causal, steps, warmup, out, q_offset=0):
     return wall * 1e3 / steps, kernel_ms
 
 
-def bench_decode(nne, torch, dev, steps=64, warmup=4, seed=0x5EED0003):
-    """Config 3: B=32, Hq=32, Hkv=8, d=128, ragged lengths, 64 append+attend steps."""
+def bench_decode(nne, torch, dev, steps=64, warmup=4, seed=0x5EED0003, hq=32, hkv=8,
+                 workload="config3: decode B=32 Hq=32 Hkv=8 d=128 "
+                          "L0~U[512,4096] ragged, 64 steps append+attend, f32",
+                 traffic=None):
+    """Config 3: B=32, Hq=32, Hkv=8, d=128, ragged lengths, 64 append+attend
+    steps.  hq/hkv give other group sizes on the same lengths (Hq=64, Hkv=8 is
+    LLaMA-2-70B's grouping: 8 query rows per KV head)."""
     import numpy as np
-    b, hq, hkv, d = 32, 32, 8, 128
+    b, d = 32, 128
     rng = np.random.default_rng(seed)
     lens0 = rng.integers(512, 4097, size=b).astype(np.int32)
     cap = 4096 + steps + warmup
@@ -188,9 +193,8 @@ def bench_decode(nne, torch, dev, steps=64, warmup=4, seed=0x5EED0003):
             "bytes_per_step": round(total / steps),
             "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS,
                          "unit": "GB/s", "frac": round(gbs / PEAK_HBM_GBS, 4),
-                         "traffic": TRAFFIC_DECODE_CONFIG3_STEP},
-            "config": {"workload": "config3: decode B=32 Hq=32 Hkv=8 d=128 "
-                                   "L0~U[512,4096] ragged, 64 steps append+attend, f32"}}
+                         "traffic": traffic},
+            "config": {"workload": workload}}
 
 
 def cpu_baseline(target_seconds=15.0):
@@ -569,7 +573,7 @@ def main():
     cpu_jobs = []
     if not args.no_decode:
         print("bench: config3 decode", file=sys.stderr, flush=True)
-        line["decode"] = bench_decode(nne, torch, dev)
+        line["decode"] = bench_decode(nne, torch, dev, traffic=TRAFFIC_DECODE_CONFIG3_STEP)
         if not args.no_cpu:
             cpu_jobs.append((line["decode"], decode_cpu_baseline))
     if not args.headline:
@@ -647,6 +651,15 @@ def main():
                     cpu_jobs.append((extra[-1], cross_cpu_baseline))
                 del kvs
             del q, k, v, o
+        print("bench: G=8 decode", file=sys.stderr, flush=True)
+        rec = bench_decode(nne, torch, dev, hq=64, seed=0x5EED0016,
+                           workload="G=8 decode (LLaMA-2-70B grouping): B=32 Hq=64 Hkv=8 d=128 "
+                                    "L0~U[512,4096] ragged, 64 steps append+attend, f32")
+        rec["workload"] = rec["config"]["workload"]
+        extra.append(rec)
+        if not args.no_cpu:
+            cpu_jobs.append((rec, lambda: decode_cpu_baseline(
+                seed=0x5EED0016, shape=(32, 64, 8, 128), label="G=8 decode step")))
         print("bench: config3 decode layer step", file=sys.stderr, flush=True)
         extra.append(bench_decode_layer(nne, torch, dev))
         if not args.no_cpu:

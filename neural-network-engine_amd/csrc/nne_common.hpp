@@ -163,6 +163,15 @@ __device__ __forceinline__ void store_coherent(float* p, float x) {
 __device__ __forceinline__ float load_coherent(const float* p) {
     return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
+// 16-byte form of load_coherent: a buffer load with the same sc1 policy
+// (buffer_load_dwordx4 ... sc1) from a range of `bytes` bytes at `base`
+// (offsets past the range read as zero).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t coherent_range(const float* base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(base), 0, bytes, 0x00020000);
+}
+__device__ __forceinline__ vf4 load_coherent4(__amdgpu_buffer_rsrc_t range, uint32_t byte_offset) {
+    return __builtin_bit_cast(vf4, __builtin_amdgcn_raw_buffer_load_b128(range, byte_offset, 0, 16));
+}
 __device__ __forceinline__ void wait_stores_performed() {
     __atomic_signal_fence(__ATOMIC_SEQ_CST);
     __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0), expcnt/lgkmcnt unconstrained

@@ -105,6 +105,23 @@ __global__ __launch_bounds__(256, 2) void qkv_rope_kernel(const QkvParams p) {
     const int j1 = min(n_chunks, j0 + p.kc_per_slice);
     const int nj = j1 - j0;
 
+    // The tile belongs to one head of q, k or v.  Thread tid finishes column
+    // tid % 64 of rows tid / 64 + 4 k if its workgroup adds the tile up; the
+    // positions and biases it needs are loaded behind the first chunks, off
+    // the launch's tail.
+    const int tiles_per_head = p.d / 64, half = p.d / 2;
+    const int hh = tile / tiles_per_head, u = tile % tiles_per_head;
+    const int which = hh < p.Hq ? 0 : (hh < p.Hq + p.Hkv ? 1 : 2);
+    const int head = which == 0 ? hh : (which == 1 ? hh - p.Hq : hh - p.Hq - p.Hkv);
+    const float* bias = p.bias[which];
+    const int ocol = tid & 63, orow = tid >> 6;
+    const int dim = tile_dim(ocol, u, half);
+    const int pcol = ocol ^ 32;   // columns c and c ^ 32 hold dims i and i + d/2 of one pair
+    const bool rotate = which < 2 && p.cos;
+    float b_own = 0.f, b_partner = 0.f;
+    constexpr int ROWS = 4 * MT;   // rows per thread
+    int pos[ROWS];
+
     // This wave's packed weights: 4 KB per chunk, 1 KB per load instruction.
     const vf4* wsrc = reinterpret_cast<const vf4*>(p.wp) +
                       ((int64_t)(tile * n_chunks + j0) * 4 + wave) * 256 + lane;
@@ -166,6 +183,12 @@ __global__ __launch_bounds__(256, 2) void qkv_rope_kernel(const QkvParams p) {
         load_x(xr[2], j0 + cl(2));
         store_x(xr[0], 0);
     }
+#pragma unroll
+    for (int k = 0; k < ROWS; ++k) pos[k] = rotate && orow + 4 * k < p.M ? p.pos[orow + 4 * k] : 0;
+    if (bias) {
+        b_own = bias[head * p.d + dim];
+        b_partner = bias[head * p.d + tile_dim(pcol, u, half)];
+    }
     __syncthreads();
     auto step = [&](int jj, auto ji) __attribute__((always_inline)) {
         constexpr int J = decltype(ji)::value;   // jj % 6
@@ -208,31 +231,54 @@ __global__ __launch_bounds__(256, 2) void qkv_rope_kernel(const QkvParams p) {
         }
         __syncthreads();
         if (!is_last) return;
-        // Last slice of the tile: add the partials in slice order.  All loads
-        // of a round are issued before the first add (one round trip per
-        // round, not one per slice).
-        const float* base = p.ws + (int64_t)tile * p.S * 64 * 64;
-        const int n_el = 64 * p.M;
-        for (int e0 = 0; e0 < n_el; e0 += 4 * 256) {
-            float v[4][QKV_MAX_S];
+    }
+
+    // RoPE table entries of this thread's outputs, loaded before the partial
+    // tiles so both round trips overlap.
+    float* out = p.out[which];
+    const int64_t osb = p.o_sb[which], osh = p.o_sh[which];
+    float cs[ROWS], sn[ROWS];
+    if (rotate) {
 #pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                const int e = e0 + tid + 256 * q;
-                const int col = e / p.M, m = e % p.M;
+        for (int k = 0; k < ROWS; ++k) {
+            if (orow + 4 * k < p.M) {
+                const int64_t tb = (int64_t)pos[k] * p.d + dim;
+                cs[k] = p.cos[tb];
+                sn[k] = p.sin[tb];
+            }
+        }
+    }
+
+    if (p.S > 1) {
+        // Last slice of the tile: add the partials in slice order.  A thread
+        // adds 4 rows of a column with 16-byte loads, every slice's loads of a
+        // round issued before the first add.
+        const float* base = p.ws + (int64_t)tile * p.S * 64 * 64;
+        const __amdgpu_buffer_rsrc_t range = coherent_range(base, (uint32_t)p.S * 64 * 64 * 4);
+        const int rg = (p.M + 3) >> 2, n_g = 64 * rg;
+        for (int g0 = 0; g0 < n_g; g0 += 2 * 256) {
+            vf4 v[2][QKV_MAX_S];
+#pragma unroll
+            for (int q = 0; q < 2; ++q) {
+                const int g = g0 + tid + 256 * q;
+                const int col = g / rg, rq = g % rg;
 #pragma unroll
                 for (int sl = 0; sl < QKV_MAX_S; ++sl)
-                    v[q][sl] = (e < n_el && sl < p.S)
-                                   ? load_coherent(base + ((int64_t)sl * 64 + col) * 64 + m) : 0.f;
+                    v[q][sl] = (g < n_g && sl < p.S)
+                                   ? load_coherent4(range, (uint32_t)(((sl * 64 + col) * 64 + 4 * rq) * 4))
+                                   : vf4{0.f, 0.f, 0.f, 0.f};
             }
 #pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                const int e = e0 + tid + 256 * q;
-                if (e >= n_el) continue;
-                float sum = v[q][0];
+            for (int q = 0; q < 2; ++q) {
+                const int g = g0 + tid + 256 * q;
+                if (g >= n_g) continue;
+                vf4 sum = v[q][0];
 #pragma unroll
                 for (int sl = 1; sl < QKV_MAX_S; ++sl)
                     if (sl < p.S) sum = sum + v[q][sl];
-                fin[e / p.M][e % p.M] = sum;
+                const int col = g / rg, rq = g % rg;
+#pragma unroll
+                for (int i = 0; i < 4; ++i) fin[col][4 * rq + i] = sum[i];
             }
         }
         if (tid == 0)
@@ -245,28 +291,18 @@ __global__ __launch_bounds__(256, 2) void qkv_rope_kernel(const QkvParams p) {
     }
     __syncthreads();
 
-    // Bias, RoPE, store.  The tile belongs to one head of q, k or v.
-    const int tiles_per_head = p.d / 64, half = p.d / 2;
-    const int hh = tile / tiles_per_head, u = tile % tiles_per_head;
-    const int which = hh < p.Hq ? 0 : (hh < p.Hq + p.Hkv ? 1 : 2);
-    const int head = which == 0 ? hh : (which == 1 ? hh - p.Hq : hh - p.Hq - p.Hkv);
-    const float* bias = p.bias[which];
-    float* out = p.out[which];
-    const int64_t osb = p.o_sb[which], osh = p.o_sh[which];
-    for (int e = tid; e < 64 * p.M; e += 256) {
-        const int col = e % 64, m = e / 64;
-        const int dim = tile_dim(col, u, half);
-        float val = fin[col][m];
-        if (bias) val = val + bias[head * p.d + dim];
-        if (which < 2 && p.cos) {
-            // rotate_half(x) = [-x2, x1] (llama.rs:149-152): columns col and
-            // col ^ 32 hold dims i and i + d/2 of one pair.
-            const int pc = col ^ 32;
-            float partner = fin[pc][m];
-            if (bias) partner = partner + bias[head * p.d + tile_dim(pc, u, half)];
-            const float rot = col < 32 ? -partner : partner;
-            const int64_t tb = (int64_t)p.pos[m] * p.d + dim;
-            val = rope_rotate(val, p.cos[tb], rot, p.sin[tb]);
+    // Bias, RoPE (rotate_half(x) = [-x2, x1], llama.rs:149-152), store.
+#pragma unroll
+    for (int k = 0; k < ROWS; ++k) {
+        const int m = orow + 4 * k;
+        if (m >= p.M) break;
+        float val = fin[ocol][m];
+        if (bias) val = val + b_own;
+        if (rotate) {
+            float partner = fin[pcol][m];
+            if (bias) partner = partner + b_partner;
+            const float rot = ocol < 32 ? -partner : partner;
+            val = rope_rotate(val, cs[k], rot, sn[k]);
         }
         out[m * osb + head * osh + dim] = val;
     }
