@@ -105,6 +105,7 @@ struct QkvParams {
 // (row0+rr) % Tq.  Every row sees every key of its sequence.
 // Sequences whose flattened prefix travels in the kernel arguments.
 constexpr int kArgSeqs = 128;
+constexpr int kMaxPackWg = 512;   // workgroups of a whole-head packed launch
 
 struct SplitKParams {
     View4 q;
@@ -123,6 +124,7 @@ struct SplitKParams {
     int masked;
     int q_off;
     int n_wg;                // workgroups of the split kernel
+    int packed;              // whole-head packing (groups in pack_head, below)
     int chunk;               // flattened keys per workgroup
     // decode step only (k_new != null): the new row [B, Hkv, 1, d] is attended
     // as key lens[b] and stored into the cache; lens_w[b] is advanced.
@@ -145,7 +147,29 @@ struct SplitKParams {
     int32_t* ws_pref;        // [B+1] flattened start of each sequence (this launch)
     float* ws_ml;            // [slots][R][2] partial (max, sum); slot = workgroup + head
     float* ws_o;             // [slots][R][D] unnormalised partial O
+    // Whole-head packing (packed != 0, arg_pref_valid launches): workgroup w
+    // streams the heads pack_head[w] .. pack_head[w+1]-1 (flattened order
+    // b * Hkv + kvh) whole, so no head is split and no records exist.
+    uint16_t pack_head[kMaxPackWg + 1];
 };
+
+// Brings [B0, E0) and [B1, E1) of the kernel argument block into the scalar
+// cache: one load per 64-byte line, all issued before a single wait.  The
+// arguments read later then hit there instead of each first use paying a
+// memory round trip in a dependent chain (about 1 us apiece at a launch).
+template <int B0, int E0, int B1, int E1>
+__device__ __forceinline__ void warm_kernargs() {
+    typedef const __attribute__((address_space(4))) int kernarg_int;
+    kernarg_int* kp = (kernarg_int*)__builtin_amdgcn_kernarg_segment_ptr();
+    constexpr int N0 = (E0 - B0 + 63) / 64, N1 = (E1 - B1 + 63) / 64;
+    int v[N0 + N1];
+#pragma unroll
+    for (int i = 0; i < N0; ++i) v[i] = kp[(B0 + 64 * i) / 4];
+#pragma unroll
+    for (int i = 0; i < N1; ++i) v[N0 + i] = kp[(B1 + 64 * i) / 4];
+#pragma unroll
+    for (int i = 0; i < N0 + N1; ++i) asm volatile("" ::"s"(v[i]));
+}
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 

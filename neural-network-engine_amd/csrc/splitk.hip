@@ -45,6 +45,7 @@
 // agent-scope fence is a whole-L2 writeback and invalidate.
 #include <atomic>
 #include <algorithm>
+#include <cstddef>
 #include <utility>
 
 #include "nne_common.hpp"
@@ -161,9 +162,9 @@ __device__ __forceinline__ int seq_len(const SplitKParams& p, int b) {
 // sequences).
 template <bool APPEND>
 __device__ __forceinline__ void build_prefix(const SplitKParams& p, int* pref, int tid, int lane,
-                                             int wave) {
+                                             int wave, int arg_pref_tid) {
     if (p.arg_pref_valid) {
-        for (int b = tid; b <= p.B; b += 256) pref[b] = p.arg_pref[b];
+        if (tid <= p.B) pref[tid] = arg_pref_tid;   // p.arg_pref[tid]; B <= kArgSeqs < 256
     } else if (wave == 0) {
         int carry = 0;
         if (lane == 0) pref[0] = 0;
@@ -351,8 +352,18 @@ __global__ __launch_bounds__(256, (D >= 128 && ROWS >= 16) ? 1 : 2) void splitk_
     const int na = (lane >> 2) & 3, ni = lane & 3;
     const int p_idx = 4 * (RPI * ((lane % LPR) >> 2) + lane / LPR) + ni;
     const int wg = blockIdx.x;
+    // Kernel arguments: the loads of the tables go out first, then the scalar
+    // fields' cache lines together, so the prologue waits one round trip for
+    // all of them.  (Left to the compiler, each first use paid its own, in a
+    // chain: 1-2 us per launch before the first K/V load.)
+    const int arg_pref_tid = p.arg_pref[min(tid, kArgSeqs)];
+    const int ph0 = p.pack_head[min(wg, kMaxPackWg - 1)];
+    const int ph1 = p.pack_head[min(wg + 1, kMaxPackWg)];
+    warm_kernargs<0, offsetof(SplitKParams, arg_pref), offsetof(SplitKParams, fused),
+                  offsetof(SplitKParams, pack_head)>();
+    asm volatile("" ::"v"(arg_pref_tid), "v"(ph0), "v"(ph1));   // loaded by now, in one wait
 
-    build_prefix<APPEND>(p, pref, tid, lane, wave);
+    build_prefix<APPEND>(p, pref, tid, lane, wave, arg_pref_tid);
     __syncthreads();
     if (wg == 0 && !p.arg_pref_valid)   // snapshot for the combine kernel (lens may advance meanwhile)
         for (int b = tid; b <= p.B; b += 256) p.ws_pref[b] = pref[b];
@@ -369,8 +380,19 @@ __global__ __launch_bounds__(256, (D >= 128 && ROWS >= 16) ? 1 : 2) void splitk_
             }
         }
     }
-    int g = wg * p.chunk;
-    const int g_end = min(total, g + p.chunk);
+    int g, g_end;
+    if (p.packed) {
+        // Flattened start of head h (h = B * Hkv: the end of the last head).
+        auto head_key = [&](int h) {
+            const int bb = h / p.Hkv, kk = h % p.Hkv;
+            return bb >= p.B ? total : pref[bb] + kk * ((pref[bb + 1] - pref[bb]) / p.Hkv);
+        };
+        g = head_key(ph0);
+        g_end = head_key(ph1);
+    } else {
+        g = wg * p.chunk;
+        g_end = min(total, g + p.chunk);
+    }
     if (g >= g_end) return;
     // first sequence whose keys reach past g
     int b = 0;
@@ -946,9 +968,75 @@ SplitKWorkspace splitk_workspace_layout(int B, int Hkv, int R, int d) {
 
 namespace {
 
+// Greedy grouping of the heads, in flattened order, into groups of at most x
+// keys (x >= the longest head): the number of groups, and with `first` their
+// first heads (first[groups] = B * Hkv).  The Hkv heads of a sequence have
+// one length, so a sequence is placed in O(1) steps plus one per group.
+int pack_groups(const SplitKParams& p, int64_t x, uint16_t* first) {
+    int groups = 0;
+    int64_t sum = 0;
+    for (int b = 0; b < p.B; ++b) {
+        const int64_t L = (p.arg_pref[b + 1] - p.arg_pref[b]) / p.Hkv;
+        int h = b * p.Hkv, n = p.Hkv;
+        while (n > 0) {
+            if (groups == 0 || sum + L > x) {
+                if (first) first[groups] = (uint16_t)h;
+                ++groups;
+                sum = 0;
+            }
+            const int64_t fit = L > 0 ? (x - sum) / L : n;
+            const int k = (int)std::min<int64_t>(n, fit);
+            sum += k * L;
+            h += k;
+            n -= k;
+        }
+    }
+    if (first) first[groups] = (uint16_t)(p.B * p.Hkv);
+    return groups;
+}
+
+// Whole-head packing against the flattened chunks.  Packed, every head is
+// streamed by one workgroup (the heads grouped into at most `slots`
+// workgroups, each as short as the grouping allows), so the launch has no
+// partial records, arrivals or merges, but a workgroup streams at one CU's
+// rate: its time is the longest group at that rate, or the whole launch at
+// the device's.  Chunked, every CU streams an equal share at the device's
+// rate, and the heads cut by the chunk boundaries pay the hand-off.  Rates
+// measured on MI355X with this kernel:
+constexpr double kCuBytesPerUs = 37e3;     // one workgroup streaming its own heads (37 GB/s)
+constexpr double kDevBytesPerUs = 6.9e6;   // the device on equal chunks (6.9 TB/s)
+constexpr double kSplitUs = 6.0;           // records, arrivals and merges of split heads:
+                                           // config 5b 29.3 us chunked, 25.9 us packed
+
+bool plan_packing(SplitKParams& p, int slots, int64_t total_keys) {
+    const int n_heads = p.B * p.Hkv;
+    if (!p.arg_pref_valid || !p.fused || slots > kMaxPackWg || n_heads == 0 || n_heads > 65535 ||
+        total_keys == 0)
+        return false;
+    int64_t longest = 0;
+    for (int b = 0; b < p.B; ++b)
+        longest = std::max<int64_t>(longest, (p.arg_pref[b + 1] - p.arg_pref[b]) / p.Hkv);
+    // smallest bottleneck x >= the longest head whose grouping fits the slots
+    int64_t lo = std::max<int64_t>(longest, (total_keys + slots - 1) / slots), hi = lo;
+    while (pack_groups(p, hi, nullptr) > slots) hi *= 2;
+    while (lo < hi) {
+        const int64_t mid = (lo + hi) / 2;
+        if (pack_groups(p, mid, nullptr) <= slots) hi = mid; else lo = mid + 1;
+    }
+    const double key_bytes = 8.0 * p.d;   // one K row and one V row
+    const double stream_us = (double)total_keys * key_bytes / kDevBytesPerUs;
+    const double packed_us = std::max((double)lo * key_bytes / kCuBytesPerUs, stream_us);
+    if (packed_us > stream_us + kSplitUs) return false;
+    p.n_wg = pack_groups(p, lo, p.pack_head);
+    p.packed = 1;
+    return true;
+}
+
 template <int D>
 hipError_t launch_flat(SplitKParams p, int64_t total_keys, int max_len, hipStream_t stream) {
     const int slots = split_workgroups();
+    p.packed = 0;
+    if (plan_packing(p, slots, total_keys)) return launch_splitk_d<D>(p, stream);
     // Equal flattened chunks, whole 16-key blocks, and at most max_parts
     // workgroups sharing any one head (a chunk boundary can add two).
     int64_t chunk = (total_keys + slots - 1) / (slots > 0 ? slots : 1);
