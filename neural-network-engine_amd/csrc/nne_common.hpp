@@ -170,6 +170,10 @@ __device__ __forceinline__ void warm_kernargs() {
 #pragma unroll
     for (int i = 0; i < N0 + N1; ++i) asm volatile("" ::"s"(v[i]));
 }
+template <int B0, int E0>
+__device__ __forceinline__ void warm_kernargs() {
+    warm_kernargs<B0, E0, E0, E0>();
+}
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 

@@ -96,6 +96,7 @@ __global__ __launch_bounds__(256, 2) void qkv_rope_kernel(const QkvParams p) {
     __shared__ float fin[64][65];                                          // tile [column][row]
     __shared__ int is_last;
 
+    warm_kernargs<0, sizeof(QkvParams)>();   // every argument's line in one round trip
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int r = lane & 15, q4 = lane >> 4;
