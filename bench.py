@@ -508,6 +508,13 @@ def probe(nne, torch, dev):
     torch.cuda.synchronize()
     bench_decode_layer(nne, torch, dev, steps=6)
     torch.cuda.synchronize()
+    bench_mha_decode_layer(nne, torch, dev, steps=6)
+    torch.cuda.synchronize()
+    q1, k1, v1 = (torch.randn(1, 4, 256, 64, generator=g, device=dev) for _ in range(3))
+    o1 = torch.empty_like(q1)
+    for _ in range(6):                        # config 1
+        nne.attention_forward(q1, k1, v1, True, out=o1)
+    torch.cuda.synchronize()
     print("probe done", file=sys.stderr, flush=True)
 
 
@@ -525,7 +532,8 @@ def main():
     ap.add_argument("--probe", action="store_true",
                     help="counter-collection run: a 1 GiB device copy (calibrates FETCH_SIZE/"
                          "WRITE_SIZE), 3 config-2 prefills, 8 config-3 decode steps, 6 "
-                         "config-5b cross-attention calls and 6 decode layer steps")
+                         "config-5b cross-attention calls, 6 config-3 and 6 GPT-2 decode layer "
+                         "steps, 6 config-1 prefills")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "

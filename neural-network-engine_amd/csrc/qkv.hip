@@ -123,9 +123,16 @@ __global__ __launch_bounds__(256, 2) void qkv_rope_kernel(const QkvParams p) {
     constexpr int ROWS = 4 * MT;   // rows per thread
     int pos[ROWS];
 
-    // This wave's packed weights: 4 KB per chunk, 1 KB per load instruction.
-    const vf4* wsrc = reinterpret_cast<const vf4*>(p.wp) +
-                      ((int64_t)(tile * n_chunks + j0) * 4 + wave) * 256 + lane;
+    // The workgroup's packed weights, 16 KB per chunk (4 KB per wave, 1 KB per
+    // load instruction), read through a buffer range that ends with its slice:
+    // the pipeline's loads past the last chunk return zeros without a memory
+    // access.  (As clamped re-reads of the last chunk they fetched 32 KB per
+    // workgroup from HBM again -- non-temporal lines are gone from L2 by then
+    // -- 15 MB, 15 % of a config-3 launch.)
+    const __amdgpu_buffer_rsrc_t wrange = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<float*>(p.wp) + (int64_t)(tile * n_chunks + j0) * 4096, 0,
+        (uint32_t)max(nj, 0) * 16384u, 0x00020000);
+    const uint32_t wlane = (uint32_t)(wave * 256 + lane) * 16;
     // x chunk staging: thread tid moves float4 number tid + 256 q of the
     // 16 MT rows x 16 float4 chunk (rows past M repeat row M - 1; their output
     // columns are never stored).
@@ -144,9 +151,11 @@ __global__ __launch_bounds__(256, 2) void qkv_rope_kernel(const QkvParams p) {
             *reinterpret_cast<vf4*>(&xs[buf][f >> 4][4 * (f & 15)]) = xr[q];
         }
     };
-    auto load_w = [&](vf4 (&w)[4], int jj) __attribute__((always_inline)) {
+    auto load_w = [&](vf4 (&w)[4], int jj) __attribute__((always_inline)) {   // non-temporal
 #pragma unroll
-        for (int i = 0; i < 4; ++i) w[i] = __builtin_nontemporal_load(wsrc + (int64_t)jj * 1024 + 64 * i);
+        for (int i = 0; i < 4; ++i)
+            w[i] = __builtin_bit_cast(vf4, __builtin_amdgcn_raw_buffer_load_b128(
+                                               wrange, wlane + (uint32_t)(jj * 1024 + 64 * i) * 16, 0, 2));
     };
 
     floatx4 acc[MT];
@@ -171,15 +180,16 @@ __global__ __launch_bounds__(256, 2) void qkv_rope_kernel(const QkvParams p) {
     // j % 3, x in LDS buffer j % 2) while the weights of chunk j + 2 and the x
     // of chunk j + 3 are loaded into registers and chunk j + 1's x (loaded
     // two steps earlier) is moved into LDS; one barrier per step, so neither
-    // the HBM weight stream nor the L2 reads of x wait at a barrier.  Loads
-    // past the last chunk reread it (their data is unused).  Unrolled by 6 so
-    // every buffer index is a compile-time constant.
+    // the HBM weight stream nor the L2 reads of x wait at a barrier.  Weight
+    // loads past the last chunk read zeros (above) and x loads reread the last
+    // chunk (an L2 hit); neither is used.  Unrolled by 6 so every buffer index
+    // is a compile-time constant.
     vf4 wbuf[3][4], xr[3][MT];
     auto cl = [&](int jj) { return min(jj, nj - 1); };
     if (nj > 0) {
         load_x(xr[0], j0);
         load_w(wbuf[0], 0);
-        load_w(wbuf[1], cl(1));
+        load_w(wbuf[1], 1);
         load_x(xr[1], j0 + cl(1));
         load_x(xr[2], j0 + cl(2));
         store_x(xr[0], 0);
@@ -193,7 +203,7 @@ __global__ __launch_bounds__(256, 2) void qkv_rope_kernel(const QkvParams p) {
     __syncthreads();
     auto step = [&](int jj, auto ji) __attribute__((always_inline)) {
         constexpr int J = decltype(ji)::value;   // jj % 6
-        load_w(wbuf[(J + 2) % 3], cl(jj + 2));
+        load_w(wbuf[(J + 2) % 3], jj + 2);
         load_x(xr[J % 3], j0 + cl(jj + 3));
         __builtin_amdgcn_sched_barrier(0);
         compute(wbuf[J % 3], J % 2);
