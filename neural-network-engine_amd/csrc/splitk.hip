@@ -968,25 +968,26 @@ SplitKWorkspace splitk_workspace_layout(int B, int Hkv, int R, int d) {
 
 namespace {
 
-// Greedy grouping of the heads, in flattened order, into groups of at most x
-// keys (x >= the longest head): the number of groups, and with `first` their
-// first heads (first[groups] = B * Hkv).  The Hkv heads of a sequence have
-// one length, so a sequence is placed in O(1) steps plus one per group.
-int pack_groups(const SplitKParams& p, int64_t x, uint16_t* first) {
+// Greedy grouping of the heads, in flattened order, into groups whose cost is
+// at most x, a head of L keys costing L + ovh (ovh: the start and end of its
+// segment in key-equivalents; x >= the costliest head): the number of
+// groups, and with `first` their first heads (first[groups] = B * Hkv).  The
+// Hkv heads of a sequence have one length, so a sequence is placed in O(1)
+// steps plus one per group.
+int pack_groups(const SplitKParams& p, int64_t x, int64_t ovh, uint16_t* first) {
     int groups = 0;
     int64_t sum = 0;
     for (int b = 0; b < p.B; ++b) {
-        const int64_t L = (p.arg_pref[b + 1] - p.arg_pref[b]) / p.Hkv;
+        const int64_t c = (p.arg_pref[b + 1] - p.arg_pref[b]) / p.Hkv + ovh;
         int h = b * p.Hkv, n = p.Hkv;
         while (n > 0) {
-            if (groups == 0 || sum + L > x) {
+            if (groups == 0 || sum + c > x) {
                 if (first) first[groups] = (uint16_t)h;
                 ++groups;
                 sum = 0;
             }
-            const int64_t fit = L > 0 ? (x - sum) / L : n;
-            const int k = (int)std::min<int64_t>(n, fit);
-            sum += k * L;
+            const int k = (int)std::min<int64_t>(n, (x - sum) / c);
+            sum += k * c;
             h += k;
             n -= k;
         }
@@ -997,37 +998,42 @@ int pack_groups(const SplitKParams& p, int64_t x, uint16_t* first) {
 
 // Whole-head packing against the flattened chunks.  Packed, every head is
 // streamed by one workgroup (the heads grouped into at most `slots`
-// workgroups, each as short as the grouping allows), so the launch has no
-// partial records, arrivals or merges, but a workgroup streams at one CU's
-// rate: its time is the longest group at that rate, or the whole launch at
-// the device's.  Chunked, every CU streams an equal share at the device's
-// rate, and the heads cut by the chunk boundaries pay the hand-off.  Rates
+// workgroups, each group as cheap as the grouping allows), so the launch has
+// no partial records, arrivals or merges, but a workgroup streams at one
+// CU's rate and pays each of its heads' segment start and end: its time is
+// the costliest group at that rate, or the whole launch at the device's.
+// Chunked, every CU streams an equal share at the device's rate, and the
+// heads cut by the chunk boundaries pay the hand-off.  Rates and costs
 // measured on MI355X with this kernel:
 constexpr double kCuBytesPerUs = 37e3;     // one workgroup streaming its own heads (37 GB/s)
 constexpr double kDevBytesPerUs = 6.9e6;   // the device on equal chunks (6.9 TB/s)
-constexpr double kSplitUs = 6.0;           // records, arrivals and merges of split heads:
-                                           // config 5b 29.3 us chunked, 25.9 us packed
+constexpr double kSegmentUs = 2.5;         // a segment's first loads and its merge and store
+constexpr double kSplitUs = 9.0;           // chunked over packed, past the stream: records,
+                                           // arrivals, merges and more segments per CU
+                                           // (config 5b: 29.3 us chunked, 25.0 us packed)
 
 bool plan_packing(SplitKParams& p, int slots, int64_t total_keys) {
     const int n_heads = p.B * p.Hkv;
     if (!p.arg_pref_valid || !p.fused || slots > kMaxPackWg || n_heads == 0 || n_heads > 65535 ||
         total_keys == 0)
         return false;
+    const double key_bytes = 8.0 * p.d;   // one K row and one V row
+    const int64_t ovh = (int64_t)(kSegmentUs * kCuBytesPerUs / key_bytes + 0.5);
     int64_t longest = 0;
     for (int b = 0; b < p.B; ++b)
         longest = std::max<int64_t>(longest, (p.arg_pref[b + 1] - p.arg_pref[b]) / p.Hkv);
-    // smallest bottleneck x >= the longest head whose grouping fits the slots
-    int64_t lo = std::max<int64_t>(longest, (total_keys + slots - 1) / slots), hi = lo;
-    while (pack_groups(p, hi, nullptr) > slots) hi *= 2;
+    // smallest bottleneck x >= the costliest head whose grouping fits the slots
+    int64_t lo = std::max<int64_t>(longest + ovh, (total_keys + n_heads * ovh + slots - 1) / slots);
+    int64_t hi = lo;
+    while (pack_groups(p, hi, ovh, nullptr) > slots) hi *= 2;
     while (lo < hi) {
         const int64_t mid = (lo + hi) / 2;
-        if (pack_groups(p, mid, nullptr) <= slots) hi = mid; else lo = mid + 1;
+        if (pack_groups(p, mid, ovh, nullptr) <= slots) hi = mid; else lo = mid + 1;
     }
-    const double key_bytes = 8.0 * p.d;   // one K row and one V row
     const double stream_us = (double)total_keys * key_bytes / kDevBytesPerUs;
     const double packed_us = std::max((double)lo * key_bytes / kCuBytesPerUs, stream_us);
     if (packed_us > stream_us + kSplitUs) return false;
-    p.n_wg = pack_groups(p, lo, p.pack_head);
+    p.n_wg = pack_groups(p, lo, ovh, p.pack_head);
     p.packed = 1;
     return true;
 }
