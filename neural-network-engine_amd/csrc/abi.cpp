@@ -226,11 +226,13 @@ int run_attention(const float* q, const int64_t* qs_, const int64_t* qst, const 
     // qoff < tk - 1.
     const int64_t tk = causal ? std::max<int64_t>(0, std::min<int64_t>(Tk, (int64_t)qoff + Tq)) : Tk;
     const bool masked = causal && (int64_t)qoff < tk - 1;
-    const bool fits32 = (int64_t)B * Hkv * Tk < INT32_MAX && (int64_t)Tk * kst[2] < INT32_MAX &&
-                        (int64_t)Tk * vst[2] < INT32_MAX;
+    // The split-K kernel addresses a head's rows with 32-bit byte offsets.
+    const bool fits32 = (int64_t)B * Hkv * Tk < INT32_MAX && (int64_t)Tk * kst[2] < (1LL << 30) &&
+                        (int64_t)Tk * vst[2] < (1LL << 30);
     if (wide && (!fits32 || rows > INT32_MAX))
         return fail(NNE_EINVAL, "Invalid configuration or argument: head dim %d > 128 with %lld "
-                                "keys per call exceeds the split-K kernel's 2^31 limit", d,
+                                "keys per call exceeds the split-K kernel's limits (2^31 keys per call, 2^30 "
+                                "floats per head)", d,
                     (long long)((int64_t)B * Hkv * Tk));
 
     if (vec && fits32 && (wide || (rows <= nne::splitk_max_rows() && tk > 0))) {
@@ -669,9 +671,9 @@ int run_decode(const float* q, const int64_t* q_strides, const float* k_cache, c
         total_keys += L * Hkv;
         seq_lens[(size_t)b] = (int32_t)L;
     }
-    if (capacity * d >= INT32_MAX)
+    if (capacity * d >= (1LL << 30))
         return fail(NNE_EINVAL, "Invalid configuration or argument: KV cache rows of one head "
-                                "(capacity %lld x d %lld) exceed 2^31 floats",
+                                "(capacity %lld x d %lld) exceed 2^30 floats",
                     (long long)capacity, (long long)d);
     if (total_keys >= INT32_MAX)
         return fail(NNE_EINVAL, "Invalid configuration or argument: %lld cached rows exceed the "

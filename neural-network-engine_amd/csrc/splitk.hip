@@ -482,34 +482,45 @@ __global__ __launch_bounds__(256, (D >= 128 && ROWS >= 16) ? 1 : 2) void splitk_
             }
         }
 
-        // Keys past the segment end are clamped to its last row (their scores
-        // are masked to -inf, so the finite data gets weight 0); columns past d
-        // read the row's last 4 floats (their Q columns are zero, their O
-        // columns are never stored).  Loads are branch-free, so the next block
-        // stays in flight while the current one computes.  They are
-        // non-temporal: each K/V byte is read once per launch, and keeping the
-        // stream out of the caches' normal allocation lifts a chunked read of
-        // the cache from ~6.0 to ~6.9 TB/s on MI355X.
+        // K and V rows of the segment are read through buffer ranges that
+        // end with its last key: loads of keys past it (the tail of the last
+        // block, and the ring's loads beyond the segment) return zeros without
+        // a memory access, and zero rows get weight 0 (their scores are masked
+        // to -inf).  Columns past d read the row's last 4 floats (their Q
+        // columns are zero, their O columns are never stored).  Loads are
+        // branch-free, so the next block stays in flight while the current
+        // one computes.  They are non-temporal where one wave reads a block:
+        // each K/V byte is read once per launch, and keeping the stream out of
+        // the caches' normal allocation lifts a chunked read of the cache from
+        // ~6.0 to ~6.9 TB/s on MI355X.  (The host keeps a head under 2^30
+        // floats, so the byte offsets fit in 32 bits.)
+        const __amdgpu_buffer_rsrc_t krange = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<float*>(kb), 0, (uint32_t)key_end * (uint32_t)kst * 4u, 0x00020000);
+        const __amdgpu_buffer_rsrc_t vrange = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<float*>(vb), 0, (uint32_t)key_end * (uint32_t)vst * 4u, 0x00020000);
+        // Byte offset = a lane constant + a wave-uniform part per load (one
+        // VALU add each; no per-load address registers live across blocks).
+        const uint32_t k_lane = ((uint32_t)(lane / LPR) * (uint32_t)kst + (uint32_t)kc_col) * 4u;
+        const uint32_t vn_lane = ((uint32_t)(lane / LPR) * (uint32_t)vst + (uint32_t)kc_col) * 4u;
+        uint32_t vw_lane[NH];
+#pragma unroll
+        for (int h = 0; h < NH; ++h) vw_lane[h] = ((uint32_t)(4 * grp) * (uint32_t)vst + (uint32_t)v_col[h]) * 4u;
+        auto ld = [&](__amdgpu_buffer_rsrc_t range, uint32_t lane_off, int key0, int st) __attribute__((always_inline)) {
+            const uint32_t uni = (uint32_t)__builtin_amdgcn_readfirstlane(key0) * (uint32_t)st * 4u;
+            return __builtin_bit_cast(vf4, __builtin_amdgcn_raw_buffer_load_b128(range, lane_off + uni, 0,
+                                                                                 NT ? 2 : 0));
+        };
         auto load_block = [&](vf4 (&kr)[NK], vf4 (&vr)[4 * NH], int kb0) __attribute__((always_inline)) {
 #pragma unroll
-            for (int i = 0; i < NK; ++i) {
-                const int key = min(kb0 + lane / LPR + RPI * i, key_end - 1);
-                kr[i] = load4<NT>(kb + key * kst + kc_col);
-            }
+            for (int i = 0; i < NK; ++i) kr[i] = ld(krange, k_lane, kb0 + RPI * i, kst);
             if constexpr (NARROW) {
 #pragma unroll
-                for (int i = 0; i < NK; ++i) {
-                    const int key = min(kb0 + lane / LPR + RPI * i, key_end - 1);
-                    vr[i] = load4<NT>(vb + key * vst + kc_col);
-                }
+                for (int i = 0; i < NK; ++i) vr[i] = ld(vrange, vn_lane, kb0 + RPI * i, vst);
             } else {
 #pragma unroll
-                for (int st = 0; st < 4; ++st) {
-                    const int key = min(kb0 + 4 * grp + st, key_end - 1);
+                for (int st = 0; st < 4; ++st)
 #pragma unroll
-                    for (int h = 0; h < NH; ++h)
-                        vr[st * NH + h] = load4<NT>(vb + key * vst + v_col[h]);
-                }
+                    for (int h = 0; h < NH; ++h) vr[st * NH + h] = ld(vrange, vw_lane[h], kb0 + st, vst);
             }
         };
 
