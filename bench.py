@@ -35,12 +35,20 @@ PEAK_HBM_GBS = 8000.0
 
 # HBM bytes per launch measured with rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE on
 # the `--probe` workload, each scaled by its reading for a plain 1 GiB device copy
-# (FETCH_SIZE x2.00, WRITE_SIZE x1.00).  Config 2 prefill: 232.9 MB read + 134.2 MB
-# written (algorithmic 201.3 + 134.2; part of the shared K/V is fetched twice).
-# Config 3 decode step (one launch, split heads merged inside it): 646.7 MB read +
-# 2.2 MB written (algorithmic ~646 + 0.8, plus the partial records of split heads).
-TRAFFIC_PREFILL_CONFIG2 = round(232.9e6 + 134.2e6)
-TRAFFIC_DECODE_CONFIG3_STEP = round(646.7e6 + 2.2e6)
+# (FETCH_SIZE x2.00, WRITE_SIZE x1.00).  Config 2 prefill: 232.6 MB read + 134.2 MB
+# written (algorithmic 201.3 + 134.2; part of the shared K/V is fetched into two
+# XCDs' L2).  Config 3 decode step (one launch, split heads merged inside it):
+# 646.3 MB read + 1.9 MB written (algorithmic 645.0 + 0.8, plus the partial records
+# of split heads).  Config 5b: 123.4 + 0.33 (algorithmic 123.2 + 0.33).  Config-3
+# decode prologue: 109.2 + 4.7 (algorithmic 101.2 + 0.8; partial tiles and x per
+# XCD).  GPT-2 decode attend: 104.4 + 0.3 (algorithmic 104.2 + 0.3).  Config 1:
+# 1.1 + 0.26 (algorithmic 0.79 + 0.26).
+TRAFFIC_PREFILL_CONFIG2 = round(232.6e6 + 134.2e6)
+TRAFFIC_DECODE_CONFIG3_STEP = round(646.3e6 + 1.9e6)
+TRAFFIC_CROSS_CONFIG5B = round(123.4e6 + 0.33e6)
+TRAFFIC_PROLOGUE_CONFIG3 = round(109.2e6 + 4.7e6)
+TRAFFIC_ATTEND_GPT2 = round(104.4e6 + 0.3e6)
+TRAFFIC_PREFILL_CONFIG1 = round(1.1e6 + 0.26e6)
 
 
 def cpu_threads():
@@ -399,7 +407,8 @@ def bench_decode_layer(nne, torch, dev, steps=32, seed=0x5EED0013):
             "prologue_bytes": pbytes, "layer_step_ms": round(step_ms, 4),
             "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS,
                          "unit": "GB/s", "frac": round(gbs / PEAK_HBM_GBS, 4),
-                         "kernel": "qkv_rope_kernel", "bytes": pbytes}}
+                         "kernel": "qkv_rope_kernel", "bytes": pbytes,
+                         "traffic": TRAFFIC_PROLOGUE_CONFIG3}}
 
 
 def bench_mha_decode_layer(nne, torch, dev, steps=32, layers=12, seed=0x5EED0015):
@@ -478,7 +487,8 @@ def bench_mha_decode_layer(nne, torch, dev, steps=32, layers=12, seed=0x5EED0015
             "roofline": {"bound": "hbm", "achieved": round(kv_bytes / (att_ms / 1e3) / 1e9, 1),
                          "peak": PEAK_HBM_GBS, "unit": "GB/s",
                          "frac": round(kv_bytes / (att_ms / 1e3) / 1e9 / PEAK_HBM_GBS, 4),
-                         "kernel": "splitk_kernel (append + attend)", "bytes": round(kv_bytes)}}
+                         "kernel": "splitk_kernel (append + attend)", "bytes": round(kv_bytes),
+                         "traffic": TRAFFIC_ATTEND_GPT2}}
 
 
 def probe(nne, torch, dev):
@@ -615,7 +625,8 @@ def main():
                         "roofline": {"bound": "mfma", "achieved": round(ach, 3),
                                      "peak": PEAK_FP32_MATRIX_TFLOPS, "unit": "TFLOP/s",
                                      "frac": round(ach / PEAK_FP32_MATRIX_TFLOPS, 4),
-                                     "flops": fl}})
+                                     "flops": fl,
+                                     "traffic": TRAFFIC_PREFILL_CONFIG1 if name == "config1" else None}})
             if not args.no_cpu:
                 # Bounded samples of the same workload (a few seconds each).
                 cpu_jobs.append((rec, {
@@ -650,7 +661,8 @@ def main():
                               "frac": round(gbs_x / PEAK_HBM_GBS, 4),
                               "roofline": {"bound": "hbm", "achieved": round(gbs_x, 1),
                                            "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                                           "frac": round(gbs_x / PEAK_HBM_GBS, 4), "bytes": by},
+                                           "frac": round(gbs_x / PEAK_HBM_GBS, 4), "bytes": by,
+                                           "traffic": TRAFFIC_CROSS_CONFIG5B},
                               "host_paced_GB/s": round(by / (hms_x / 1e3) / 1e9, 1),
                               "note": "3 K/V sets rotated (369 MB > 256 MB MALL); calls queued "
                                       "behind a spin kernel so the GPU runs them back to back; "
