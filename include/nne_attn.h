@@ -196,7 +196,8 @@ int nne_decode_workspace_size(int64_t B, int64_t Hq, int64_t Hkv, int64_t d,
  * t = 1).  Ragged lengths, any Hq / Hkv, any batch, head dims up to 256
  * (multiples of 4).  With more than 4 query heads per KV head or d > 128, q
  * must be a 16-byte vector view (strides multiples of 4, 16-byte aligned).
- * ws: the caller's
+ * NNE_EINVAL if capacity * d >= 2^30 (a head's rows are addressed with
+ * 32-bit byte offsets).  ws: the caller's
  * workspace of at least nne_decode_workspace_size, or NULL for the library's
  * per-stream one. */
 int nne_decode_attention(const float *q, const int64_t q_strides[4], const float *k_cache,
