@@ -200,6 +200,10 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t coherent_range(const float* ba
 __device__ __forceinline__ vf4 load_coherent4(__amdgpu_buffer_rsrc_t range, uint32_t byte_offset) {
     return __builtin_bit_cast(vf4, __builtin_amdgcn_raw_buffer_load_b128(range, byte_offset, 0, 16));
 }
+__device__ __forceinline__ float2 load_coherent2(__amdgpu_buffer_rsrc_t range, uint32_t byte_offset) {
+    const auto v = __builtin_amdgcn_raw_buffer_load_b64(range, byte_offset, 0, 16);
+    return float2{__uint_as_float(v[0]), __uint_as_float(v[1])};
+}
 __device__ __forceinline__ void wait_stores_performed() {
     __atomic_signal_fence(__ATOMIC_SEQ_CST);
     __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0), expcnt/lgkmcnt unconstrained

@@ -120,14 +120,6 @@ __device__ __forceinline__ floatx4 mfma4(float a, float b, floatx4 c) {
     return __builtin_amdgcn_mfma_f32_4x4x1f32(a, b, c, CB, AB, 0);
 }
 
-// Monotonic map of floats (incl. -inf) to unsigned, for LDS atomic max.
-__device__ __forceinline__ unsigned float_order(float x) {
-    const unsigned u = __float_as_uint(x);
-    return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
-}
-__device__ __forceinline__ float float_unorder(unsigned k) {
-    return __uint_as_float((k & 0x80000000u) ? (k & 0x7fffffffu) : ~k);
-}
 
 // 16-byte load, non-temporal when each byte is read by one wave only.
 template <bool NT>
@@ -183,105 +175,75 @@ __device__ __forceinline__ void build_prefix(const SplitKParams& p, int* pref, i
 }
 
 // Merges the n partial records (slots s0 .. s0+n-1) of one head into its
-// output, then clears the head's arrival counter.  R <= ROWS <= 64 and
-// n * R <= 1024 (the host bounds the workgroups per head), so each thread
-// holds at most 4 (max, sum) pairs; the O rows are read NPRE records per
-// round trip.
+// output, then clears the head's arrival counter.  Thread t owns the 4-float
+// groups t, t + 256, ... of the R x D output rows: it reads its row's
+// (max, sum) and its 4 floats of O from every record and combines them in
+// record order -- M = max_c m_c, w_c = 2^(m_c - M), O = sum_c w_c O_c /
+// sum_c w_c l_c -- so the result has the same bits whichever workgroup
+// merges, and nothing goes through LDS or a barrier.  The records are read
+// with 16-byte (O) and 8-byte ((max, sum)) coherent loads through a range
+// that ends with the head's last record, NREC records per round trip, every
+// load of a round issued before the first use (loads past the last record
+// read zeros without a memory access).
 template <int D, int ROWS>
 __device__ __forceinline__ void merge_head_records(const SplitKParams& p, int b, int kvh, int head,
-                                                   int64_t s0, int n, float* w_s, unsigned* red_m,
-                                                   float* red_l, int tid) {
-    constexpr int EPT = ROWS * D / 256;   // output elements per thread (R <= ROWS)
-    constexpr int NPRE = EPT >= 16 ? 2 : 32 / EPT;   // partials per element per round trip
-    const int NR = n * p.R;
-    const int RD = p.R * D;
-    const float* o_src = p.ws_o + s0 * RD;
-    // Every load is issued before the first barrier: one memory round trip.
-    float pre[EPT][NPRE];
+                                                   int64_t s0, int n, int tid) {
+    constexpr int VPT = (ROWS * D / 4 + 255) / 256;   // 4-float groups per thread
+    constexpr int NREC = VPT >= 8 ? 2 : 16 / VPT;     // records per round trip
+    const int R = p.R, n4 = R * D / 4;
+    const __amdgpu_buffer_rsrc_t orange =
+        coherent_range(p.ws_o + s0 * R * D, (uint32_t)n * (uint32_t)(R * D) * 4u);
+    const __amdgpu_buffer_rsrc_t mrange =
+        coherent_range(p.ws_ml + s0 * R * 2, (uint32_t)n * (uint32_t)R * 8u);
 #pragma unroll
-    for (int j = 0; j < EPT; ++j) {
-        const int e = tid + 256 * j;
+    for (int v = 0; v < VPT; ++v) {
+        const int g = tid + 256 * v;
+        if (g >= n4) break;
+        const int rr = 4 * g / D, dd = 4 * g % D;
+        // Row maximum over every record (a separate round only when the
+        // records do not fit one).
+        float M = kNegInf;
+        if (n > NREC) {
+            for (int c0 = 0; c0 < n; c0 += 16) {
+                float m[16];
 #pragma unroll
-        for (int c = 0; c < NPRE; ++c)
-            pre[j][c] = (e < RD && c < n) ? load_coherent(o_src + (int64_t)c * RD + e) : 0.f;
-    }
-    float mv[4], lv[4];
+                for (int c = 0; c < 16; ++c)
+                    m[c] = load_coherent2(mrange, (uint32_t)(((c0 + c) * R + rr) * 8)).x;
 #pragma unroll
-    for (int k = 0; k < 4; ++k) {
-        const int e = tid + 256 * k;
-        const int c = e / p.R, rr = e % p.R;
-        mv[k] = e < NR ? load_coherent(p.ws_ml + ((s0 + c) * p.R + rr) * 2) : kNegInf;
-        lv[k] = e < NR ? load_coherent(p.ws_ml + ((s0 + c) * p.R + rr) * 2 + 1) : 0.f;
-    }
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-        const int e = tid + 256 * k;
-        if (e < NR) atomicMax(red_m + e % p.R, float_order(mv[k]));
-    }
-    __syncthreads();
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-        const int e = tid + 256 * k;
-        if (e < NR) {
-            const float M = float_unorder(red_m[e % p.R]);
-            const float f = fast_exp2(mv[k] - (M == kNegInf ? 0.f : M));
-            w_s[e] = f;
-            w_s[1024 + e] = f * lv[k];
+                for (int c = 0; c < 16; ++c)
+                    if (c0 + c < n) M = fmaxf(M, m[c]);
+            }
         }
-    }
-    __syncthreads();
-    // Denominators in a fixed order: 16 lanes per row (record c to lane
-    // c % 16), then a butterfly over the 16, so repeated calls give the same
-    // bits whichever workgroup merges and however its waves are scheduled.
+        float den = 0.f;
+        vf4 acc = vf4{0.f, 0.f, 0.f, 0.f};
+        for (int c0 = 0; c0 < n; c0 += NREC) {
+            float2 ml[NREC];
+            vf4 o[NREC];
 #pragma unroll
-    for (int r0 = 0; r0 < ROWS; r0 += 16) {
-        const int rr = r0 + (tid >> 4), part = tid & 15;
-        float l = 0.f;
-        if (rr < p.R)
-            for (int c = part; c < n; c += 16) l += w_s[1024 + c * p.R + rr];
-        l += __shfl_xor(l, 1, 16);
-        l += __shfl_xor(l, 2, 16);
-        l += __shfl_xor(l, 4, 16);
-        l += __shfl_xor(l, 8, 16);
-        if (rr < p.R && part == 0) red_l[rr] = l;
-    }
-    float acc[EPT];
+            for (int c = 0; c < NREC; ++c) {
+                ml[c] = load_coherent2(mrange, (uint32_t)(((c0 + c) * R + rr) * 8));
+                o[c] = load_coherent4(orange, (uint32_t)(((c0 + c) * R * D + 4 * g) * 4));
+            }
+            if (n <= NREC) {
 #pragma unroll
-    for (int j = 0; j < EPT; ++j) {
-        const int rr = (tid + 256 * j) / D;
-        acc[j] = 0.f;
+                for (int c = 0; c < NREC; ++c)
+                    if (c < n) M = fmaxf(M, ml[c].x);
+            }
+            const float M_use = M == kNegInf ? 0.f : M;
 #pragma unroll
-        for (int c = 0; c < NPRE; ++c)
-            if (c < n && tid + 256 * j < RD) acc[j] += w_s[c * p.R + rr] * pre[j][c];
-    }
-    // Further records: all loads of a round issued before its first add.
-    for (int c0 = NPRE; c0 < n; c0 += NPRE) {
-#pragma unroll
-        for (int j = 0; j < EPT; ++j) {
-            const int e = tid + 256 * j;
-#pragma unroll
-            for (int c = 0; c < NPRE; ++c)
-                pre[j][c] = (e < RD && c0 + c < n) ? load_coherent(o_src + (int64_t)(c0 + c) * RD + e) : 0.f;
+            for (int c = 0; c < NREC; ++c) {
+                if (c0 + c < n) {
+                    const float w = fast_exp2(ml[c].x - M_use);
+                    den += w * ml[c].y;
+                    acc += w * o[c];
+                }
+            }
         }
+        const int gr = p.row0 + rr, hq = kvh * p.G + gr / p.Tq, t = gr % p.Tq;
+        float* orow = p.o.p + b * p.o.sb + hq * p.o.sh + t * p.o.st;
 #pragma unroll
-        for (int j = 0; j < EPT; ++j) {
-            const int rr = (tid + 256 * j) / D;
-#pragma unroll
-            for (int c = 0; c < NPRE; ++c)
-                if (c0 + c < n && tid + 256 * j < RD) acc[j] += w_s[(c0 + c) * p.R + rr] * pre[j][c];
-        }
-    }
-    __syncthreads();                      // red_l complete
-#pragma unroll
-    for (int j = 0; j < EPT; ++j) {
-        const int e = tid + 256 * j;
-        if (e >= RD) break;
-        const int rr = e / D, dd = e % D;
-        if (dd < p.d) {
-            const float den = red_l[rr];
-            const int gr = p.row0 + rr, hq = kvh * p.G + gr / p.Tq, t = gr % p.Tq;
-            p.o.p[b * p.o.sb + hq * p.o.sh + t * p.o.st + dd] = den > 0.f ? acc[j] / den : 0.f;
-        }
+        for (int i = 0; i < 4; ++i)
+            if (dd + i < p.d) orow[dd + i] = den > 0.f ? acc[i] / den : 0.f;
     }
     if (tid == 0)
         __hip_atomic_store(p.ws_cnt + head, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -327,14 +289,11 @@ __global__ __launch_bounds__(256, (D >= 128 && ROWS >= 16) ? 1 : 2) void splitk_
     static_assert(ROWS == 4 || ROWS == 16 || ROWS == 32 || ROWS == 64, "row tile");
     static_assert(!NARROW || D <= 128, "4-row tile up to d = 128");
     static_assert(4 * (NARROW ? 4 : 16) * OS <= 4 * KB * KS, "merge buffer must fit in the K slices");
-    static_assert(2048 <= 4 * KB * KS, "merge weights (2 x 1024) must fit in the K slices");
     static_assert(NK == 4 * NH, "K and V loads per block");
 
     __shared__ __attribute__((aligned(16))) float lds[4 * KB * KS];
     __shared__ float ml_s[4][16][2];
     __shared__ vf4 p_s[4][16];           // narrow: P of a wave's 16 keys
-    __shared__ unsigned red_m[64];       // fused combine: per-row max (ordered)
-    __shared__ float red_l[64];          // fused combine: per-row denominator
     __shared__ int pend_s[2][3];         // fused combine: heads this workgroup merges
     __shared__ int n_pend_s;
     __shared__ int pref[MAX_SEQS + 1];
@@ -783,11 +742,8 @@ __global__ __launch_bounds__(256, (D >= 128 && ROWS >= 16) ? 1 : 2) void splitk_
         const int L = (pref[bb + 1] - pref[bb]) / p.Hkv;
         const int h0 = pref[bb] + kv * L;
         const int n = (h0 + L - 1) / p.chunk - w_first + 1;
-        if (tid < 64) { red_m[tid] = float_order(kNegInf); red_l[tid] = 0.f; }
-        __syncthreads();
         merge_head_records<D, ROWS>(p, bb, kv, bb * p.Hkv + kv, (int64_t)w_first + bb * p.Hkv + kv, n,
-                              lds, red_m, red_l, tid);
-        __syncthreads();
+                                    tid);
     }
 }
 
