@@ -106,6 +106,7 @@ struct QkvParams {
 // Sequences whose flattened prefix travels in the kernel arguments.
 constexpr int kArgSeqs = 128;
 constexpr int kMaxPackWg = 512;   // workgroups of a whole-head packed launch
+constexpr int kMaxCutWg = 256;    // workgroups of a launch with cut chunks (chunk_end)
 
 struct SplitKParams {
     View4 q;
@@ -125,7 +126,8 @@ struct SplitKParams {
     int q_off;
     int n_wg;                // workgroups of the split kernel
     int packed;              // whole-head packing (groups in pack_head, below)
-    int chunk;               // flattened keys per workgroup
+    int chunk;               // flattened keys per workgroup (cut == 0)
+    int cut;                 // chunks cut by the host (chunk_end, below)
     // decode step only (k_new != null): the new row [B, Hkv, 1, d] is attended
     // as key lens[b] and stored into the cache; lens_w[b] is advanced.
     const float* k_new;
@@ -150,7 +152,14 @@ struct SplitKParams {
     // Whole-head packing (packed != 0, arg_pref_valid launches): workgroup w
     // streams the heads pack_head[w] .. pack_head[w+1]-1 (flattened order
     // b * Hkv + kvh) whole, so no head is split and no records exist.
+    union {
     uint16_t pack_head[kMaxPackWg + 1];
+    // Cut chunks (cut != 0, fused launches): workgroup w streams the
+    // flattened keys [chunk_end[w-1], chunk_end[w]) (chunk_end[-1] = 0,
+    // chunk_end[n_wg-1] = every key), cut so that a workgroup's keys plus a
+    // fixed cost for each segment after its first are about equal.
+    int chunk_end[kMaxCutWg];
+    };
 };
 
 // Brings [B0, E0) and [B1, E1) of the kernel argument block into the scalar

@@ -45,6 +45,7 @@
 // agent-scope fence is a whole-L2 writeback and invalidate.
 #include <atomic>
 #include <algorithm>
+#include <climits>
 #include <cstddef>
 #include <utility>
 
@@ -294,9 +295,10 @@ __global__ __launch_bounds__(256, (D >= 128 && ROWS >= 16) ? 1 : 2) void splitk_
     __shared__ __attribute__((aligned(16))) float lds[4 * KB * KS];
     __shared__ float ml_s[4][16][2];
     __shared__ vf4 p_s[4][16];           // narrow: P of a wave's 16 keys
-    __shared__ int pend_s[2][3];         // fused combine: heads this workgroup merges
+    __shared__ int pend_s[2][4];         // fused combine: heads this workgroup merges
     __shared__ int n_pend_s;
     __shared__ int pref[MAX_SEQS + 1];
+    __shared__ int cut_s[kMaxCutWg + 1]; // cut chunks: workgroup w streams [cut_s[w], cut_s[w+1])
 
     const int tid = threadIdx.x, lane = tid & 63;
     // Wave index as a scalar: keeps the per-wave block loop uniform, so the
@@ -318,11 +320,16 @@ __global__ __launch_bounds__(256, (D >= 128 && ROWS >= 16) ? 1 : 2) void splitk_
     const int arg_pref_tid = p.arg_pref[min(tid, kArgSeqs)];
     const int ph0 = p.pack_head[min(wg, kMaxPackWg - 1)];
     const int ph1 = p.pack_head[min(wg + 1, kMaxPackWg)];
+    const int cut_tid = p.chunk_end[min(tid, kMaxCutWg - 1)];
     warm_kernargs<0, offsetof(SplitKParams, arg_pref), offsetof(SplitKParams, fused),
                   offsetof(SplitKParams, pack_head)>();
-    asm volatile("" ::"v"(arg_pref_tid), "v"(ph0), "v"(ph1));   // loaded by now, in one wait
+    asm volatile("" ::"v"(arg_pref_tid), "v"(ph0), "v"(ph1), "v"(cut_tid));   // loaded by now, in one wait
 
     build_prefix<APPEND>(p, pref, tid, lane, wave, arg_pref_tid);
+    if (p.cut) {
+        if (tid == 0) cut_s[0] = 0;
+        if (tid < p.n_wg) cut_s[tid + 1] = cut_tid;
+    }
     __syncthreads();
     if (wg == 0 && !p.arg_pref_valid)   // snapshot for the combine kernel (lens may advance meanwhile)
         for (int b = tid; b <= p.B; b += 256) p.ws_pref[b] = pref[b];
@@ -348,10 +355,23 @@ __global__ __launch_bounds__(256, (D >= 128 && ROWS >= 16) ? 1 : 2) void splitk_
         };
         g = head_key(ph0);
         g_end = head_key(ph1);
+    } else if (p.cut) {
+        g = cut_s[wg];
+        g_end = cut_s[wg + 1];
     } else {
         g = wg * p.chunk;
         g_end = min(total, g + p.chunk);
     }
+    // Workgroup whose chunk holds flattened key `key`.
+    auto owner = [&](int key) {
+        if (!p.cut) return key / p.chunk;
+        int lo = 0, hi = p.n_wg - 1;
+        while (lo < hi) {
+            const int mid = (lo + hi + 1) >> 1;
+            if (cut_s[mid] <= key) lo = mid; else hi = mid - 1;
+        }
+        return lo;
+    };
     if (g >= g_end) return;
     // first sequence whose keys reach past g
     int b = 0;
@@ -719,16 +739,18 @@ __global__ __launch_bounds__(256, (D >= 128 && ROWS >= 16) ? 1 : 2) void splitk_
             // Count this workgroup in.  The last of the head's n workgroups
             // merges it after its own segments (a workgroup has at most two
             // split heads: its first and its last segment).
+            const int w_first = key_begin == 0 ? wg : owner(h_start);
+            const int w_last = key_end == Lb ? wg : owner(h_start + Lb - 1);
             wait_stores_performed();
             __syncthreads();
             if (tid == 0) {
-                const int w_first = h_start / p.chunk, w_last = (h_start + Lb - 1) / p.chunk;
                 const unsigned old = __hip_atomic_fetch_add(p.ws_cnt + head, 1u, __ATOMIC_RELAXED,
                                                             __HIP_MEMORY_SCOPE_AGENT);
                 if (old == (unsigned)(w_last - w_first) && n_pend_s < 2) {
                     pend_s[n_pend_s][0] = b;
                     pend_s[n_pend_s][1] = kvh;
                     pend_s[n_pend_s][2] = w_first;
+                    pend_s[n_pend_s][3] = w_last - w_first + 1;
                     ++n_pend_s;
                 }
             }
@@ -738,10 +760,7 @@ __global__ __launch_bounds__(256, (D >= 128 && ROWS >= 16) ? 1 : 2) void splitk_
     }
     const int n_pend = n_pend_s;
     for (int i = 0; i < n_pend; ++i) {
-        const int bb = pend_s[i][0], kv = pend_s[i][1], w_first = pend_s[i][2];
-        const int L = (pref[bb + 1] - pref[bb]) / p.Hkv;
-        const int h0 = pref[bb] + kv * L;
-        const int n = (h0 + L - 1) / p.chunk - w_first + 1;
+        const int bb = pend_s[i][0], kv = pend_s[i][1], w_first = pend_s[i][2], n = pend_s[i][3];
         merge_head_records<D, ROWS>(p, bb, kv, bb * p.Hkv + kv, (int64_t)w_first + bb * p.Hkv + kv, n,
                                     tid);
     }
@@ -1005,11 +1024,91 @@ bool plan_packing(SplitKParams& p, int slots, int64_t total_keys) {
     return true;
 }
 
+// Cut chunks.  With equal chunks, every segment of a workgroup after its
+// first costs it that segment's hand-off and the latency of its first loads
+// (6-8 us at the loaded latency of a device-wide stream: a workgroup's first
+// two blocks of a segment arrive ~7.8 us after it starts), so workgroups with
+// more segments end later (config-3 decode on MI355X, equal chunks: 84, 93
+// and 97 us for 1, 2 and 3 segments).  Cut, a workgroup's budget x counts
+// that cost: in flattened order, each workgroup takes keys until its keys plus
+// ovh per segment after its first reach x (ovh: the cost in keys at one
+// workgroup's share of the device's rate).  Swept on MI355X from 0 to 16 us:
+// config-3 decode 112.4 us at 0 and ~108.5 from 3 to 10; the G = 8 decode
+// (16-row tile) 103.6 at 0, 100.5 at 3, 97.1 at 8 and 96.7 at 10, 98.7 at 13.
+constexpr double kCutSegmentUs = 8.0;
+constexpr double kCutWgBytesPerUs = 26e3;   // 6.7 TB/s over 256 workgroups
+
+// The number of workgroups of the cut with budget x (with `ends`, their chunk
+// ends), or max_wg + 1 if it takes more than max_wg workgroups or gives a head
+// more than max_parts of them.
+int cut_chunks(const SplitKParams& p, int64_t x, int64_t ovh, int max_wg, int* ends) {
+    int count = 0;
+    int64_t cost = 0;
+    bool open = false;
+    for (int b = 0; b < p.B; ++b) {
+        const int64_t L = (p.arg_pref[b + 1] - p.arg_pref[b]) / p.Hkv;
+        for (int kvh = 0; kvh < p.Hkv && L > 0; ++kvh) {
+            const int64_t h0 = p.arg_pref[b] + kvh * L;
+            int64_t pos = 0;
+            int parts = 0;
+            while (pos < L) {
+                if (open && cost + ovh + KB > x) {   // no room for another segment
+                    if (ends) ends[count - 1] = (int)(h0 + pos);
+                    open = false;
+                }
+                if (open) {
+                    cost += ovh;
+                } else {
+                    if (++count > max_wg) return max_wg + 1;
+                    cost = 0;
+                    open = true;
+                }
+                const int64_t take = std::min(L - pos, x - cost);
+                cost += take;
+                pos += take;
+                if (++parts > p.max_parts) return max_wg + 1;
+                if (cost >= x) {
+                    if (ends) ends[count - 1] = (int)(h0 + pos);
+                    open = false;
+                }
+            }
+        }
+    }
+    if (open && ends) ends[count - 1] = p.arg_pref[p.B];
+    return count;
+}
+
+// The smallest budget whose cut fits `slots` workgroups (and at least 4
+// blocks and an eighth of the longest head, as for equal chunks).
+bool plan_cut(SplitKParams& p, int slots, int64_t total_keys, int max_len) {
+    slots = std::min(slots, kMaxCutWg);
+    if (!p.arg_pref_valid || !p.fused || total_keys == 0 || total_keys > INT32_MAX || slots < 1)
+        return false;
+    const int64_t ovh = (int64_t)(kCutSegmentUs * kCutWgBytesPerUs / (8.0 * p.d) + 0.5);
+    int64_t lo = std::max<int64_t>((total_keys + slots - 1) / slots,
+                                   std::max<int64_t>(4 * KB, (max_len + 7) / 8));
+    int64_t hi = lo;
+    while (cut_chunks(p, hi, ovh, slots, nullptr) > slots) {
+        if (hi > total_keys) return false;
+        hi *= 2;
+    }
+    while (lo < hi) {
+        const int64_t mid = (lo + hi) / 2;
+        if (cut_chunks(p, mid, ovh, slots, nullptr) <= slots) hi = mid; else lo = mid + 1;
+    }
+    p.n_wg = cut_chunks(p, lo, ovh, slots, p.chunk_end);
+    p.chunk = (int)std::min<int64_t>(lo, INT32_MAX);
+    p.cut = 1;
+    return true;
+}
+
 template <int D>
 hipError_t launch_flat(SplitKParams p, int64_t total_keys, int max_len, hipStream_t stream) {
     const int slots = split_workgroups();
     p.packed = 0;
+    p.cut = 0;
     if (plan_packing(p, slots, total_keys)) return launch_splitk_d<D>(p, stream);
+    if (plan_cut(p, slots, total_keys, max_len)) return launch_splitk_d<D>(p, stream);
     // Equal flattened chunks, whole 16-key blocks, and at most max_parts
     // workgroups sharing any one head (a chunk boundary can add two).
     int64_t chunk = (total_keys + slots - 1) / (slots > 0 ? slots : 1);

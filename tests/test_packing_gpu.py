@@ -29,36 +29,7 @@ pytestmark = pytest.mark.gpu
 
 
 def run(nne, cuda, b, hq, hkv, d, lens, append, seed):
-    import torch
-    rng = np.random.default_rng(seed)
-    lens = np.asarray(lens, np.int32)
-    cap = int(lens.max()) + 2
-    kc = rng.standard_normal((b, hkv, cap, d), dtype=np.float32)
-    vc = rng.standard_normal((b, hkv, cap, d), dtype=np.float32)
-    q = rng.standard_normal((b, hq, 1, d), dtype=np.float32)
-    cache = nne.KVCache(1, b, hkv, cap, d, device=cuda)
-    cache.k[0].copy_(torch.from_numpy(kc))
-    cache.v[0].copy_(torch.from_numpy(vc))
-    cache.set_lengths(0, lens)
-    qd = torch.from_numpy(q).to(cuda)
-    if append:
-        kn = rng.standard_normal((b, hkv, 1, d), dtype=np.float32)
-        vn = rng.standard_normal((b, hkv, 1, d), dtype=np.float32)
-        out = cache.decode_step(0, qd, torch.from_numpy(kn).to(cuda), torch.from_numpy(vn).to(cuda))
-        ref, rkc, _, rlens = T.ref_decode_step(q, kc, vc, lens, kn, vn)
-        torch.cuda.synchronize()
-        assert np.array_equal(cache.lens_host[0], rlens)
-        assert np.array_equal(cache.lens_dev[0].cpu().numpy(), rlens)
-        rows = np.arange(b)
-        assert np.array_equal(cache.k[0].cpu().numpy()[rows, :, lens], rkc[rows, :, lens])
-    else:
-        out = cache.attend(0, qd)
-        ref = T.ref_decode_attend(q, kc, vc, lens)
-        again = cache.attend(0, qd)
-        torch.cuda.synchronize()
-        assert np.array_equal(out.cpu().numpy(), again.cpu().numpy()), "repeat calls differ"
-    torch.cuda.synchronize()
-    T.assert_close(out.cpu().numpy(), ref, what="packed b=%d hq=%d hkv=%d d=%d" % (b, hq, hkv, d))
+    T.decode_vs_oracle(nne, cuda, b, hq, hkv, d, lens, append, seed, "packed")
 
 
 @pytest.mark.parametrize("append", [False, True])
