@@ -284,9 +284,15 @@ __global__ __launch_bounds__(256, (D >= 128 && ROWS >= 16) ? 1 : 2) void splitk_
     constexpr int OS = D + 4;            // merge-buffer row stride (rows start 4 banks apart)
     constexpr int NQN = D / 16;          // narrow: Q registers per lane
     constexpr int CBV = D == 128 ? 3 : 2;  // narrow: PV broadcast group (LPR / 4 blocks)
-    // K/V blocks held in registers per wave (at d = 256 one 16-key block is
-    // 32 KB of K and V per wave, and the other waves cover its latency)
-    constexpr int DEPTH = D >= 256 ? 1 : 2;
+    // K/V blocks held in registers per wave.  At d = 256 one 16-key block is
+    // 32 KB of K and V per wave, and the other waves cover its latency.  The
+    // 4-row tile at d = 128 also keeps one: 256 workgroups with 2 blocks per
+    // wave in flight hold ~32 MB of loads, and that queue sets the loaded
+    // latency (a segment's first blocks arrived 7.8 us after its start, 3.7
+    // us with one), while the other waves' blocks keep the stream busy
+    // (config-3 decode 108.8 -> 107.5 us on MI355X; the 16-row tile, with 4x
+    // the MFMA work per block, loses 5 us with one).
+    constexpr int DEPTH = (D >= 256 || (D >= 128 && NARROW)) ? 1 : 2;
     static_assert(ROWS == 4 || ROWS == 16 || ROWS == 32 || ROWS == 64, "row tile");
     static_assert(!NARROW || D <= 128, "4-row tile up to d = 128");
     static_assert(4 * (NARROW ? 4 : 16) * OS <= 4 * KB * KS, "merge buffer must fit in the K slices");
