@@ -38,13 +38,13 @@ PEAK_HBM_GBS = 8000.0
 # (FETCH_SIZE x2.00, WRITE_SIZE x1.00).  Config 2 prefill: 232.6 MB read + 134.2 MB
 # written (algorithmic 201.3 + 134.2; part of the shared K/V is fetched into two
 # XCDs' L2).  Config 3 decode step (one launch, split heads merged inside it):
-# 646.3 MB read + 1.9 MB written (algorithmic 645.0 + 0.8, plus the partial records
+# 646.0 MB read + 1.8 MB written (algorithmic 645.0 + 0.8, plus the partial records
 # of split heads).  Config 5b: 123.4 + 0.33 (algorithmic 123.2 + 0.33).  Config-3
 # decode prologue: 109.2 + 4.7 (algorithmic 101.2 + 0.8; partial tiles and x per
 # XCD).  GPT-2 decode attend: 104.4 + 0.3 (algorithmic 104.2 + 0.3).  Config 1:
 # 1.1 + 0.26 (algorithmic 0.79 + 0.26).
-TRAFFIC_PREFILL_CONFIG2 = round(232.6e6 + 134.2e6)
-TRAFFIC_DECODE_CONFIG3_STEP = round(646.3e6 + 1.9e6)
+TRAFFIC_PREFILL_CONFIG2 = round(233.0e6 + 134.2e6)
+TRAFFIC_DECODE_CONFIG3_STEP = round(646.0e6 + 1.8e6)
 TRAFFIC_CROSS_CONFIG5B = round(123.4e6 + 0.33e6)
 TRAFFIC_PROLOGUE_CONFIG3 = round(109.2e6 + 4.7e6)
 TRAFFIC_ATTEND_GPT2 = round(104.4e6 + 0.3e6)
