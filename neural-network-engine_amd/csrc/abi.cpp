@@ -289,8 +289,9 @@ int run_attention(const float* q, const int64_t* qs_, const int64_t* qst, const 
     p.qscale = scale * nne::kLog2e;
     // Small problems: one workgroup per 16-row block, waves over its key
     // tiles, merged in LDS.
-    if (nne::small_prefill_fits(p, vec, device_cus())) {
-        hipError_t e = nne::launch_small_prefill(p, causal, stream);
+    const int cus = device_cus();
+    if (nne::small_prefill_fits(p, vec, cus)) {
+        hipError_t e = nne::launch_small_prefill(p, causal, cus, stream);
         if (e != hipSuccess) return hip_fail(e, "small prefill launch");
         return NNE_OK;
     }

@@ -36,7 +36,7 @@ PrefillSplit prefill_split_plan(PrefillParams& p, bool causal, bool vec);
 // whether the problem is one (16-byte vector views, d <= 128, at most one
 // workgroup per CU, at most two key tiles per wave).
 bool small_prefill_fits(const PrefillParams& p, bool vec, int cus);
-hipError_t launch_small_prefill(PrefillParams p, bool causal, hipStream_t stream);
+hipError_t launch_small_prefill(PrefillParams p, bool causal, int cus, hipStream_t stream);
 
 // Split-K workspace of one launch (at most splitk_max_seqs() sequences and
 // splitk_rows_per_launch() rows): per-sequence prefix (B+1 ints) and partial

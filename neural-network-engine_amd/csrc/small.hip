@@ -1,5 +1,6 @@
 // Prefill for problems too small to fill the device: one workgroup per
-// (sequence, query head, block of 16 query rows), whose waves split the
+// (sequence, query head, block of 16 query rows) -- two, each with half of the
+// output dims, while that leaves at most one per CU -- whose waves split the
 // block's key tiles and merge through LDS.
 //
 // Algorithm: the online softmax of the reference's flash_attention_forward
@@ -64,14 +65,21 @@ __device__ __forceinline__ void wave_lds_fence() {
 // MI355X: 16 waves of one tile each 7.0 us, 8 waves of two tiles 6.5 us --
 // the LDS merge of twice as many partial O cost more than the second tile.
 // The heaviest causal block (16 tiles) keeps its CU's four MFMA pipes busy
-// for ~1.7 us; with the ~1.6 us launch and ~1.5 us first loads that is most
-// of the call.
+// for ~1.7 us (~1.3 us with half of P V per workgroup); with the ~1.6 us
+// launch and ~1.5 us first loads that is most of the call.  Config 1 with two
+// workgroups per block: 6.3 -> 5.8 us; with four (a quarter of P V each,
+// 4-byte V loads) 6.15 us.
 constexpr int SMALL_WAVES = 8;
 constexpr int SMALL_TILES_PER_WAVE = 2;
 template <int D>
 constexpr int small_waves() { return SMALL_WAVES; }
 
-template <int D, bool CAUSAL>
+// DP = 2: the 4 components of each V vector (dims 4i + c) are split over two
+// workgroups per row block, c in {0, 1} and {2, 3}.  Both compute the block's
+// whole S = Q K^T and softmax (the same bits), each its half of O = P V, so
+// the heaviest block's MFMA work per CU drops from 32 to 24 instructions per
+// tile and its V loads by half, with no hand-off between them.
+template <int D, bool CAUSAL, int DP>
 __global__ __launch_bounds__(64 * small_waves<D>(), 1) void small_prefill_kernel(const PrefillParams p) {
     constexpr int NW = small_waves<D>();
     constexpr int KS = D + 4;            // LDS row stride (16-byte reads conflict-free)
@@ -103,9 +111,10 @@ __global__ __launch_bounds__(64 * small_waves<D>(), 1) void small_prefill_kernel
     // most keys come first.
     const int n_rb = (p.Tq + SKB - 1) / SKB;
     const int n_items = p.B * p.Hq * n_rb;
-    const int per_xcd = (n_items + 7) >> 3;
-    const int idx = (blockIdx.x & 7) * per_xcd + (blockIdx.x >> 3);
-    if (idx >= n_items) return;          // whole workgroup: no barrier is skipped
+    const int per_xcd = (n_items * DP + 7) >> 3;
+    const int idx_p = (blockIdx.x & 7) * per_xcd + (blockIdx.x >> 3);
+    if (idx_p >= n_items * DP) return;   // whole workgroup: no barrier is skipped
+    const int idx = idx_p / DP, part = idx_p % DP;
     const int rb_i = idx % n_rb, bh = idx / n_rb;
     const int rb = CAUSAL ? n_rb - 1 - rb_i : rb_i;
     const int bi = bh / p.Hq, hq = bh % p.Hq, kvh = hq / p.G;
@@ -122,7 +131,7 @@ __global__ __launch_bounds__(64 * small_waves<D>(), 1) void small_prefill_kernel
     const int kc_col = min(4 * (lane % LPR), p.d - 4);
     int v_col[NH];
 #pragma unroll
-    for (int h = 0; h < NH; ++h) v_col[h] = min(64 * h + 4 * col, p.d - 4);
+    for (int h = 0; h < NH; ++h) v_col[h] = min(64 * h + 4 * col, p.d - 4) + (4 / DP) * part;
     float* Kw = lds + wave * SKB * KS;
 
     // The block's 16 Q rows, loaded once for all waves (scaled by
@@ -138,8 +147,10 @@ __global__ __launch_bounds__(64 * small_waves<D>(), 1) void small_prefill_kernel
     // Both tiles of this wave (wave and wave + NW) in flight at once.  Loads
     // clamp to the last key (masked below) and to the row's last 4 floats
     // past d (their Q columns are zero), so none is out of bounds.
-    vf4 kr[SMALL_TILES_PER_WAVE][NK], vr[SMALL_TILES_PER_WAVE][4 * NH];
-    auto load_tile = [&](vf4 (&kt)[NK], vf4 (&vt)[4 * NH], int kb0) __attribute__((always_inline)) {
+    typedef float vfp __attribute__((ext_vector_type(4 / DP)));   // this part's V components
+    vf4 kr[SMALL_TILES_PER_WAVE][NK];
+    vfp vr[SMALL_TILES_PER_WAVE][4 * NH];
+    auto load_tile = [&](vf4 (&kt)[NK], vfp (&vt)[4 * NH], int kb0) __attribute__((always_inline)) {
 #pragma unroll
         for (int i = 0; i < NK; ++i) {
             const int key = min(kb0 + lane / LPR + RPI * i, n_keys - 1);
@@ -150,7 +161,7 @@ __global__ __launch_bounds__(64 * small_waves<D>(), 1) void small_prefill_kernel
             const int key = min(kb0 + 4 * grp + st, n_keys - 1);
 #pragma unroll
             for (int h = 0; h < NH; ++h)
-                vt[st * NH + h] = *reinterpret_cast<const vf4*>(vb + key * vst + v_col[h]);
+                vt[st * NH + h] = *reinterpret_cast<const vfp*>(vb + key * vst + v_col[h]);
         }
     };
 #pragma unroll
@@ -168,9 +179,10 @@ __global__ __launch_bounds__(64 * small_waves<D>(), 1) void small_prefill_kernel
         qf[4 * s4 + 3] = x.w;
     }
 
-    floatx4 o[NB];
+    constexpr int NC = 4 / DP;           // V components (dim blocks per h) of this part
+    floatx4 o[NH * NC];
 #pragma unroll
-    for (int b = 0; b < NB; ++b) o[b] = floatx4{0.f, 0.f, 0.f, 0.f};
+    for (int b = 0; b < NH * NC; ++b) o[b] = floatx4{0.f, 0.f, 0.f, 0.f};
     float m_run = kNegInf, l_run = 0.f;
     // last key this lane's row may see (tile masks only where a tile reaches past it)
     const int row_last = CAUSAL ? row + p.q_offset : p.Tk - 1;
@@ -218,32 +230,35 @@ __global__ __launch_bounds__(64 * small_waves<D>(), 1) void small_prefill_kernel
         l_run = alpha * l_run + ls;       // this lane's 4 keys; summed over lanes below
         m_run = m_new;
 #pragma unroll
-        for (int b = 0; b < NB; ++b) o[b] *= alpha;
+        for (int b = 0; b < NH * NC; ++b) o[b] *= alpha;
         // O^T += V^T P^T: step st pairs key kb0 + 4*grp + st (register st of
-        // P^T); dim block 4h + c covers dims 64h + 4*i + c, i = lane % 16.
+        // P^T); dim block NC*h + c covers dims 64h + 4*i + NC*part + c,
+        // i = lane % 16.
 #pragma unroll
         for (int st = 0; st < 4; ++st)
 #pragma unroll
             for (int h = 0; h < NH; ++h) {
-                const vf4 vv = vr[j][st * NH + h];
-                o[4 * h + 0] = __builtin_amdgcn_mfma_f32_16x16x4f32(vv.x, s[st], o[4 * h + 0], 0, 0, 0);
-                o[4 * h + 1] = __builtin_amdgcn_mfma_f32_16x16x4f32(vv.y, s[st], o[4 * h + 1], 0, 0, 0);
-                o[4 * h + 2] = __builtin_amdgcn_mfma_f32_16x16x4f32(vv.z, s[st], o[4 * h + 2], 0, 0, 0);
-                o[4 * h + 3] = __builtin_amdgcn_mfma_f32_16x16x4f32(vv.w, s[st], o[4 * h + 3], 0, 0, 0);
+                const vfp vv = vr[j][st * NH + h];
+#pragma unroll
+                for (int c = 0; c < NC; ++c)
+                    o[NC * h + c] = __builtin_amdgcn_mfma_f32_16x16x4f32(vv[c], s[st], o[NC * h + c], 0, 0, 0);
             }
     }
 
     // Merge the waves' (max, sum, O) through LDS: O[row col][dim] with
-    // dim = 64h + 16*grp + 4*reg + c  for  o[4h + c][reg].
+    // dim = 64h + 16*grp + 4*reg + NC*part + c  for  o[NC*h + c][reg].
     const float l_tot = rows4_sum(l_run);
     __syncthreads();                      // every wave is done with its K slice
     float* ob = lds;                      // [NW waves][16 rows][KS]
 #pragma unroll
     for (int h = 0; h < NH; ++h)
 #pragma unroll
-        for (int reg = 0; reg < 4; ++reg)
-            *reinterpret_cast<vf4*>(ob + (wave * SKB + col) * KS + 64 * h + 16 * grp + 4 * reg) =
-                vf4{o[4 * h + 0][reg], o[4 * h + 1][reg], o[4 * h + 2][reg], o[4 * h + 3][reg]};
+        for (int reg = 0; reg < 4; ++reg) {
+            vfp ov;
+#pragma unroll
+            for (int c = 0; c < NC; ++c) ov[c] = o[NC * h + c][reg];
+            *reinterpret_cast<vfp*>(ob + (wave * SKB + col) * KS + 64 * h + 16 * grp + 4 * reg + NC * part) = ov;
+        }
     if (grp == 0) {
         ml_s[wave][col][0] = m_run;
         ml_s[wave][col][1] = l_tot;
@@ -266,28 +281,37 @@ __global__ __launch_bounds__(64 * small_waves<D>(), 1) void small_prefill_kernel
         wgt_s[w][rr] = L > 0.f ? f / L : 0.f;
     }
     __syncthreads();
-    // 16-byte output vectors (d % 4 == 0 and 16-byte views on this path).
+    // 16-byte output vectors (8-byte with DP = 2: this part's 2 of every 4
+    // dims; d % 4 == 0 and 16-byte views on this path).
     for (int e = tid; e < SKB * (D / 4); e += 64 * NW) {
-        const int rr = e / (D / 4), c = 4 * (e % (D / 4));
-        vf4 acc = vf4{0.f, 0.f, 0.f, 0.f};
+        const int rr = e / (D / 4), c = 4 * (e % (D / 4)) + NC * part;
+        vfp acc = vfp(0.f);
 #pragma unroll
         for (int w = 0; w < NW; ++w)
-            acc += wgt_s[w][rr] * *reinterpret_cast<const vf4*>(ob + (w * SKB + rr) * KS + c);
+            acc += wgt_s[w][rr] * *reinterpret_cast<const vfp*>(ob + (w * SKB + rr) * KS + c);
         if (r0 + rr < p.Tq && c < p.d)
-            *reinterpret_cast<vf4*>(p.o.p + bi * p.o.sb + hq * p.o.sh + (int64_t)(r0 + rr) * p.o.st + c) = acc;
+            *reinterpret_cast<vfp*>(p.o.p + bi * p.o.sb + hq * p.o.sh + (int64_t)(r0 + rr) * p.o.st + c) = acc;
     }
 }
 
+template <int D, int DP>
+hipError_t launch_small_dp(const PrefillParams& p, bool causal, int n_items, hipStream_t stream) {
+    const dim3 grid((unsigned)(8 * ((n_items * DP + 7) / 8))), block(64 * small_waves<D>());
+    if (causal)
+        hipLaunchKernelGGL((small_prefill_kernel<D, true, DP>), grid, block, 0, stream, p);
+    else
+        hipLaunchKernelGGL((small_prefill_kernel<D, false, DP>), grid, block, 0, stream, p);
+    return hipGetLastError();
+}
+
+// Two workgroups per row block (each half of P V) while that still leaves
+// at most one per CU.
 template <int D>
-hipError_t launch_small_d(const PrefillParams& p, bool causal, hipStream_t stream) {
+hipError_t launch_small_d(const PrefillParams& p, bool causal, int cus, hipStream_t stream) {
     const int n_rb = (p.Tq + SKB - 1) / SKB;
     const int n_items = p.B * p.Hq * n_rb;
-    const dim3 grid((unsigned)(8 * ((n_items + 7) / 8))), block(64 * small_waves<D>());
-    if (causal)
-        hipLaunchKernelGGL((small_prefill_kernel<D, true>), grid, block, 0, stream, p);
-    else
-        hipLaunchKernelGGL((small_prefill_kernel<D, false>), grid, block, 0, stream, p);
-    return hipGetLastError();
+    if (2 * n_items <= cus) return launch_small_dp<D, 2>(p, causal, n_items, stream);
+    return launch_small_dp<D, 1>(p, causal, n_items, stream);
 }
 
 }  // namespace
@@ -302,10 +326,10 @@ bool small_prefill_fits(const PrefillParams& p, bool vec, int cus) {
     return wgs > 0 && wgs <= cus && tiles <= SMALL_TILES_PER_WAVE * SMALL_WAVES;
 }
 
-hipError_t launch_small_prefill(PrefillParams p, bool causal, hipStream_t stream) {
+hipError_t launch_small_prefill(PrefillParams p, bool causal, int cus, hipStream_t stream) {
     p.G = p.Hq / p.Hkv;
     if ((int64_t)p.B * p.Hq * p.Tq == 0) return hipSuccess;
-    return p.d <= 64 ? launch_small_d<64>(p, causal, stream) : launch_small_d<128>(p, causal, stream);
+    return p.d <= 64 ? launch_small_d<64>(p, causal, cus, stream) : launch_small_d<128>(p, causal, cus, stream);
 }
 
 }  // namespace nne

@@ -345,7 +345,10 @@ def test_head_dims_above_128(nne, cuda, b, hq, hkv, tq, tk, d, causal, q_off):
 # 16-row block) with at most two 16-key tiles per wave run on the small
 # prefill kernel: the waves of a workgroup take one row block's key tiles and
 # merge in LDS.  Row counts that are not multiples of 16, GQA, offsets of both
-# signs (rows that see no key), Tk < Tq and Tk > Tq, padded head dims.
+# signs (rows that see no key), Tk < Tq and Tk > Tq, padded head dims.  Up to
+# half as many row blocks as CUs, two workgroups share a block (each computes
+# S and the softmax, and half of P V); the last two shapes have more blocks
+# (240 and 132), one workgroup each.
 @pytest.mark.parametrize("b,hq,hkv,tq,tk,d,causal,q_off", [
     (1, 4, 4, 256, 256, 64, True, 0),      # config 1
     (2, 6, 2, 37, 37, 64, True, 0),
@@ -355,6 +358,8 @@ def test_head_dims_above_128(nne, cuda, b, hq, hkv, tq, tk, d, causal, q_off):
     (2, 4, 4, 64, 64, 128, True, 0),
     (1, 2, 1, 130, 250, 96, False, 0),
     (1, 5, 5, 17, 200, 128, True, 183),
+    (2, 8, 4, 240, 240, 64, True, 0),
+    (1, 12, 3, 176, 176, 128, False, 0),
 ])
 def test_small_prefill_kernel_shapes(nne, cuda, b, hq, hkv, tq, tk, d, causal, q_off):
     print("case small prefill", b, hq, hkv, tq, tk, d, causal, q_off, flush=True)
