@@ -1,18 +1,11 @@
-// Shared device helpers and launch-parameter structs for the attention kernels.
-//
-// Layout conventions (all f32):
-//   Q/O  [B, Hq,  T_q, d]  and  K/V [B, Hkv, T_k, d], each a strided view
-//   (element strides for batch, head, row, dim).  Query head hq reads KV head
-//   hq / G with G = Hq / Hkv, the repeat-KV mapping of the reference's
-//   GroupedQueryAttention (src/models/llama.rs:256-266).
-//   A key c is visible to query row r iff c <= r + q_offset (causal) -- the
-//   reference's flash path uses q_offset = 0 (src/nn/flash_attention.rs:113),
-//   its cached GQA/MHA paths use q_offset = start_pos (llama.rs:280-283,
-//   attention.rs:104-108).
+// Shared device helpers of the attention kernels; the launch-parameter
+// structs and layout conventions are in nne_params.hpp.
 #pragma once
 
 #include <hip/hip_runtime.h>
 #include <stdint.h>
+
+#include "nne_params.hpp"
 
 namespace nne {
 
@@ -24,143 +17,6 @@ typedef float vf4 __attribute__((ext_vector_type(4)));
 
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kNegInf = -__builtin_huge_valf();
-
-struct View4 {
-    const float* p;
-    int64_t sb, sh, st, sd;
-};
-
-struct OutView4 {
-    float* p;
-    int64_t sb, sh, st, sd;
-};
-
-// Prefill (MFMA) kernel parameters.  One workgroup = 4 waves; each wave owns
-// one "unit" = 32 query rows of one query head.  Units of one KV head are
-// numbered u = row_block * G + g, and workgroup w of that KV head takes units
-// 4w .. 4w+3, so the G query heads of a group share every K/V tile the
-// workgroup stages in LDS.
-constexpr int kMaxSplitItems = 256;   // work items per KV head of a key-split launch
-
-struct PrefillParams {
-    View4 q, k, v;
-    OutView4 o;
-    int B, Hq, Hkv, G, Tq, Tk, d;
-    int q_offset;
-    float qscale;   // softmax scale * log2(e), folded into Q
-    int n_rb;       // ceil(Tq / 32)
-    int n_units;    // G * n_rb
-    int n_wg;       // ceil(n_units / 4) work items (4 units each) per KV head
-    int total;      // B * Hkv * n_wg work items
-    // Persistent schedule: a work item is the 4 units of one workgroup-sized
-    // step of a KV head.  With `pairing`, items of ranks r and n_wg-1-r of a
-    // head form one super-item (equal causal work); n_pairs super-items per
-    // head, n_super in all, per_xcd of them per XCD.
-    int pairing;
-    int n_pairs;
-    int n_super;
-    int per_xcd;
-    // Key split for problems too small to fill the chip (n_chunks > 1): the
-    // key tiles of every work item are cut into chunks of chunk_tiles tiles,
-    // one workgroup per (item, chunk); each leaves a partial (max, sum, O)
-    // record in ws and counts itself in cnt[item] (zeroed, left zeroed), and
-    // the last to arrive merges the item's records and writes O.
-    int n_chunks;       // largest chunk count of an item
-    int chunk_tiles;
-    float* ws;
-    uint32_t* cnt;
-    // Workgroup w of a KV head runs chunk w - part_prefix[i] of item i, where
-    // part_prefix[i] <= w < part_prefix[i + 1] (items of a head in rank order,
-    // empty items one chunk); part_prefix[n_wg] workgroups per head.
-    uint16_t part_prefix[kMaxSplitItems + 1];
-};
-
-// Fused decode prologue (qkv.hip): rows m < M of x [M, C] (row stride x_rs,
-// unit column stride) times the packed q/k/v weights (n_tiles tiles of 64
-// output columns, C split into S slices of kc_per_slice 64-wide chunks), plus
-// bias[j] (j = q, k, v; [H_j * d] or null); q and k rotated at position
-// pos[m] with tables cos/sin [max_seq_len, d] (no rotation when cos is null);
-// row m, head h, dim i written to
-// out[j] + m * o_sb[j] + h * o_sh[j] + i.  With S > 1, ws holds the partial
-// tiles ([n_tiles][S][64][64]) and cnt[n_tiles] the zeroed arrival counters.
-struct QkvParams {
-    const float* x;
-    int64_t x_rs;
-    const float* wp;
-    const float* bias[3];
-    const float* cos;
-    const float* sin;
-    const int32_t* pos;
-    float* out[3];
-    int64_t o_sb[3], o_sh[3];
-    int M, C, Hq, Hkv, d;
-    int n_tiles, S, kc_per_slice;
-    float* ws;
-    uint32_t* cnt;
-};
-
-// Split-K few-query kernel parameters (decode and cross-attention).  Each KV
-// head serves G * Tq query rows; a launch takes R of them starting at row0,
-// and its row rr maps to query head kvh*G + (row0+rr)/Tq and query position
-// (row0+rr) % Tq.  Every row sees every key of its sequence.
-// Sequences whose flattened prefix travels in the kernel arguments.
-constexpr int kArgSeqs = 128;
-constexpr int kMaxPackWg = 512;   // workgroups of a whole-head packed launch
-constexpr int kMaxCutWg = 256;    // workgroups of a launch with cut chunks (chunk_end)
-
-struct SplitKParams {
-    View4 q;
-    const float* k;
-    const float* v;
-    int64_t ksb, ksh, kst;   // K strides (dim stride 1)
-    int64_t vsb, vsh, vst;   // V strides (dim stride 1)
-    const int32_t* lens;     // per-sequence key counts (device), or null
-    int tk;                  // key count when lens == null
-    int max_keys;            // host-validated upper bound on every key count
-    OutView4 o;
-    int B, Hq, Hkv, G, Tq, d, R;
-    int row0;                // first of this launch's rows (row passes of many-row heads)
-    float qscale;            // softmax scale * log2(e)
-    // Causal rows (masked != 0): query t sees keys c <= q_off + t only.
-    int masked;
-    int q_off;
-    int n_wg;                // workgroups of the split kernel
-    int packed;              // whole-head packing (groups in pack_head, below)
-    int chunk;               // flattened keys per workgroup (cut == 0)
-    int cut;                 // chunks cut by the host (chunk_end, below)
-    // decode step only (k_new != null): the new row [B, Hkv, 1, d] is attended
-    // as key lens[b] and stored into the cache; lens_w[b] is advanced.
-    const float* k_new;
-    const float* v_new;
-    int64_t kn_sb, kn_sh, vn_sb, vn_sh;
-    int32_t* lens_w;
-    // Flattened start of each sequence, pref[b] = Hkv * sum_{b' < b} L_b',
-    // computed by the host when B <= kArgSeqs (arg_pref valid), else by the
-    // split kernel from lens into ws_pref.
-    int arg_pref_valid;
-    int arg_pref[kArgSeqs + 1];
-    // Fused combine (arg_pref_valid launches): the last workgroup to finish a
-    // split head merges its partial records; ws_cnt[head] counts arrivals and
-    // is left at zero.  max_parts bounds the workgroups sharing one head.
-    int fused;
-    int max_parts;
-    uint32_t* ws_cnt;        // [B*Hkv] arrival counters, zero between launches
-    // workspace
-    int32_t* ws_pref;        // [B+1] flattened start of each sequence (this launch)
-    float* ws_ml;            // [slots][R][2] partial (max, sum); slot = workgroup + head
-    float* ws_o;             // [slots][R][D] unnormalised partial O
-    // Whole-head packing (packed != 0, arg_pref_valid launches): workgroup w
-    // streams the heads pack_head[w] .. pack_head[w+1]-1 (flattened order
-    // b * Hkv + kvh) whole, so no head is split and no records exist.
-    union {
-    uint16_t pack_head[kMaxPackWg + 1];
-    // Cut chunks (cut != 0, fused launches): workgroup w streams the
-    // flattened keys [chunk_end[w-1], chunk_end[w]) (chunk_end[-1] = 0,
-    // chunk_end[n_wg-1] = every key), cut so that a workgroup's keys plus a
-    // fixed cost for each segment after its first are about equal.
-    int chunk_end[kMaxCutWg];
-    };
-};
 
 // Brings [B0, E0) and [B1, E1) of the kernel argument block into the scalar
 // cache: one load per 64-byte line, all issued before a single wait.  The
