@@ -297,3 +297,20 @@ def test_undersized_caller_workspace_is_refused_before_launch(nne):
                                   0, 0.0, ctypes.byref(few), None)
     assert rc == nne.NNE_EINVAL
     assert "counters" in lib.nne_last_error().decode()
+
+
+def test_integration_build_lists_every_source():
+    """The Rust build script in INTEGRATION.md compiles the same sources as
+    neural-network-engine_amd/build.py (a missing one would leave symbols
+    undefined at link time)."""
+    import os
+    import re
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    build_py = open(os.path.join(root, "neural-network-engine_amd", "build.py")).read()
+    sources = re.search(r"^SOURCES = \[(.*)\]$", build_py, re.M).group(1)
+    sources = re.findall(r'"([^"]+)"', sources)
+    doc = open(os.path.join(root, "INTEGRATION.md")).read()
+    args = re.search(r'\.args\(\[("prefill\.hip"[^\]]*)\]', doc).group(1)
+    assert re.findall(r'"([^"]+)"', args) == sources
+    for s in sources:
+        assert "csrc/" + s in doc.split("## 1.")[0], s
