@@ -42,13 +42,20 @@ PEAK_HBM_GBS = 8000.0
 # of split heads).  Config 5b: 123.4 + 0.33 (algorithmic 123.2 + 0.33).  Config-3
 # decode prologue: 109.2 + 4.7 (algorithmic 101.2 + 0.8; partial tiles and x per
 # XCD).  GPT-2 decode attend: 104.4 + 0.3 (algorithmic 104.2 + 0.3).  Config 1:
-# 1.1 + 0.26 (algorithmic 0.79 + 0.26).
+# 1.1 + 0.26 (algorithmic 0.79 + 0.26).  Config 4: 283.0 + 67.1 (algorithmic
+# 201.3 + 67.1; the persistent workgroups of a KV head on one XCD re-fetch part of
+# its 8.4 MB of K/V, more than the XCD's 4 MB L2).  Config 5a: 186.8 + 61.4
+# (algorithmic 184.3 + 61.4).  G = 8 decode step: 677.2 + 3.25 (algorithmic
+# 681.3 + 1.3, plus the 16-row partial records of split heads).
 TRAFFIC_PREFILL_CONFIG2 = round(233.0e6 + 134.2e6)
 TRAFFIC_DECODE_CONFIG3_STEP = round(646.0e6 + 1.8e6)
 TRAFFIC_CROSS_CONFIG5B = round(123.4e6 + 0.33e6)
 TRAFFIC_PROLOGUE_CONFIG3 = round(109.2e6 + 4.7e6)
 TRAFFIC_ATTEND_GPT2 = round(104.4e6 + 0.3e6)
 TRAFFIC_PREFILL_CONFIG1 = round(1.1e6 + 0.26e6)
+TRAFFIC_PREFILL_CONFIG4 = round(283.0e6 + 67.1e6)
+TRAFFIC_PREFILL_CONFIG5A = round(186.8e6 + 61.4e6)
+TRAFFIC_DECODE_G8_STEP = round(677.2e6 + 3.25e6)
 
 
 def cpu_threads():
@@ -525,6 +532,17 @@ def probe(nne, torch, dev):
     for _ in range(6):                        # config 1
         nne.attention_forward(q1, k1, v1, True, out=o1)
     torch.cuda.synchronize()
+    del q1, k1, v1, o1
+    for (bb, h, tt, causal, std, calls) in ((1, 16, 16384, True, 0.5, 2),    # config 4
+                                            (8, 20, 1500, False, 1.0, 3)):   # config 5a
+        q, k, v = (torch.randn(bb, h, tt, 64, generator=g, device=dev) * std for _ in range(3))
+        o = torch.empty_like(q)
+        for _ in range(calls):
+            nne.attention_forward(q, k, v, causal, out=o)
+        torch.cuda.synchronize()
+        del q, k, v, o
+    bench_decode(nne, torch, dev, steps=8, warmup=1, hq=64, seed=0x5EED0016)   # G = 8 decode
+    torch.cuda.synchronize()
     print("probe done", file=sys.stderr, flush=True)
 
 
@@ -543,7 +561,8 @@ def main():
                     help="counter-collection run: a 1 GiB device copy (calibrates FETCH_SIZE/"
                          "WRITE_SIZE), 3 config-2 prefills, 8 config-3 decode steps, 6 "
                          "config-5b cross-attention calls, 6 config-3 and 6 GPT-2 decode layer "
-                         "steps, 6 config-1 prefills")
+                         "steps, 6 config-1 prefills, 2 config-4 and 3 config-5a prefills, 8 "
+                         "G=8 decode steps")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
@@ -626,7 +645,9 @@ def main():
                                      "peak": PEAK_FP32_MATRIX_TFLOPS, "unit": "TFLOP/s",
                                      "frac": round(ach / PEAK_FP32_MATRIX_TFLOPS, 4),
                                      "flops": fl,
-                                     "traffic": TRAFFIC_PREFILL_CONFIG1 if name == "config1" else None}})
+                                     "traffic": {"config1": TRAFFIC_PREFILL_CONFIG1,
+                                                 "config4": TRAFFIC_PREFILL_CONFIG4,
+                                                 "config5a": TRAFFIC_PREFILL_CONFIG5A}[name]}})
             if not args.no_cpu:
                 # Bounded samples of the same workload (a few seconds each).
                 cpu_jobs.append((rec, {
@@ -674,7 +695,8 @@ def main():
         print("bench: G=8 decode", file=sys.stderr, flush=True)
         rec = bench_decode(nne, torch, dev, hq=64, seed=0x5EED0016,
                            workload="G=8 decode (LLaMA-2-70B grouping): B=32 Hq=64 Hkv=8 d=128 "
-                                    "L0~U[512,4096] ragged, 64 steps append+attend, f32")
+                                    "L0~U[512,4096] ragged, 64 steps append+attend, f32",
+                           traffic=TRAFFIC_DECODE_G8_STEP)
         rec["workload"] = rec["config"]["workload"]
         extra.append(rec)
         if not args.no_cpu:
