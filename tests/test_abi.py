@@ -314,3 +314,17 @@ def test_integration_build_lists_every_source():
     assert re.findall(r'"([^"]+)"', args) == sources
     for s in sources:
         assert "csrc/" + s in doc.split("## 1.")[0], s
+
+
+def test_integration_declares_every_entry_point():
+    """INTEGRATION.md's `lib.rs` declares each function of include/nne_attn.h
+    once, and nothing else."""
+    import os
+    import re
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    header = open(os.path.join(root, "include", "nne_attn.h")).read()
+    declared = set(re.findall(r"\b(nne_[a-z0-9_]+)\s*\(", header))
+    doc = open(os.path.join(root, "INTEGRATION.md")).read()
+    bound = re.findall(r"pub fn (nne_[a-z0-9_]+)\s*\(", doc)
+    assert len(bound) == len(set(bound))
+    assert set(bound) == declared
