@@ -207,8 +207,8 @@ __global__ __launch_bounds__(256, 2) void qkv_rope_kernel(const QkvParams p) {
         load_x(xr[J % 3], j0 + cl(jj + 3));
         __builtin_amdgcn_sched_barrier(0);
         // Raised wave priority over the MFMAs: the other workgroup on the CU
-        // issues its loads and LDS traffic under them (B = 32: 25.2 -> 25.0 us,
-        // B = 64: 45.1 -> 44.7 us on MI355X).
+        // issues its loads and LDS traffic under them (at most ~1 % on MI355X:
+        // B = 32 25.2 -> 25.0 us in one A/B, level in another).
         __builtin_amdgcn_s_setprio(1);
         compute(wbuf[J % 3], J % 2);
         __builtin_amdgcn_s_setprio(0);
