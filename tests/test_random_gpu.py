@@ -115,3 +115,41 @@ def test_random_decode_steps(nne, cuda, seed):
     assert list(cache.lens_dev[0].cpu().numpy()) == list(lens)
     assert np.array_equal(cache.k[0].cpu().numpy(), kc)
     assert np.array_equal(cache.v[0].cpu().numpy(), vc)
+
+
+def draw_wide_decode_case(seed):
+    """Wider ragged decode batches than test_random_decode_steps: up to 160
+    sequences (past 128 the flattened prefix is not in the kernel arguments
+    and the launch cuts equal chunks), lengths up to 5000, batches of short
+    heads with empty ones, or one long head among short ones; the split-K
+    layout is whichever the launch chooses (whole heads, cut chunks, equal
+    chunks).  Dense cache arrays stay under 600 MB."""
+    rng = np.random.default_rng(5000 + seed)
+    b = int(rng.integers(1, 161))
+    hkv = int(rng.choice([1, 2, 4, 8]))
+    g = int(rng.choice([1, 2, 4, 8]))
+    d = int(rng.choice([64, 128]))
+    kind = int(rng.integers(0, 3))
+    if kind == 0:
+        lens = rng.integers(0, 5000, size=b)
+    elif kind == 1:
+        lens = np.where(rng.random(b) < 0.1, 0, rng.integers(1, 300, size=b))
+    else:
+        lens = rng.integers(1, 400, size=b)
+        lens[int(rng.integers(0, b))] = int(rng.integers(8000, 20000))
+    lens = lens.astype(np.int32)
+    while b > 1 and b * hkv * (int(lens.max()) + 2) * d > 1.5e8:
+        b = max(1, b // 2)
+        lens = lens[:b].copy()
+        if kind == 2 and lens.max() < 8000:
+            lens[0] = 8000
+    append = bool(rng.random() < 0.7)
+    return b, hkv, g, d, lens, append
+
+
+@pytest.mark.parametrize("seed", range(12))
+def test_random_wide_decode(nne, cuda, seed):
+    b, hkv, g, d, lens, append = draw_wide_decode_case(seed)
+    print("case seed=%d b=%d hkv=%d g=%d d=%d max_len=%d keys=%d append=%d"
+          % (seed, b, hkv, g, d, lens.max(), lens.sum(), append), flush=True)
+    T.decode_vs_oracle(nne, cuda, b, hkv * g, hkv, d, lens, append, 7000 + seed, "wide seed %d" % seed)
