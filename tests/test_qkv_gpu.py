@@ -101,6 +101,41 @@ def test_qkv_rope_matches_oracle(nne, cuda, b, c, hq, hkv, d, bias):
     T.assert_close(host(v), rv, what="v")
 
 
+@pytest.mark.parametrize("seed", range(12))
+def test_qkv_rope_random_shapes(nne, cuda, seed):
+    """Seeded random prologue shapes: d_model any multiple of 64 up to 3072 (one
+    chunk to 48, so C splits into 1 to 8 slices), head dims 64 to 256 (1 to 4
+    tiles per head), 1 to 4 KV heads with group sizes 1, 2 and 4, 1 to 100 rows
+    (more than 64: two launches), with and without bias."""
+    rng = np.random.default_rng(9000 + seed)
+    b = int(rng.integers(1, 101))
+    c = 64 * int(rng.integers(1, 49))
+    d = int(rng.choice([64, 128, 192, 256]))
+    hkv = int(rng.integers(1, 5))
+    hq = hkv * int(rng.choice([1, 2, 4]))
+    bias = bool(rng.random() < 0.5)
+    print("case seed=%d b=%d c=%d hq=%d hkv=%d d=%d bias=%d" % (seed, b, c, hq, hkv, d, bias),
+          flush=True)
+    x = rnd(rng, b, c)
+    wq, wk, wv = weights(rng, hq * d, c), weights(rng, hkv * d, c), weights(rng, hkv * d, c)
+    bq, bk, bv = ((rnd(rng, hq * d, scale=0.1), rnd(rng, hkv * d, scale=0.1),
+                   rnd(rng, hkv * d, scale=0.1)) if bias else (None, None, None))
+    max_len = 300
+    pos = rng.integers(0, max_len, b).astype(np.int32)
+    rope = nne.RotaryEmbedding(d, max_len, device=cuda)
+    packed = nne.qkv_pack(dev(wq, cuda), dev(wk, cuda), dev(wv, cuda), hq, hkv)
+    q, k, v = nne.qkv_rope(dev(x, cuda), packed,
+                           None if bq is None else dev(bq, cuda),
+                           None if bk is None else dev(bk, cuda),
+                           None if bv is None else dev(bv, cuda), rope, dev(pos, cuda), pos, hq,
+                           hkv)
+    rq, rk, rv = T.ref_qkv_rope(x[:, None, :], wq, wk, wv, bq, bk, bv, rope.cos_host,
+                                rope.sin_host, pos, hq, hkv)
+    T.assert_close(host(q), rq, what="q seed %d" % seed)
+    T.assert_close(host(k), rk, what="k seed %d" % seed)
+    T.assert_close(host(v), rv, what="v seed %d" % seed)
+
+
 def test_qkv_rope_llama7b_shapes(nne, cuda):
     """Config-3 projection shapes: B = 32, C = 4096, Hq = 32, Hkv = 8, d = 128."""
     rng = np.random.default_rng(3)
