@@ -13,10 +13,14 @@ same line carries:
   * decode   -- config 3: 64 single-token decode steps (append + attend) over
     a ragged KV cache, B=32, Hq=32, Hkv=8, d=128, L0 ~ U[512, 4096], as KV-read
     GB/s against HBM peak (8 TB/s);
-  * cpu_baseline -- the CPU restatement of the reference's GQA attention path
-    (oracle/oracle.c, a "port"), timed on this host's cores on a bounded sample
-    of the same workload, with as many threads as Rayon's global pool would
-    take here (the available parallelism: affinity mask and cgroup quota);
+  * cpu_baseline -- the reference's own CPU path for GQA attention restated in
+    C (oracle/rayon_path.c, a "port": its AVX2/FMA GEMM and GEMV kernels, Rayon
+    splits, repeat-KV, mask, softmax; Tensor::cat of the cache for decode),
+    timed on this host's cores on a bounded sample of the same workload, with
+    as many threads as Rayon's global pool would take here (the available
+    parallelism: affinity mask and cgroup quota).  The flash legs (configs 1,
+    4, 5a) time the oracle's flash_attention_forward, which is scalar like the
+    reference's;
   * other_configs -- configs 1, 4, 5a and 5b and the decode layer steps, each
     with its own kernel time, roofline fraction and cpu_baseline.
 
@@ -212,34 +216,54 @@ def bench_decode(nne, torch, dev, steps=64, warmup=4, seed=0x5EED0003, hq=32, hk
             "config": {"workload": workload}}
 
 
-def cpu_baseline(target_seconds=15.0):
-    """Oracle (CPU restatement of llama.rs:253-296) on a bounded sample of config 2."""
-    import numpy as np
+RP_RESTATES = ("gemm_2d_a_bt_avx2_fma_parallel / gemv_a_bt_m1_avx2_fma_parallel (QK^T) and "
+               "gemm_2d_avx2_fma_parallel / gemv_m1_avx2_fma (PV) under the batched matmul "
+               "drivers, matmul.rs:30-80, 87-560, 749-1056, 1112-1318; softmax fast path with "
+               "find_row_max_avx2 / scale_row_avx2, reduce.rs:234-330; repeat-KV as Storage::zeros "
+               "+ broadcast add, llama.rs:256-266, ops.rs:43-84; the -1e4 mask as a broadcast add, "
+               "llama.rs:277-292; to_contiguous gathers, mod.rs:184-197")
+
+
+def _rp():
     sys.path.insert(0, os.path.join(ROOT, "tests"))
     import nne_testlib as T
+    return T
+
+
+def _components(times, digits=4):
+    return {k: round(v, digits) for k, v in times.items() if v > 0}
+
+
+def cpu_baseline(reps=2):
+    """Config 2 on the reference's own CPU path for GQA attention
+    (llama.rs:253-296 through its AVX2/FMA GEMMs, oracle/rayon_path.c): one of
+    the 4 batch elements (all 32 query and 8 KV heads, T = 2048), median of
+    reps calls."""
+    import numpy as np
+    T = _rp()
     threads = cpu_threads()
-    t, d, hkv_s = 2048, 128, 1
+    b, hq, hkv, t, d = 1, 32, 8, 2048, 128
     rng = np.random.default_rng(0x5EED0002)
     s = rng.uniform(0.5, 1.5, size=t).astype(np.float32)
-    # one batch element, growing numbers of query heads sharing one KV head
-    k = rng.standard_normal((1, hkv_s, t, d)).astype(np.float32) * s[None, None, :, None]
-    v = rng.standard_normal((1, hkv_s, t, d)).astype(np.float32)
-    heads = max(16, threads)
-    while True:
-        q = rng.standard_normal((1, heads, t, d)).astype(np.float32) * s[None, None, :, None]
+    q = rng.standard_normal((b, hq, t, d), dtype=np.float32) * s[None, None, :, None]
+    k = rng.standard_normal((b, hkv, t, d), dtype=np.float32) * s[None, None, :, None]
+    v = rng.standard_normal((b, hkv, t, d), dtype=np.float32)
+    runs = []
+    for _ in range(reps):
         t0 = time.perf_counter()
-        T.ref_standard(q, k, v, masked=True, threads=threads)
-        el = time.perf_counter() - t0
-        if el >= target_seconds / 4 or heads >= 1024:
-            break
-        heads *= 2
-    flops = causal_flops(1, heads, t, d)
-    return with_host({"value": round(flops / el / 1e12, 6), "unit": "TFLOP/s", "cores": threads,
-            "kind": "port",
-            "sample": "config 2 GQA causal prefill restated from llama.rs:253-296 "
-                      "(repeat-KV, -1e4 mask, softmax, PV; f32), B=1, %d query heads on one "
-                      "KV head, T=2048, d=128; %.2f s wall; FLOPs counted like the GPU "
-                      "(unmasked pairs only)" % (heads, el)})
+        _, comp = T.rp_attention(q, k, v, mode="gqa", causal=True, threads=threads)
+        runs.append((time.perf_counter() - t0, comp))
+    el, comp = sorted(runs, key=lambda r: r[0])[len(runs) // 2]
+    flops = causal_flops(b, hq, t, d)
+    return with_host({
+        "value": round(flops / el / 1e12, 6), "unit": "TFLOP/s", "cores": threads,
+        "kind": "port", "restates": RP_RESTATES,
+        "sample": "config 2, one of its 4 batch elements (Hq=32, Hkv=8, T=2048, d=128, causal), "
+                  "GroupedQueryAttention::forward_gqa_cached steps 4-7 (llama.rs:253-296) on the "
+                  "reference's CPU path: repeat-KV, QK^T, scale, -1e4 mask, softmax, PV (f32, "
+                  "AVX2/FMA, %d threads), median of %d: %.2f s; FLOPs counted like the GPU "
+                  "(unmasked pairs only)" % (threads, reps, el),
+        "components_s": _components(comp)})
 
 
 def flash_cpu_baseline(b, h, t, d, causal, std, sample, reps=1, seed=0x5EED0004):
@@ -268,37 +292,45 @@ def flash_cpu_baseline(b, h, t, d, causal, std, sample, reps=1, seed=0x5EED0004)
                       sample, threads, "causal" if causal else "non-causal", reps, el)})
 
 
-def cross_cpu_baseline(b=8, h=20, tq=8, tk=1500, d=64, reps=5, seed=0x5EED0005):
-    """Oracle cross-attention core (attention.rs:193-203: scores, softmax, PV
-    over the cached memory K/V) for config 5b on the host cores."""
+def cross_cpu_baseline(b=8, h=20, tq=8, tk=1500, d=64, reps=1, seed=0x5EED0005):
+    """Config 5b in full on the reference's CPU path for cross-attention
+    (attention.rs:193-203): q and the slot's K/V are the transposed views of
+    their [B, T, H, d] projections, so matmul_transposed_b and matmul gather
+    them (to_contiguous) before the AVX2 kernels."""
     import numpy as np
-    sys.path.insert(0, os.path.join(ROOT, "tests"))
-    import nne_testlib as T
+    T = _rp()
     threads = cpu_threads()
     rng = np.random.default_rng(seed)
-    q = rng.standard_normal((b, h, tq, d), dtype=np.float32)
-    k, v = (rng.standard_normal((b, h, tk, d), dtype=np.float32) for _ in range(2))
-    times = []
+    q = rng.standard_normal((b, tq, h, d), dtype=np.float32)
+    k, v = (rng.standard_normal((b, tk, h, d), dtype=np.float32) for _ in range(2))
+    runs = []
     for _ in range(reps):
         t0 = time.perf_counter()
-        T.ref_standard(q, k, v, masked=False, threads=threads)
-        times.append(time.perf_counter() - t0)
-    el = sorted(times)[len(times) // 2]
+        _, comp = T.rp_attention(q, k, v, mode="cross", q_bthd=True, kv_bthd=True,
+                                 threads=threads)
+        runs.append((time.perf_counter() - t0, comp))
+    el, comp = sorted(runs, key=lambda r: r[0])[len(runs) // 2]
     by = (2 * b * h * tk * d + 2 * b * h * tq * d) * 4
-    return with_host({"value": round(by / el / 1e9, 2), "unit": "GB/s", "cores": threads, "kind": "port",
-            "sample": "config 5b in full (B=8, H=20, 8 queries onto 1500 frames, d=64), "
-                      "attention core restated from attention.rs:193-203 (f32), median of "
-                      "%d: %.4f s; bytes counted like the GPU line" % (reps, el)})
+    return with_host({
+        "value": round(by / el / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
+        "restates": RP_RESTATES,
+        "sample": "config 5b in full (B=8, H=20, 8 queries onto 1500 frames, d=64): "
+                  "forward_cross_attention_cached steps 3-5 (attention.rs:193-203) on the "
+                  "reference's CPU path, q/K/V as the transposed views the projections leave "
+                  "(gathered by to_contiguous), scale as a broadcast mul, %d threads, median of "
+                  "%d: %.3f s; bytes counted like the GPU line" % (threads, reps, el),
+        "components_s": _components(comp)})
 
 
-def decode_cpu_baseline(seed=0x5EED0003, n_seq=8, steps=16, shape=(32, 32, 8, 128),
-                        len_range=(512, 4096), label="config 3 decode step"):
-    """Oracle decode step (append, then attend, llama.rs:239-296 with t = 1)
-    on the first n_seq sequences of a decode workload (default config 3),
-    timed on the host cores."""
+def decode_cpu_baseline(seed=0x5EED0003, n_seq=4, steps=2, shape=(32, 32, 8, 128),
+                        len_range=(512, 4096), label="config 3 decode step", mode="gqa"):
+    """Decode steps (t = 1, append then attend) on the reference's CPU path:
+    a ragged batch needs one B = 1 call per sequence (its slots hold one
+    length), each Tensor::cat-ing its K and V slot (ops.rs:215-275) and then
+    attending (llama.rs:239-296 for "gqa", attention.rs:79-122 for "mha").
+    The first n_seq sequences of the workload for `steps` steps."""
     import numpy as np
-    sys.path.insert(0, os.path.join(ROOT, "tests"))
-    import nne_testlib as T
+    T = _rp()
     threads = cpu_threads()
     b, hq, hkv, d = shape
     rng = np.random.default_rng(seed)
@@ -306,53 +338,65 @@ def decode_cpu_baseline(seed=0x5EED0003, n_seq=8, steps=16, shape=(32, 32, 8, 12
     cap = int(lens.max()) + steps
     kc = rng.standard_normal((n_seq, hkv, cap, d), dtype=np.float32)
     vc = rng.standard_normal((n_seq, hkv, cap, d), dtype=np.float32)
-    o = T.oracle()
+    qs = rng.standard_normal((steps, n_seq, hq, d), dtype=np.float32)
+    kns = rng.standard_normal((steps, n_seq, hkv, d), dtype=np.float32)
+    vns = rng.standard_normal((steps, n_seq, hkv, d), dtype=np.float32)
+    t0 = time.perf_counter()
+    _, comp = T.rp_decode_run(qs, kc, vc, lens, kns, vns, mode=mode, threads=threads)
+    el = time.perf_counter() - t0
     total = 0.0
-    el = 0.0
     for i in range(steps):
-        q = rng.standard_normal((n_seq, hq, 1, d), dtype=np.float32)
-        kn = rng.standard_normal((n_seq, hkv, 1, d), dtype=np.float32)
-        vn = rng.standard_normal((n_seq, hkv, 1, d), dtype=np.float32)
-        out = np.zeros((n_seq, hq, 1, d), np.float32)
-        t0 = time.perf_counter()
-        rc = o.oracle_decode_step(T._p(q), T._p(kc), T._p(vc), lens.ctypes.data_as(T._i32),
-                                  T._p(kn), T._p(vn), T._p(out), n_seq, hq, hkv, cap, d, 0, 0.0,
-                                  threads)
-        el += time.perf_counter() - t0
-        assert rc == 0
-        total += float(lens.sum()) * hkv * d * 4 * 2 + 2 * n_seq * hq * d * 4 + n_seq * hkv * d * 8
-    return with_host({"value": round(total / el / 1e9, 2), "unit": "GB/s", "cores": threads, "kind": "port",
-            "sample": "%s (B=%d, Hq=%d, Hkv=%d, d=%d) restated from llama.rs:239-296 (append "
-                      "in place, repeat-KV head mapping, softmax, PV; f32), the first %d sequences "
-                      "(lengths %d-%d), %d steps, %.2f s; bytes counted like the GPU line; "
-                      "the reference's per-step Tensor::cat copy of the cache is not included"
-                      % (label, b, hq, hkv, d, n_seq, int(lens.min()) - steps,
-                         int(lens.max()) - steps, steps, el)})
+        total += float((lens + i + 1).sum()) * hkv * d * 4 * 2 + 2 * n_seq * hq * d * 4 \
+            + n_seq * hkv * d * 8
+    cat_s = comp.get("cat", 0.0)
+    return with_host({
+        "value": round(total / el / 1e9, 4), "unit": "GB/s", "cores": threads, "kind": "port",
+        "restates": "Tensor::cat, ops.rs:215-275 (serial, per element); " + RP_RESTATES,
+        "sample": "%s (B=%d, Hq=%d, Hkv=%d, d=%d): the first %d sequences (lengths %d-%d) for %d "
+                  "steps, one B = 1 call per sequence as the reference must for ragged lengths: "
+                  "Tensor::cat of the K and V slots, then %s on the reference's CPU path (%d "
+                  "threads): %.2f s, of which the cat copies %.2f s; bytes counted like the GPU "
+                  "line" % (label, b, hq, hkv, d, n_seq, int(lens.min()), int(lens.max()), steps,
+                            "repeat-KV, QK^T, scale, softmax, PV" if hq > hkv else
+                            "QK^T, scale, softmax, PV", threads, el, cat_s),
+        "value_without_cat": round(total / max(el - cat_s, 1e-9) / 1e9, 4),
+        "components_s": _components(comp)})
 
 
-def prologue_cpu_baseline(seed=0x5EED0014):
-    """Oracle decode prologue (llama.rs:226-235: q/k/v Linear with bias
-    order of linear.rs:47-57, head split, RotaryEmbedding::apply) for one
-    config-3 step (B = 32 rows, d_model 4096), single-threaded."""
+def prologue_cpu_baseline(seed=0x5EED0014, reps=15):
+    """One config-3 decode prologue step (B = 32 rows) on the reference's CPU
+    path: per sequence (one B = 1 call each) the q/k/v Linear layers
+    (linear.rs:47-57: a GEMV, gemv_a_bt_m1_avx2_fma_parallel, per projection)
+    and RotaryEmbedding::apply on q and k (llama.rs:109-157).  Median of reps
+    steps."""
     import numpy as np
-    sys.path.insert(0, os.path.join(ROOT, "tests"))
-    import nne_testlib as T
+    T = _rp()
+    threads = cpu_threads()
     b, hq, hkv, d = 32, 32, 8, 128
     c = hq * d
     rng = np.random.default_rng(seed)
-    x = rng.standard_normal((b, 1, c), dtype=np.float32)
+    x = rng.standard_normal((b, c), dtype=np.float32)
     w = [rng.standard_normal((h * d, c), dtype=np.float32) * (1.0 / c) ** 0.5 for h in (hq, hkv, hkv)]
     cos, sin = T.ref_rope_tables(4200, d)
     pos = rng.integers(512, 4097, size=b).astype(np.int32)
-    t0 = time.perf_counter()
-    T.ref_qkv_rope(x, w[0], w[1], w[2], None, None, None, cos, sin, pos, hq, hkv)
-    el = time.perf_counter() - t0
-    wbytes = (hq + 2 * hkv) * d * c * 4
-    return with_host({"value": round(wbytes / el / 1e9, 3), "unit": "GB/s", "cores": 1, "kind": "port",
-            "sample": "one config-3 decode prologue (B = 32, d_model 4096, Hq = 32, Hkv = 8, "
-                      "d = 128) restated from llama.rs:226-235 (q/k/v projections, head split, "
-                      "RoPE; f32), one thread: %.2f s, %.2f GFLOP/s; GB/s of weights like the "
-                      "GPU line" % (el, 2.0 * b * c * (hq + 2 * hkv) * d / el / 1e9)})
+    runs = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        _, _, _, comp = T.rp_qkv_rope_run(x, *w, None, None, None, cos, sin, pos, hq, hkv,
+                                          threads=threads)
+        runs.append((time.perf_counter() - t0, comp))
+    el, comp = sorted(runs, key=lambda r: r[0])[len(runs) // 2]
+    pbytes = (hq + 2 * hkv) * d * c * 4 + b * c * 4 + b * (hq + 2 * hkv) * d * 4
+    return with_host({
+        "value": round(pbytes / el / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
+        "restates": "Linear::forward, linear.rs:47-57, via matmul_transposed_b -> "
+                    "gemv_a_bt_m1_avx2_fma_parallel (matmul.rs:888-1056); "
+                    "RotaryEmbedding::apply, llama.rs:109-157 (neg, cat, broadcast mul, add)",
+        "sample": "one config-3 decode prologue step in full (32 rows, d_model 4096, Hq=32, "
+                  "Hkv=8, d=128), one B = 1 call per sequence as the reference runs a ragged "
+                  "batch (each row streams the 100.7 MB of weights again), %d threads, median of "
+                  "%d steps: %.4f s; bytes per step counted like the GPU line" % (threads, reps, el),
+        "components_s": _components(comp, 5)})
 
 
 def bench_decode_layer(nne, torch, dev, steps=32, seed=0x5EED0013):
@@ -710,8 +754,8 @@ def main():
         extra.append(bench_mha_decode_layer(nne, torch, dev))
         if not args.no_cpu:
             cpu_jobs.append((extra[-1], lambda: decode_cpu_baseline(
-                seed=0x5EED0015, n_seq=32, steps=8, shape=(32, 12, 12, 64), len_range=(128, 1024),
-                label="GPT-2-small MHA decode attend")))
+                seed=0x5EED0015, n_seq=16, steps=2, shape=(32, 12, 12, 64), len_range=(128, 1024),
+                label="GPT-2-small MHA decode attend", mode="mha")))
         line["other_configs"] = extra
     if not args.no_cpu:
         print("bench: cpu baseline", file=sys.stderr, flush=True)

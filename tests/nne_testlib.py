@@ -195,6 +195,125 @@ def ref_qkv_rope(x, wq, wk, wv, bq, bk, bv, cos, sin, start_pos, hq, hkv):
     return q, k, v
 
 
+RAYON_LIB = os.path.join(ORACLE_DIR, "librayon_path.so")
+RP_COMPONENTS = ("repeat_kv", "gather", "qk", "scale", "mask", "softmax", "pv", "cat", "free",
+                 "linear", "rope")
+RP_MODES = {"gqa": 0, "mha": 1, "cross": 2}
+_rayon = None
+
+
+def rayon_path():
+    """oracle/librayon_path.so: the timing restatement of the reference's CPU
+    standard-attention path (AVX2/FMA GEMMs, Rayon splits); bench.py's
+    cpu_baseline legs time it.  Checked against the oracle in
+    tests/test_rayon_path.py."""
+    global _rayon
+    if _rayon is None:
+        if not os.path.exists(RAYON_LIB):
+            subprocess.run(["make", "-s", "-C", ORACLE_DIR, "librayon_path.so"], check=True)
+        r = ctypes.CDLL(RAYON_LIB)
+        _d = ctypes.POINTER(ctypes.c_double)
+        _c = ctypes.c_int
+        r.rp_set_threads.argtypes = [_c]
+        r.rp_set_threads.restype = None
+        r.rp_max_threads.restype = _c
+        r.rp_components.restype = _c
+        r.rp_attention.argtypes = [_f, _f, _f, _f] + [_c] * 11 + [_d]
+        r.rp_attention.restype = _c
+        r.rp_decode_run.argtypes = [_f, _f, _f, _i32, _f, _f, _f] + [_c] * 7 + [_f, _f, _d]
+        r.rp_decode_run.restype = _c
+        r.rp_qkv_rope_run.argtypes = [_f] * 9 + [_i32] + [_c] * 5 + [_f, _f, _f, _d]
+        r.rp_qkv_rope_run.restype = _c
+        assert r.rp_components() == len(RP_COMPONENTS)
+        _rayon = r
+    return _rayon
+
+
+def _rp_times(t):
+    return {n: float(t[i]) for i, n in enumerate(RP_COMPONENTS)}
+
+
+def rp_attention(q, k, v, mode="gqa", causal=True, start_pos=0, q_bthd=False, kv_bthd=False,
+                 threads=None):
+    """The reference's standard attention on the CPU path it really runs
+    (llama.rs:253-296 for "gqa", attention.rs:93-122 for "mha",
+    attention.rs:193-203 for "cross").  q [B, Hq, Tq, d], k/v [B, Hkv, Tk, d]
+    as logical shapes; *_bthd passes them as the reference's transposed views
+    of [B, T, H, d] buffers (give the arrays in that memory order).  Returns
+    (context [B, Hq, Tq, d], seconds per component)."""
+    q, k, v = (np.ascontiguousarray(x, dtype=np.float32) for x in (q, k, v))
+    if q_bthd:
+        b, tq, hq, d = q.shape
+    else:
+        b, hq, tq, d = q.shape
+    if kv_bthd:
+        hkv, tk = k.shape[2], k.shape[1]
+    else:
+        hkv, tk = k.shape[1], k.shape[2]
+    r = rayon_path()
+    if threads:
+        r.rp_set_threads(int(threads))
+    out = np.zeros((b, hq, tq, d), np.float32)
+    t = (ctypes.c_double * len(RP_COMPONENTS))()
+    rc = r.rp_attention(_p(q), _p(k), _p(v), _p(out), b, hq, hkv, tq, tk, d, int(q_bthd),
+                        int(kv_bthd), int(start_pos), RP_MODES[mode], int(causal), t)
+    assert rc == 0, rc
+    return out, _rp_times(t)
+
+
+def rp_decode_run(qs, kc, vc, lens, kns, vns, mode="gqa", threads=None, want_cache=False):
+    """steps decode steps (t = 1) as the reference runs a ragged batch: one
+    B = 1 call per sequence, each Tensor::cat-ing its slot, then attending.
+    qs [steps, B, Hq, d]; kc/vc [B, Hkv, cap, d]; kns/vns [steps, B, Hkv, d].
+    Returns (outs [steps, B, Hq, d], seconds per component[, kc', vc'])."""
+    qs, kns, vns, kc, vc = (np.ascontiguousarray(x, dtype=np.float32)
+                            for x in (qs, kns, vns, kc, vc))
+    lens = np.ascontiguousarray(lens, dtype=np.int32)
+    steps, b, hq, d = qs.shape
+    hkv, cap = kc.shape[1], kc.shape[2]
+    r = rayon_path()
+    if threads:
+        r.rp_set_threads(int(threads))
+    outs = np.zeros((steps, b, hq, d), np.float32)
+    t = (ctypes.c_double * len(RP_COMPONENTS))()
+    kend = np.zeros_like(kc) if want_cache else None
+    vend = np.zeros_like(vc) if want_cache else None
+    rc = r.rp_decode_run(_p(qs), _p(kc), _p(vc), lens.ctypes.data_as(_i32), _p(kns), _p(vns),
+                         _p(outs), b, hq, hkv, cap, d, steps, RP_MODES[mode], _po(kend),
+                         _po(vend), t)
+    assert rc == 0, rc
+    if want_cache:
+        return outs, _rp_times(t), kend, vend
+    return outs, _rp_times(t)
+
+
+def rp_qkv_rope_run(x, wq, wk, wv, bq, bk, bv, cos, sin, pos, hq, hkv, threads=None):
+    """The decode prologue as the reference runs a ragged batch: per
+    sequence, the three Linear projections (gemv_a_bt_m1 + bias) and RoPE
+    through its elementwise ops.  x [B, C]; cos/sin [max_pos, d] or None.
+    Returns (q [B, Hq, d], k [B, Hkv, d], v [B, Hkv, d], seconds per
+    component)."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    b, c = x.shape
+    d = wq.shape[0] // hq
+    ws = [np.ascontiguousarray(a, dtype=np.float32) for a in (wq, wk, wv)]
+    bs = [None if a is None else np.ascontiguousarray(a, dtype=np.float32) for a in (bq, bk, bv)]
+    tabs = [None if a is None else np.ascontiguousarray(a, dtype=np.float32) for a in (cos, sin)]
+    pos = np.ascontiguousarray(np.broadcast_to(np.asarray(pos, np.int32), (b,)))
+    r = rayon_path()
+    if threads:
+        r.rp_set_threads(int(threads))
+    q = np.zeros((b, hq, d), np.float32)
+    k = np.zeros((b, hkv, d), np.float32)
+    v = np.zeros((b, hkv, d), np.float32)
+    t = (ctypes.c_double * len(RP_COMPONENTS))()
+    rc = r.rp_qkv_rope_run(_p(x), _p(ws[0]), _p(ws[1]), _p(ws[2]), _po(bs[0]), _po(bs[1]),
+                           _po(bs[2]), _po(tabs[0]), _po(tabs[1]), pos.ctypes.data_as(_i32), b, c,
+                           hq, hkv, d, _p(q), _p(k), _p(v), t)
+    assert rc == 0, rc
+    return q, k, v, _rp_times(t)
+
+
 def assert_close(got, ref, atol=ATOL, rtol=RTOL, what=""):
     got = np.asarray(got, dtype=np.float64)
     ref = np.asarray(ref, dtype=np.float64)
