@@ -235,14 +235,13 @@ def _components(times, digits=4):
 
 
 def cpu_baseline(reps=2):
-    """Config 2 on the reference's own CPU path for GQA attention
-    (llama.rs:253-296 through its AVX2/FMA GEMMs, oracle/rayon_path.c): one of
-    the 4 batch elements (all 32 query and 8 KV heads, T = 2048), median of
-    reps calls."""
+    """Config 2 in full on the reference's own CPU path for GQA attention
+    (llama.rs:253-296 through its AVX2/FMA GEMMs, oracle/rayon_path.c), median
+    of reps calls."""
     import numpy as np
     T = _rp()
     threads = cpu_threads()
-    b, hq, hkv, t, d = 1, 32, 8, 2048, 128
+    b, hq, hkv, t, d = 4, 32, 8, 2048, 128
     rng = np.random.default_rng(0x5EED0002)
     s = rng.uniform(0.5, 1.5, size=t).astype(np.float32)
     q = rng.standard_normal((b, hq, t, d), dtype=np.float32) * s[None, None, :, None]
@@ -258,7 +257,7 @@ def cpu_baseline(reps=2):
     return with_host({
         "value": round(flops / el / 1e12, 6), "unit": "TFLOP/s", "cores": threads,
         "kind": "port", "restates": RP_RESTATES,
-        "sample": "config 2, one of its 4 batch elements (Hq=32, Hkv=8, T=2048, d=128, causal), "
+        "sample": "config 2 in full (B=4, Hq=32, Hkv=8, T=2048, d=128, causal), "
                   "GroupedQueryAttention::forward_gqa_cached steps 4-7 (llama.rs:253-296) on the "
                   "reference's CPU path: repeat-KV, QK^T, scale, -1e4 mask, softmax, PV (f32, "
                   "AVX2/FMA, %d threads), median of %d: %.2f s; FLOPs counted like the GPU "
@@ -292,7 +291,7 @@ def flash_cpu_baseline(b, h, t, d, causal, std, sample, reps=1, seed=0x5EED0004)
                       sample, threads, "causal" if causal else "non-causal", reps, el)})
 
 
-def cross_cpu_baseline(b=8, h=20, tq=8, tk=1500, d=64, reps=1, seed=0x5EED0005):
+def cross_cpu_baseline(b=8, h=20, tq=8, tk=1500, d=64, reps=3, seed=0x5EED0005):
     """Config 5b in full on the reference's CPU path for cross-attention
     (attention.rs:193-203): q and the slot's K/V are the transposed views of
     their [B, T, H, d] projections, so matmul_transposed_b and matmul gather
@@ -322,7 +321,7 @@ def cross_cpu_baseline(b=8, h=20, tq=8, tk=1500, d=64, reps=1, seed=0x5EED0005):
         "components_s": _components(comp)})
 
 
-def decode_cpu_baseline(seed=0x5EED0003, n_seq=4, steps=2, shape=(32, 32, 8, 128),
+def decode_cpu_baseline(seed=0x5EED0003, n_seq=8, steps=4, shape=(32, 32, 8, 128),
                         len_range=(512, 4096), label="config 3 decode step", mode="gqa"):
     """Decode steps (t = 1, append then attend) on the reference's CPU path:
     a ragged batch needs one B = 1 call per sequence (its slots hold one
@@ -754,7 +753,7 @@ def main():
         extra.append(bench_mha_decode_layer(nne, torch, dev))
         if not args.no_cpu:
             cpu_jobs.append((extra[-1], lambda: decode_cpu_baseline(
-                seed=0x5EED0015, n_seq=16, steps=2, shape=(32, 12, 12, 64), len_range=(128, 1024),
+                seed=0x5EED0015, n_seq=32, steps=4, shape=(32, 12, 12, 64), len_range=(128, 1024),
                 label="GPT-2-small MHA decode attend", mode="mha")))
         line["other_configs"] = extra
     if not args.no_cpu:

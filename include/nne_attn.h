@@ -85,6 +85,9 @@ uint64_t nne_stream_resource_bytes(void *stream);
  *             every call leaves the counters it used at zero, so an array
  *             zeroed once with nne_counters_init serves any number of calls
  *             of any entry point.
+ * Alignment: records at least 16-byte aligned (the kernels move them with
+ * 16-byte loads and stores; allocations from hipMalloc are 256-byte aligned),
+ * counters 4-byte aligned -- NNE_EINVAL otherwise.
  * The *_workspace_size queries give what a call needs; one workspace sized
  * for the largest of them serves every call.  Calls that share a workspace
  * must not overlap in time (calls on one stream never do).  A NULL
@@ -228,8 +231,13 @@ int nne_decode_step(const float *q, const int64_t q_strides[4], float *k_cache, 
  * arguments, semantics and errors as nne_decode_step without the workspace:
  * its split-K partial records and arrival counters live in a static device
  * array of NNE_NOALLOC_SCRATCH_BYTES that every GPU the library runs on holds
- * until the process ends, and the call makes no hipMalloc, hipFree or other
- * allocation.  NNE_EINVAL if the step needs more scratch than that (at
+ * until the process ends, and the call makes no device allocation (no
+ * hipMalloc or hipFree; it clears its counters with a fill kernel, not a
+ * memset).  Like nne_decode_step, the call plans the step on the host from
+ * lens_host (split layout, append row) and advances lens_host itself; a HIP
+ * graph captured from one call therefore replays that same step, for the same
+ * lengths, and does not advance to later steps.  NNE_EINVAL if the step needs
+ * more scratch than that (at
  * d = 128 it holds about 7800 (sequence, KV head) pairs with up to 4 query
  * heads per KV head, about 1700 with up to 16).  Every
  * call on a GPU shares that GPU's array: calls that overlap in time on one

@@ -372,9 +372,12 @@ class KVCache:
     Per layer: K and V buffers [B, Hkv, capacity, d] (head-major, rows appended
     in place) and per-sequence lengths kept on the device (read by kernels) and
     on the host (validation, launch sizing).  Sequences may be ragged.
-    ``layers`` is the reference's per-layer slot vector over these buffers."""
+    ``layers`` is the reference's per-layer slot vector over these buffers.
+    With own_workspace=False the decode calls pass no workspace and run on the
+    library's per-stream one instead of the cache's."""
 
-    def __init__(self, num_layers, batch, num_kv_heads, capacity, head_dim, device="cuda"):
+    def __init__(self, num_layers, batch, num_kv_heads, capacity, head_dim, device="cuda",
+                 own_workspace=True):
         import torch
         self.batch, self.num_kv_heads = int(batch), int(num_kv_heads)
         self.capacity, self.head_dim = int(capacity), int(head_dim)
@@ -384,7 +387,7 @@ class KVCache:
         self.lens_dev = [torch.zeros(self.batch, dtype=torch.int32, device=device)
                          for _ in range(num_layers)]
         self.lens_host = [np.zeros(self.batch, dtype=np.int32) for _ in range(num_layers)]
-        self._ws = Workspace(device)
+        self._ws = Workspace(device) if own_workspace else None
         self._engaged = [False] * num_layers    # Some(..) in the reference's slot vector
 
     @property
@@ -447,6 +450,8 @@ class KVCache:
         """The cache's own decode workspace (records and zeroed counters),
         grown to what num_heads query heads need: (pointer argument,
         keep-alive).  The library allocates nothing for these calls."""
+        if self._ws is None:
+            return None, None      # the library's per-stream workspace
         size = NneWorkspaceSize()
         rc = lib().nne_decode_workspace_size(self.batch, num_heads, self.num_kv_heads,
                                              self.head_dim, ctypes.byref(size))

@@ -146,6 +146,10 @@ hipError_t stream_resources(int64_t n, uint64_t ws_bytes, hipStream_t s, uint32_
 int call_workspace(const nne_workspace_t* ws, uint64_t need_bytes, int64_t need_counters,
                    hipStream_t s, void** records, uint32_t** counters, const char* what) {
     if (ws) {
+        if ((ws->records && reinterpret_cast<uintptr_t>(ws->records) % 16) ||
+            (ws->counters && reinterpret_cast<uintptr_t>(ws->counters) % 4))
+            return fail(NNE_EINVAL, "Invalid configuration or argument: %s workspace records must "
+                                    "be 16-byte aligned and counters 4-byte aligned", what);
         if (need_bytes > 0 && (!ws->records || ws->records_bytes < need_bytes))
             return fail(NNE_EINVAL, "Invalid configuration or argument: %s workspace holds %llu "
                                     "record bytes, the call needs %llu", what,

@@ -17,7 +17,9 @@
 // time on one GPU -- on any streams, from any threads -- race and must be
 // serialised by the caller.  The array keeps the last call's contents; each
 // call clears the arrival counters it uses with a fill kernel before its
-// launch (no memset node, so a graph capture of the call replays correctly).
+// launch (a kernel, not a memset).  The call plans the step on the host from
+// lens_host and advances lens_host itself, so a graph captured from one call
+// replays that one step for the same lengths; it does not advance.
 #include <hip/hip_runtime.h>
 
 #include <cstdio>

@@ -88,7 +88,6 @@ __global__ __launch_bounds__(64 * small_waves<D>(), 1) void small_prefill_kernel
     constexpr int NK = SKB / RPI;        // K float4 loads per lane per tile
     constexpr int NH = D / 64;           // V float4 loads per key step
     constexpr int NQ = D / 4;            // Q^T registers per lane
-    constexpr int NB = D / 16;           // 16-dim output blocks
     static_assert(NK == 4 * NH, "K and V loads per tile");
 
     // K slices of the waves during the tile loop, then the waves' partial O.

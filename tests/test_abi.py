@@ -299,6 +299,19 @@ def test_undersized_caller_workspace_is_refused_before_launch(nne):
     assert "counters" in lib.nne_last_error().decode()
 
 
+def test_misaligned_caller_workspace_is_refused_before_launch(nne):
+    lib = nne.lib()
+    lens = np.array([3, 5], np.int32)
+    lp = lens.ctypes.data_as(ctypes.POINTER(ctypes.c_int32))
+    for rec, cnt in ((4096 + 8, 4096), (4096, 4096 + 2)):
+        ws = nne.NneWorkspace(records=rec, records_bytes=1 << 30, counters=cnt, n_counters=1 << 20)
+        rc = lib.nne_decode_step(FAKE, None, FAKE, FAKE, FAKE, lp, FAKE, None, FAKE, None, FAKE,
+                                 None, 2, 4, 2, 16, 16, 0, 0.0, ctypes.byref(ws), None)
+        assert rc == nne.NNE_EINVAL
+        assert "aligned" in lib.nne_last_error().decode()
+        assert list(lens) == [3, 5]
+
+
 def test_integration_build_lists_every_source():
     """The Rust build script in INTEGRATION.md compiles the same sources as
     neural-network-engine_amd/build.py (a missing one would leave symbols

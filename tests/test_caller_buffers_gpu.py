@@ -49,7 +49,10 @@ def test_every_entry_point_on_caller_buffers_allocates_nothing(nne, cuda):
                                                workspace=workspace)
             out["cross"] = nne.attention_forward(qx, kx, vx, False, stream=stream,
                                                  workspace=workspace)
-            cache = nne.KVCache(1, b, hkv, cap, d, device=cuda)
+            # the library leg's cache passes no workspace, so its decode
+            # calls run on the library's per-stream records and counters
+            cache = nne.KVCache(1, b, hkv, cap, d, device=cuda,
+                                own_workspace=workspace is not None)
             cache.k[0].copy_(dev(kc))
             cache.v[0].copy_(dev(vc))
             cache.set_lengths(0, lens)
@@ -68,7 +71,10 @@ def test_every_entry_point_on_caller_buffers_allocates_nothing(nne, cuda):
     got = run(s, ws, "caller")
     assert nne.stream_resource_bytes(s) == 0
     print("case the same calls on the library's workspace", flush=True)
-    ref = run(torch.cuda.current_stream(), None, "library")
+    lib_stream = torch.cuda.Stream(device=cuda)
+    ref = run(lib_stream, None, "library")
+    assert nne.stream_resource_bytes(lib_stream) > 0
+    nne.release_stream(lib_stream)
     for key in got:
         assert np.array_equal(got[key], ref[key]), key
     # and against the oracle

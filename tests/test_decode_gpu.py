@@ -132,6 +132,58 @@ def test_config3_full_batch_one_step(nne, cuda):
     T.assert_close(out, ref, what="config3 full batch")
 
 
+def oracle_step_in_place(q, kc, vc, lens, kn, vn):
+    """The oracle's append + attend, updating kc, vc and lens in place (no
+    copies of the 545 MB caches per step)."""
+    b, hq, _, d = q.shape
+    hkv, cap = kc.shape[1], kc.shape[2]
+    out = np.zeros((b, hq, 1, d), np.float32)
+    rc = T.oracle().oracle_decode_step(T._p(q), T._p(kc), T._p(vc), lens.ctypes.data_as(T._i32),
+                                       T._p(kn), T._p(vn), T._p(out), b, hq, hkv, cap, d, 0, 0.0,
+                                       T._threads())
+    assert rc == 0
+    return out
+
+
+@pytest.mark.parametrize("hq", [32, 64])
+def test_bench_decode_sequence_against_oracle(nne, cuda, hq):
+    """The exact sequence bench.py times for config 3 (Hq = 32) and the G = 8
+    line (Hq = 64): B = 32, Hkv = 8, d = 128, L0 ~ U[512, 4096], 64 append +
+    attend steps queued back to back with no host synchronisation between
+    them, on the bench's own seeded inputs.  Every step's output against the
+    oracle; the cache and lengths bit-exact after the last step.  The cut
+    chunks are re-planned every step as the lengths grow."""
+    import torch
+    seed = 0x5EED0003 if hq == 32 else 0x5EED0016
+    print("case bench decode sequence hq=%d" % hq, flush=True)
+    b, hkv, d, steps, warmup = 32, 8, 128, 64, 4
+    rng = np.random.default_rng(seed)
+    lens0 = rng.integers(512, 4097, size=b).astype(np.int32)
+    cap = 4096 + steps + warmup
+    cache = nne.KVCache(1, b, hkv, cap, d, device=cuda)
+    g = torch.Generator(device=cuda).manual_seed(seed)
+    cache.k[0].normal_(generator=g)
+    cache.v[0].normal_(generator=g)
+    qs = torch.randn(steps, b, hq, 1, d, generator=g, device=cuda)
+    kn = torch.randn(steps, b, hkv, 1, d, generator=g, device=cuda)
+    vn = torch.randn(steps, b, hkv, 1, d, generator=g, device=cuda)
+    kc, vc = host(cache.k[0]), host(cache.v[0])
+    cache.set_lengths(0, lens0)
+    outs = torch.empty(steps, b, hq, 1, d, device=cuda)
+    for i in range(steps):
+        cache.decode_step(0, qs[i], kn[i], vn[i], out=outs[i])
+    got = host(outs)
+    qs_h, kn_h, vn_h = host(qs), host(kn), host(vn)
+    lens = lens0.copy()
+    for i in range(steps):
+        ref = oracle_step_in_place(qs_h[i], kc, vc, lens, kn_h[i], vn_h[i])
+        T.assert_close(got[i], ref, what="bench decode hq=%d step %d" % (hq, i))
+    assert (lens == lens0 + steps).all()
+    assert list(cache.lens_host[0]) == list(lens)
+    assert list(host(cache.lens_dev[0])) == list(lens)
+    assert np.array_equal(host(cache.k[0]), kc) and np.array_equal(host(cache.v[0]), vc)
+
+
 def test_decode_matches_last_row_of_gpu_prefill(nne, cuda):
     """Cached decode == the corresponding row of the causal prefill kernel
     (kv_cache_tests.rs:68-103 pattern), across the two GPU kernels."""

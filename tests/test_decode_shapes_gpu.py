@@ -44,9 +44,9 @@ def run_case(nne, cuda, b, hq, hkv, d, lens, append, seed, cap=None):
         torch.cuda.synchronize()
         assert np.array_equal(cache.lens_host[0], rlens)
         assert np.array_equal(cache.lens_dev[0].cpu().numpy(), rlens)
-        rows = np.arange(b)
-        got_k = cache.k[0].cpu().numpy()
-        assert np.array_equal(got_k[rows, :, lens], rkc[rows, :, lens])
+        # the whole cache: the appended rows and every row that must not move
+        assert np.array_equal(cache.k[0].cpu().numpy(), rkc)
+        assert np.array_equal(cache.v[0].cpu().numpy(), rvc)
     else:
         out = cache.attend(0, qd)
         ref = T.ref_decode_attend(q, kc, vc, lens)
@@ -70,6 +70,28 @@ def test_decode_group_sizes_and_head_dims(nne, cuda, b, hq, hkv, d, append):
     lens = rng.integers(1, 700, size=b)
     lens[0] = 1100                     # one long head split over several workgroups
     run_case(nne, cuda, b, hq, hkv, d, lens, append, seed=hq + d)
+
+
+@pytest.mark.parametrize("b,hq,hkv,d", [
+    (130, 20, 1, 64),      # 20 rows: the 32-row tile
+    (145, 64, 1, 128),     # 64 rows: 4 row groups
+    (160, 96, 1, 64),      # 96 rows: a 64-row launch, then a 32-row one
+    (150, 96, 1, 128),
+    (140, 8, 2, 256),      # d = 256, G = 4
+    (135, 48, 1, 256),     # d = 256, 48 rows: a 32-row launch, then a 16-row one
+])
+@pytest.mark.parametrize("append", [True, False])
+def test_decode_wide_rows_beyond_128_sequences(nne, cuda, b, hq, hkv, d, append):
+    """More than 128 sequences: the flattened prefix is scanned on the GPU and
+    a second kernel merges split heads, zero-fills empty sequences and
+    advances lens.  With row-range launches the later launches read lens
+    after that kernel of the first launch has advanced it."""
+    print("case decode wide b=%d hq=%d hkv=%d d=%d append=%s" % (b, hq, hkv, d, append), flush=True)
+    rng = np.random.default_rng(b * 31 + hq + d)
+    lens = rng.integers(1, 400, size=b)
+    lens[rng.integers(0, b, size=5)] = 0
+    lens[3] = 1500                     # one long head split over several workgroups
+    run_case(nne, cuda, b, hq, hkv, d, lens, append, seed=b + hq + d)
 
 
 @pytest.mark.parametrize("append", [True, False])

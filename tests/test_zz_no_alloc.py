@@ -1,6 +1,6 @@
 """nne_decode_step_noalloc (the decode step on the library's static device
 scratch) against nne_decode_step (caller workspace: records and counters),
-both through the C ABI.
+both through the C ABI, and against the CPU oracle's decode step.
 
 Two calls in a row on the same scratch, the second with a smaller input
 (fewer sequences, fewer heads, a smaller head dim), so a call that read the
@@ -84,18 +84,30 @@ def test_noalloc_decode_step_matches_decode_step(nne, cuda, order):
                                    workspace=ws)
         a, r = runs["noalloc"], runs["reference"]
         T.assert_close(a[0], r[0], what="noalloc output")
+        ref, rkc, rvc, rlens = T.ref_decode_step(q.cpu().numpy(), kc.cpu().numpy(),
+                                                 vc.cpu().numpy(), lens, kn.cpu().numpy(),
+                                                 vn.cpu().numpy())
+        T.assert_close(a[0], ref, what="noalloc output against the oracle")
+        assert np.array_equal(a[1], rkc) and np.array_equal(a[2], rvc)
+        assert np.array_equal(a[3], rlens)
         assert np.array_equal(a[1], r[1]) and np.array_equal(a[2], r[2])
         assert np.array_equal(a[3], lens + 1) and np.array_equal(a[4], lens + 1)
         assert np.array_equal(r[3], lens + 1)
 
 
-def test_noalloc_rejects_steps_beyond_its_scratch(nne):
-    """Refused on the host, before any device work."""
+def test_noalloc_rejects_steps_beyond_its_scratch(nne, cuda):
+    """Refused on the host, before any device work.  Only k_new and v_new are
+    real (small) device tensors; every other pointer is NULL, so if the
+    scratch check ever moved after the argument checks the call would fail
+    on a host NULL check, never on the device."""
+    import torch
     lib = nne.lib()
     lens = np.full(2048, 5, np.int32)
-    rc = lib.nne_decode_step_noalloc(4096, None, 4096, 4096, 4096, lens.ctypes.data_as(_i32p), 4096,
-                                     None, 4096, None, 4096, None, 2048, 128, 8, 64, 128, 0, 0.0,
-                                     None)
+    kn = torch.zeros(16, device=cuda)
+    vn = torch.zeros(16, device=cuda)
+    rc = lib.nne_decode_step_noalloc(None, None, None, None, None, lens.ctypes.data_as(_i32p),
+                                     kn.data_ptr(), None, vn.data_ptr(), None, None, None, 2048,
+                                     128, 8, 64, 128, 0, 0.0, None)
     assert rc == nne.NNE_EINVAL
     assert "scratch" in lib.nne_last_error().decode()
     assert (lens == 5).all()
