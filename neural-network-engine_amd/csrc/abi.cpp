@@ -207,8 +207,8 @@ int run_attention(const float* q, const int64_t* qs_, const int64_t* qst, const 
     const int B = (int)qs_[0], Hq = (int)qs_[1], Tq = (int)qs_[2], d = (int)qs_[3];
     const int Hkv = (int)ks_[1], Tk = (int)ks_[2];
     if ((int64_t)B * Hq * Tq == 0 || d == 0) return NNE_OK;
-    // Head dims above 128 run on the split-K kernel (d <= 256); the MFMA
-    // prefill kernel holds Q^T and O^T of up to 128 dims in registers.
+    // Head dims above 128 (d <= 256) run on the wave-pair MFMA kernel, or on
+    // the split-K kernel when a KV head has few query rows.
     const bool wide = nne::prefill_padded_dim(d) == 0;
     if (wide && nne::splitk_padded_dim(d) == 0)
         return fail(NNE_EINVAL, "Invalid configuration or argument: head dim %d > 256 is not "
@@ -233,7 +233,20 @@ int run_attention(const float* q, const int64_t* qs_, const int64_t* qst, const 
     // The split-K kernel addresses a head's rows with 32-bit byte offsets.
     const bool fits32 = (int64_t)B * Hkv * Tk < INT32_MAX && (int64_t)Tk * kst[2] < (1LL << 30) &&
                         (int64_t)Tk * vst[2] < (1LL << 30);
-    if (wide && (!fits32 || rows > INT32_MAX))
+    if (wide && rows > nne::splitk_max_rows()) {
+        nne::PrefillParams p{};
+        p.q = make_view(q, qst);
+        p.k = make_view(k, kst);
+        p.v = make_view(v, vst);
+        p.o = make_out(o, ost);
+        p.B = B; p.Hq = Hq; p.Hkv = Hkv; p.Tq = Tq; p.Tk = Tk; p.d = d;
+        p.q_offset = qoff;
+        p.qscale = scale * nne::kLog2e;
+        hipError_t e = nne::launch_prefill_wide(p, causal, stream);
+        if (e != hipSuccess) return hip_fail(e, "wide prefill attention launch");
+        return NNE_OK;
+    }
+    if (wide && !fits32)
         return fail(NNE_EINVAL, "Invalid configuration or argument: head dim %d > 128 with %lld "
                                 "keys per call exceeds the split-K kernel's limits (2^31 keys per call, 2^30 "
                                 "floats per head)", d,
@@ -328,7 +341,10 @@ nne_workspace_size_t attention_workspace(const int64_t* qs_, const int64_t* ks_,
     const int qoff = (int)std::max<int64_t>(-(1 << 30), std::min<int64_t>(q_offset, 1 << 30));
     const int64_t rows = (int64_t)(Hq / Hkv) * Tq;
     const int64_t tk = causal ? std::min<int64_t>(Tk, (int64_t)qoff + Tq) : Tk;
-    if (d % 4 == 0 && (wide || (rows <= nne::splitk_max_rows() && tk > 0))) {
+    // Wide head dims with more rows per KV head take the wave-pair kernel,
+    // which needs no workspace.
+    const bool wide_mfma = wide && rows > nne::splitk_max_rows();
+    if (d % 4 == 0 && !wide_mfma && (wide || (rows <= nne::splitk_max_rows() && tk > 0))) {
         const int rp = wide ? wide_rows_per_launch(d, causal) : (int)rows;
         const int Bl = std::min(B, nne::splitk_max_seqs());
         const nne::SplitKWorkspace w =

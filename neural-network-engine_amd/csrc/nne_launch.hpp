@@ -20,6 +20,8 @@ int splitk_rows_per_launch(int d);
 // `vec` selects 16-byte loads/stores: requires dim stride 1, d % 4 == 0,
 // 16-byte aligned base pointers and row/head/batch strides that are multiples of 4.
 hipError_t launch_prefill(PrefillParams p, bool causal, bool vec, hipStream_t stream);
+// Head dims 129..256 (16-byte vector views): the wave-pair MFMA kernel.
+hipError_t launch_prefill_wide(PrefillParams p, bool causal, hipStream_t stream);
 // Key-split plan for a prefill problem too small to fill the device (fills
 // p.n_chunks / p.chunk_tiles; n_chunks stays 0 when the problem is large
 // enough).  The caller then sets p.ws (ws_bytes) and p.cnt (n_counters zeroed

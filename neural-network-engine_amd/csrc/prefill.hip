@@ -47,18 +47,19 @@ namespace nne {
 
 namespace {
 
-template <int D, bool VEC>
+template <int D, bool VEC, int THREADS = 256>
 struct TileLoader {
     // K/V tile of 32 keys x D dims = 8*D float4; 256 threads -> D/32 each.
-    static constexpr int NV = D / 32;
+    static constexpr int NV = 8 * D / THREADS;
     static constexpr int C4 = D / 4;    // float4 columns per row
+    static_assert(NV * THREADS == 8 * D, "whole tile per pass");
     float4 kr[NV], vr[NV];
 
     __device__ __forceinline__ void load(const PrefillParams& p, const float* kb, const float* vb,
                                          int key0, int tid) {
 #pragma unroll
         for (int i = 0; i < NV; ++i) {
-            const int idx = tid + 256 * i;
+            const int idx = tid + THREADS * i;
             const int row = idx / C4, c = (idx % C4) * 4;
             const int key = key0 + row;
             if (VEC) {
@@ -85,7 +86,7 @@ struct TileLoader {
         constexpr int KS = D + 4, VS = D + 8;
 #pragma unroll
         for (int i = 0; i < NV; ++i) {
-            const int idx = tid + 256 * i;
+            const int idx = tid + THREADS * i;
             const int row = idx / C4, c = (idx % C4) * 4;
             *reinterpret_cast<float4*>(ks + row * KS + c) = kr[i];
             *reinterpret_cast<float4*>(vs + row * VS + c) = vr[i];
@@ -454,6 +455,227 @@ __global__ __launch_bounds__(256, (D >= 128 && (SPLIT || !VEC)) ? 1 : 2) void pr
     }
 }
 
+// Head dims 129..256, padded to 256.  Q^T and O^T of 256 dims do not fit one
+// wave's registers beside its K/V operands, so every 32-row unit is served
+// by two waves, one per half of the head dim: wave (unit u, half h) holds
+// Q^T and O^T of dims [128h, 128h + 128).  Per 32-key tile each wave computes
+// the partial S^T over its dims (the d = 128 kernel's 64 MFMAs), the two swap
+// their partials through the K/V stage that is idle during the tile, and
+// both add them -- a + b == b + a, so the pair holds the same S bit for bit
+// and runs the same online softmax -- then each accumulates its half of
+// O^T = V^T P^T.  8 waves (4 units, the 4 (row block, query head) units of
+// the d = 128 kernel) per workgroup and one workgroup per CU: two stages of
+// 32 keys x 256 dims of K and V take 134 KB of LDS.  K/V come from HBM once
+// per KV head and workgroup step, as at d <= 128.
+template <bool CAUSAL>
+__global__ __launch_bounds__(512, 1) void prefill_wide_kernel(const PrefillParams p) {
+    constexpr int D = 256, DH = D / 2;
+    constexpr int KS = D + 4, VS = D + 8;
+    constexpr int STAGE = 32 * KS + 32 * VS;
+    constexpr int NB = DH / 32;          // 32-wide output column blocks per wave
+    constexpr int XW = 16 * 64;          // floats of one wave's partial S^T
+    static_assert(8 * XW <= STAGE, "the partials fit the idle stage");
+    __shared__ __attribute__((aligned(16))) float lds[2 * STAGE];
+
+    const int x = blockIdx.x & 7, q = blockIdx.x >> 3, S = gridDim.x >> 3;
+
+#pragma nounroll
+    for (int j = 0;; ++j) {
+    int head = 0, wgi = 0;
+    const int st = item_at(p, j, x, q, S, head, wgi);
+    if (st == 0) break;
+    if (st == 2) continue;
+    int tid = threadIdx.x;
+    asm volatile("" : "+v"(tid));
+    const int lane = tid & 63, wave = tid >> 6;
+    const int l32 = lane & 31, half = lane >> 5;
+    const int dh = wave >> 2;            // head-dim half of this wave
+    const int bi = head / p.Hkv, kvh = head % p.Hkv;
+
+    const int unit = wgi * 4 + (wave & 3);
+    const bool active = unit < p.n_units;
+    const int rb = active ? unit / p.G : 0;
+    const int g = active ? unit % p.G : 0;
+    const int hq = kvh * p.G + g;
+    const int row0 = rb * 32;
+    const int qrow = row0 + l32;
+
+    const int n_kt = (p.Tk + 31) >> 5;
+    int last_unit = wgi * 4 + 3;
+    if (last_unit > p.n_units - 1) last_unit = p.n_units - 1;
+    const int wg_last_key = last_visible_key(p, last_unit / p.G, CAUSAL);
+    int n_tiles = wg_last_key < 0 ? 0 : (wg_last_key >> 5) + 1;
+    if (n_tiles > n_kt) n_tiles = n_kt;
+    const int wave_last_key = last_visible_key(p, rb, CAUSAL);
+    const int wave_tiles = active ? (wave_last_key < 0 ? 0 : (wave_last_key >> 5) + 1) : 0;
+
+    // Q^T fragment: qf[s] = Q[qrow][dh*128 + half*64 + s] * scale*log2(e)
+    float qf[DH / 2];
+    {
+        const float* qp = p.q.p + bi * p.q.sb + hq * p.q.sh + (int64_t)qrow * p.q.st;
+        const bool rok = active && qrow < p.Tq;
+#pragma unroll
+        for (int s4 = 0; s4 < DH / 8; ++s4) {
+            const int c = dh * DH + half * (DH / 2) + 4 * s4;
+            const float4 t = (rok && c < p.d) ? *reinterpret_cast<const float4*>(qp + c)
+                                              : make_float4(0.f, 0.f, 0.f, 0.f);
+            qf[4 * s4 + 0] = t.x * p.qscale;
+            qf[4 * s4 + 1] = t.y * p.qscale;
+            qf[4 * s4 + 2] = t.z * p.qscale;
+            qf[4 * s4 + 3] = t.w * p.qscale;
+        }
+    }
+
+    const float* kb = p.k.p + bi * p.k.sb + kvh * p.k.sh;
+    const float* vb = p.v.p + bi * p.v.sb + kvh * p.v.sh;
+
+    floatx16 o[NB];
+#pragma unroll
+    for (int b = 0; b < NB; ++b)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) o[b][r] = 0.f;
+    float m_run = kNegInf, l_run = 0.f;
+
+    TileLoader<D, true, 512> ld;
+    if (n_tiles > 0) {
+        ld.load(p, kb, vb, 0, tid);
+        ld.store(lds, lds + 32 * KS, tid);
+    }
+    __syncthreads();
+
+    for (int kt = 0; kt < n_tiles; ++kt) {
+        const bool has_next = kt + 1 < n_tiles;
+        const bool mine = kt < wave_tiles;
+        const float* Ks = lds + (kt & 1) * STAGE;
+        const float* Vs = Ks + 32 * KS;
+        float* other = lds + ((kt + 1) & 1) * STAGE;   // idle until the next tile's store
+        floatx16 s;
+        if (mine) {
+            // Partial S^T = K Q^T over this wave's 128 dims, log2 domain.
+#pragma unroll
+            for (int r = 0; r < 16; ++r) s[r] = 0.f;
+            const float* krow = Ks + l32 * KS + dh * DH + half * (DH / 2);
+            __builtin_amdgcn_s_setprio(1);
+#pragma unroll
+            for (int t = 0; t < DH / 8; ++t) {
+                const float4 kq = *reinterpret_cast<const float4*>(krow + 4 * t);
+                s = __builtin_amdgcn_mfma_f32_32x32x2f32(kq.x, qf[4 * t + 0], s, 0, 0, 0);
+                s = __builtin_amdgcn_mfma_f32_32x32x2f32(kq.y, qf[4 * t + 1], s, 0, 0, 0);
+                s = __builtin_amdgcn_mfma_f32_32x32x2f32(kq.z, qf[4 * t + 2], s, 0, 0, 0);
+                s = __builtin_amdgcn_mfma_f32_32x32x2f32(kq.w, qf[4 * t + 3], s, 0, 0, 0);
+            }
+#pragma unroll
+            for (int i = 0; i < 4; ++i) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+#pragma unroll
+            for (int i = 0; i < DH / 8 - 4; ++i) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
+                __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+            }
+            __builtin_amdgcn_sched_group_barrier(0x008, 16, 0);
+            __builtin_amdgcn_s_setprio(0);
+            // This wave's partial, register-group major (each store one
+            // contiguous, conflict-free 1 KB wave access).
+            float* xo = other + wave * XW + 4 * lane;
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                *reinterpret_cast<float4*>(xo + 256 * i) =
+                    make_float4(s[4 * i], s[4 * i + 1], s[4 * i + 2], s[4 * i + 3]);
+        }
+        if (has_next) ld.load(p, kb, vb, (kt + 1) * 32, tid);
+        __syncthreads();   // partials visible
+        if (mine) {
+            // Add the partner's partial: wave w pairs with wave w ^ 4.
+            const float* xi = other + (wave ^ 4) * XW + 4 * lane;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const float4 t = *reinterpret_cast<const float4*>(xi + 256 * i);
+                s[4 * i] += t.x;
+                s[4 * i + 1] += t.y;
+                s[4 * i + 2] += t.z;
+                s[4 * i + 3] += t.w;
+            }
+            const int key0 = kt * 32;
+            const bool need_mask = (key0 + 32 > p.Tk) || (CAUSAL && key0 + 31 > row0 + p.q_offset);
+            if (need_mask) {
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const int key = key0 + 8 * (r >> 2) + 4 * half + (r & 3);
+                    const bool vis = key < p.Tk && (!CAUSAL || key <= qrow + p.q_offset);
+                    s[r] = vis ? s[r] : kNegInf;
+                }
+            }
+            // Online softmax with the lazy rescale of the d <= 128 kernel; both
+            // waves of the pair take the same decisions on the same values.
+            float mt = s[0];
+#pragma unroll
+            for (int r = 1; r < 16; ++r) mt = fmaxf(mt, s[r]);
+            mt = pair_max(mt);
+            if (__builtin_amdgcn_ballot_w64(mt > m_run + 8.f) != 0) {
+                const float m_new = fmaxf(m_run, mt);
+                const float alpha = fast_exp2(m_run - ((m_new == kNegInf) ? 0.f : m_new));
+                l_run *= alpha;
+#pragma unroll
+                for (int b = 0; b < NB; ++b)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) o[b][r] *= alpha;
+                m_run = m_new;
+            }
+            const float m_use = (m_run == kNegInf) ? 0.f : m_run;
+            float ls = 0.f;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                s[r] = fast_exp2(s[r] - m_use);
+                ls += s[r];
+            }
+            l_run += ls;
+
+            // O^T += V^T P^T over this wave's 128 output dims.
+            __builtin_amdgcn_s_setprio(1);
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const float* vrow = Vs + (8 * (r >> 2) + 4 * half + (r & 3)) * VS + dh * DH + l32;
+#pragma unroll
+                for (int b = 0; b < NB; ++b)
+                    o[b] = __builtin_amdgcn_mfma_f32_32x32x2f32(vrow[32 * b], s[r], o[b], 0, 0, 0);
+            }
+            constexpr int NVR = 16 * NB / 2;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+#pragma unroll
+            for (int i = 0; i < NVR - 4; ++i) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+                __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+            }
+            __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);
+            __builtin_amdgcn_s_setprio(0);
+        }
+        if (has_next) {
+            __syncthreads();   // every partial read before the stage is refilled
+            ld.store(other, other + 32 * KS, tid);
+        }
+        __syncthreads();
+    }
+
+    const float l_tot = pair_sum(l_run);
+    const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
+    if (active && qrow < p.Tq) {
+        float* op = p.o.p + bi * p.o.sb + hq * p.o.sh + (int64_t)qrow * p.o.st;
+#pragma unroll
+        for (int b = 0; b < NB; ++b) {
+#pragma unroll
+            for (int qq = 0; qq < 4; ++qq) {
+                const int c = dh * DH + 32 * b + 8 * qq + 4 * half;
+                if (c < p.d)
+                    *reinterpret_cast<float4*>(op + c) =
+                        make_float4(o[b][4 * qq] * inv, o[b][4 * qq + 1] * inv,
+                                    o[b][4 * qq + 2] * inv, o[b][4 * qq + 3] * inv);
+            }
+        }
+    }
+    __syncthreads();   // the next item's first tile reuses the LDS stages
+    }
+}
+
 // CUs and resident workgroups per CU of the kernel on the current device.
 template <int D, bool CAUSAL, bool VEC>
 void residency(int& cus, int& per_cu) {
@@ -482,19 +704,12 @@ void residency(int& cus, int& per_cu) {
 // k minimises rounds * k (the time of a round grows with the workgroups that
 // share a CU; one workgroup per CU leaves its SIMDs a single wave, taken as
 // 30 % slower).  Causal problems with enough work pair ranks r and n_wg-1-r
-// so that every super-item costs the same.
-template <int D, bool CAUSAL, bool VEC>
-hipError_t launch_t(PrefillParams p, hipStream_t stream) {
-    if (p.n_chunks > 1 && p.ws && p.cnt) {
-        hipLaunchKernelGGL((prefill_mfma_kernel<D, CAUSAL, VEC, true>),
-                           dim3(8 * ((p.B * p.Hkv * p.part_prefix[p.n_wg] + 7) / 8)), dim3(256), 0, stream, p);
-        return hipGetLastError();
-    }
-    int cus = 0, k_max = 0;
-    residency<D, CAUSAL, VEC>(cus, k_max);
+// so that every super-item costs the same.  Fills p's schedule fields and
+// returns S.
+int persistent_slots(PrefillParams& p, bool causal, int cus, int k_max) {
     const int cu_per_xcd = cus / 8;
     const int64_t heads = (int64_t)p.B * p.Hkv;
-    p.pairing = (CAUSAL && p.n_wg > 1 && heads * ((p.n_wg + 1) / 2) >= (int64_t)cus * k_max) ? 1 : 0;
+    p.pairing = (causal && p.n_wg > 1 && heads * ((p.n_wg + 1) / 2) >= (int64_t)cus * k_max) ? 1 : 0;
     p.n_pairs = p.pairing ? (p.n_wg + 1) / 2 : p.n_wg;
     p.n_super = (int)(heads * p.n_pairs);
     p.per_xcd = (p.n_super + 7) / 8;
@@ -509,7 +724,44 @@ hipError_t launch_t(PrefillParams p, hipStream_t stream) {
     // A partly empty last round costs more than the hardware's own dispatch of
     // one super-item per workgroup (which also covers small problems).
     if (S >= p.per_xcd || (double)p.per_xcd / ((double)best_rounds * S) < 0.97) S = p.per_xcd;
+    return S;
+}
+
+template <int D, bool CAUSAL, bool VEC>
+hipError_t launch_t(PrefillParams p, hipStream_t stream) {
+    if (p.n_chunks > 1 && p.ws && p.cnt) {
+        hipLaunchKernelGGL((prefill_mfma_kernel<D, CAUSAL, VEC, true>),
+                           dim3(8 * ((p.B * p.Hkv * p.part_prefix[p.n_wg] + 7) / 8)), dim3(256), 0, stream, p);
+        return hipGetLastError();
+    }
+    int cus = 0, k_max = 0;
+    residency<D, CAUSAL, VEC>(cus, k_max);
+    const int S = persistent_slots(p, CAUSAL, cus, k_max);
     hipLaunchKernelGGL((prefill_mfma_kernel<D, CAUSAL, VEC, false>), dim3(8 * S), dim3(256), 0, stream, p);
+    return hipGetLastError();
+}
+
+// Head dims 129..256: the wave-pair kernel, one workgroup of 8 waves per CU.
+template <bool CAUSAL>
+hipError_t launch_wide_t(PrefillParams p, hipStream_t stream) {
+    constexpr auto kernel = prefill_wide_kernel<CAUSAL>;
+    static std::atomic<int> cached_cus[64], cached_per[64];
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
+    int cus = cached_cus[dev].load(std::memory_order_acquire);
+    int k_max = cached_per[dev].load(std::memory_order_relaxed);
+    if (cus == 0 || k_max == 0) {
+        if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+            cus < 8)
+            cus = 256;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&k_max, kernel, 512, 0) != hipSuccess ||
+            k_max < 1)
+            k_max = 1;
+        cached_per[dev].store(k_max, std::memory_order_relaxed);
+        cached_cus[dev].store(cus, std::memory_order_release);
+    }
+    const int S = persistent_slots(p, CAUSAL, cus, k_max);
+    hipLaunchKernelGGL(kernel, dim3(8 * S), dim3(512), 0, stream, p);
     return hipGetLastError();
 }
 
@@ -608,6 +860,13 @@ PrefillSplit prefill_split_plan(PrefillParams& p, bool causal, bool vec) {
     r.ws_bytes = grid * (512 + 128 * (uint64_t)D) * 4;
     r.n_counters = p.total;
     return r;
+}
+
+hipError_t launch_prefill_wide(PrefillParams p, bool causal, hipStream_t stream) {
+    derive_schedule(p);
+    if (p.total == 0) return hipSuccess;
+    if (p.d <= 128 || p.d > 256) return hipErrorInvalidValue;
+    return causal ? launch_wide_t<true>(p, stream) : launch_wide_t<false>(p, stream);
 }
 
 hipError_t launch_prefill(PrefillParams p, bool causal, bool vec, hipStream_t stream) {

@@ -320,14 +320,20 @@ def test_stream_release_frees_and_reallocates(nne, cuda):
     (1, 2, 2, 200, 200, 256, True, 0),      # flash causal, d = 256
     (1, 1, 1, 300, 300, 256, False, 0),     # non-causal
     (2, 4, 2, 70, 90, 192, True, 20),       # GQA, bottom-right offset, padded dim
-    (1, 3, 3, 33, 33, 160, True, 0),        # rows of one launch span two heads' positions
-    (2, 8, 2, 8, 500, 256, False, 0),       # few-query cross-attention, d = 256
+    (1, 3, 3, 33, 33, 160, True, 0),        # a 1-row block after a full one
+    (2, 8, 2, 8, 500, 256, False, 0),       # 8 queries x G = 4: one 32-row unit per KV head
     (1, 2, 1, 40, 64, 256, True, -10),      # rows that see no key
+    (1, 8, 2, 257, 257, 256, True, 0),      # GQA, units that straddle workgroups
+    (3, 5, 5, 100, 37, 224, False, 0),      # Tk < Tq, padded dim
+    (1, 4, 4, 64, 1000, 256, True, 936),    # a few rows at the end of a long cache
+    (2, 4, 4, 3, 300, 256, True, 297),      # 3 rows per KV head: split-K kernel
+    (1, 8, 2, 4, 100, 192, False, 0),       # 16 rows per KV head: split-K kernel
 ])
 def test_head_dims_above_128(nne, cuda, b, hq, hkv, tq, tk, d, causal, q_off):
     """flash_attention_forward takes any head dim (flash_attention.rs:39-48):
-    d in (128, 256] runs on the split-K kernel, 16 causal (32 other) rows per
-    launch, each launch over the keys its rows can see."""
+    d in (128, 256] runs on the wave-pair MFMA kernel (each 32-row unit on two
+    waves, one per half of the head dim), or on the split-K kernel when a KV
+    head has at most 16 query rows."""
     print("case wide head dim", b, hq, hkv, tq, tk, d, causal, q_off, flush=True)
     s = 17 * tq + d
     q, k, v = rnd(s, b, hq, tq, d), rnd(s + 1, b, hkv, tk, d), rnd(s + 2, b, hkv, tk, d)
@@ -339,6 +345,45 @@ def test_head_dims_above_128(nne, cuda, b, hq, hkv, tq, tk, d, causal, q_off):
     T.assert_close(got[:, :, r0:], ref, what="d=%d" % d)
     if hq == hkv and tq == tk and q_off == 0:
         T.assert_close(got, T.ref_flash(q, k, v, causal), what="d=%d flash" % d)
+
+
+def test_wide_head_dim_strided_views_and_repeat(nne, cuda):
+    """d = 256 on [B, T, H, d] views (the FlashAttention layer's projections),
+    output written through a strided view; a second call gives the same bits."""
+    import torch
+    print("case wide head dim strided views", flush=True)
+    b, h, t, d = 2, 3, 150, 256
+    rng = np.random.default_rng(61)
+    qt, kt, vt = (rng.standard_normal((b, t, h, d), dtype=np.float32) for _ in range(3))
+    qv, kv, vv = (dev(x, cuda).transpose(1, 2) for x in (qt, kt, vt))
+    out = torch.zeros(b, t, h, d, device=cuda)
+    nne.attention_forward(qv, kv, vv, True, out=out.transpose(1, 2))
+    first = host(out).copy()
+    nne.attention_forward(qv, kv, vv, True, out=out.transpose(1, 2))
+    assert np.array_equal(host(out), first)
+    ref = T.ref_flash(qt.transpose(0, 2, 1, 3), kt.transpose(0, 2, 1, 3),
+                      vt.transpose(0, 2, 1, 3), True)
+    T.assert_close(first.transpose(0, 2, 1, 3), ref, what="d=256 strided")
+
+
+def test_wide_head_dim_long_causal_prefill(nne, cuda):
+    """Causal GQA prefill at T = 4096, d = 256 (Hq = 8, Hkv = 2): rows at the
+    start, middle and end of sampled heads against the oracle (each row over
+    every key it can see), row 0 == V[0] for every head, all finite."""
+    print("case wide head dim T=4096", flush=True)
+    b, hq, hkv, t, d = 1, 8, 2, 4096, 256
+    rng = np.random.default_rng(62)
+    q, k, v = (rng.standard_normal((b, h, t, d), dtype=np.float32) for h in (hq, hkv, hkv))
+    got = host(nne.attention_forward(dev(q, cuda), dev(k, cuda), dev(v, cuda), True))
+    assert np.isfinite(got).all()
+    g = hq // hkv
+    np.testing.assert_allclose(got[0, :, 0], v[0, np.arange(hq) // g, 0], rtol=1e-6, atol=1e-6)
+    for h in (0, 5):
+        for r0 in (0, 2000, 4032):
+            rows = slice(r0, r0 + 64)
+            ref = T.ref_standard(q[:, h:h + 1, rows], k[:, h // g:h // g + 1],
+                                 v[:, h // g:h // g + 1], True, start_pos=r0)
+            T.assert_close(got[:, h:h + 1, rows], ref, what="T=4096 d=256 head %d rows %d" % (h, r0))
 
 
 # Problems of at most one workgroup per CU (one per sequence, query head and
