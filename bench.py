@@ -21,8 +21,9 @@ same line carries:
     parallelism: affinity mask and cgroup quota).  The flash legs (configs 1,
     4, 5a) time the oracle's flash_attention_forward, which is scalar like the
     reference's;
-  * other_configs -- configs 1, 4, 5a and 5b and the decode layer steps, each
-    with its own kernel time, roofline fraction and cpu_baseline.
+  * other_configs -- configs 1, 4, 5a and 5b, a head-dim-256 causal prefill,
+    the G = 8 decode and the decode layer steps, each with its own kernel
+    time, roofline fraction and cpu_baseline.
 
     python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-cpu] [--headline]
 """
@@ -60,6 +61,7 @@ TRAFFIC_PREFILL_CONFIG1 = round(1.1e6 + 0.26e6)
 TRAFFIC_PREFILL_CONFIG4 = round(283.0e6 + 67.1e6)
 TRAFFIC_PREFILL_CONFIG5A = round(186.8e6 + 61.4e6)
 TRAFFIC_DECODE_G8_STEP = round(677.2e6 + 3.25e6)
+TRAFFIC_PREFILL_D256 = None     # not yet measured
 
 
 def cpu_threads():
@@ -576,9 +578,10 @@ def probe(nne, torch, dev):
         nne.attention_forward(q1, k1, v1, True, out=o1)
     torch.cuda.synchronize()
     del q1, k1, v1, o1
-    for (bb, h, tt, causal, std, calls) in ((1, 16, 16384, True, 0.5, 2),    # config 4
-                                            (8, 20, 1500, False, 1.0, 3)):   # config 5a
-        q, k, v = (torch.randn(bb, h, tt, 64, generator=g, device=dev) * std for _ in range(3))
+    for (bb, h, tt, dd, causal, std, calls) in ((1, 16, 16384, 64, True, 0.5, 2),   # config 4
+                                                (8, 20, 1500, 64, False, 1.0, 3),   # config 5a
+                                                (1, 16, 4096, 256, True, 1.0, 3)):  # d = 256
+        q, k, v = (torch.randn(bb, h, tt, dd, generator=g, device=dev) * std for _ in range(3))
         o = torch.empty_like(q)
         for _ in range(calls):
             nne.attention_forward(q, k, v, causal, out=o)
@@ -604,8 +607,8 @@ def main():
                     help="counter-collection run: a 1 GiB device copy (calibrates FETCH_SIZE/"
                          "WRITE_SIZE), 3 config-2 prefills, 8 config-3 decode steps, 6 "
                          "config-5b cross-attention calls, 6 config-3 and 6 GPT-2 decode layer "
-                         "steps, 6 config-1 prefills, 2 config-4 and 3 config-5a prefills, 8 "
-                         "G=8 decode steps")
+                         "steps, 6 config-1 prefills, 2 config-4, 3 config-5a and 3 d=256 "
+                         "prefills, 8 G=8 decode steps")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
@@ -663,6 +666,7 @@ def main():
             "config1": (1, 4, 256, 64, True, 1.0),
             "config4": (1, 16, 16384, 64, True, 0.5),
             "config5a": (8, 20, 1500, 64, False, 1.0),
+            "d256": (1, 16, 4096, 256, True, 1.0),
         }.items():
             q = torch.randn(bb, h, tt, dd, generator=g, device=dev) * std
             k = torch.randn(bb, h, tt, dd, generator=g, device=dev) * std
@@ -670,7 +674,8 @@ def main():
             o = torch.empty_like(q)
             ms_c, kms_c = time_prefill(nne, torch, q, k, v, causal, max(3, args.steps // 2), 2, o)
             fl = causal_flops(bb, h, tt, dd) if causal else full_flops(bb, h, tt, tt, dd)
-            rec = {"workload": name}
+            rec = {"workload": name if name != "d256" else
+                   "d256: causal prefill, head dim 256 (wave-pair kernel), B=1 H=16 T=4096 f32"}
             if name == "config1":
                 # A ~15 us call: host-paced events measure Python's issue
                 # rate, so the device rate is taken with the calls queued.
@@ -690,7 +695,8 @@ def main():
                                      "flops": fl,
                                      "traffic": {"config1": TRAFFIC_PREFILL_CONFIG1,
                                                  "config4": TRAFFIC_PREFILL_CONFIG4,
-                                                 "config5a": TRAFFIC_PREFILL_CONFIG5A}[name]}})
+                                                 "config5a": TRAFFIC_PREFILL_CONFIG5A,
+                                                 "d256": TRAFFIC_PREFILL_D256}[name]}})
             if not args.no_cpu:
                 # Bounded samples of the same workload (a few seconds each).
                 cpu_jobs.append((rec, {
@@ -703,6 +709,9 @@ def main():
                     "config5a": lambda: flash_cpu_baseline(1, 20, 1500, 64, False, 1.0,
                                                            "one of the 8 batch elements of "
                                                            "config 5a (H=20, T=1500, d=64)"),
+                    "d256": lambda: flash_cpu_baseline(1, 16, 2048, 256, True, 1.0,
+                                                       "the d = 256 line at half its length "
+                                                       "(B=1, H=16, T=2048, d=256)"),
                 }[name]))
             extra.append(rec)
             if name == "config5a":

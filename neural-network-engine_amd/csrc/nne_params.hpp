@@ -52,6 +52,13 @@ struct PrefillParams {
     int n_pairs;
     int n_super;
     int per_xcd;
+    // One item per workgroup (hardware dispatch) of a causal problem whose
+    // XCDs hold whole KV heads: items are taken longest first across the
+    // XCD's order_hpx heads, and while the XCD's items fit two per CU
+    // (order_cu CUs per XCD) the two workgroups of a CU get complementary
+    // lengths.  order_cu = 0: items in head-major rank order.
+    int order_cu;
+    int order_hpx;
     // Key split for problems too small to fill the chip (n_chunks > 1): the
     // key tiles of every work item are cut into chunks of chunk_tiles tiles,
     // one workgroup per (item, chunk); each leaves a partial (max, sum, O)

@@ -386,6 +386,32 @@ def test_wide_head_dim_long_causal_prefill(nne, cuda):
             T.assert_close(got[:, h:h + 1, rows], ref, what="T=4096 d=256 head %d rows %d" % (h, r0))
 
 
+@pytest.mark.parametrize("hq,hkv,t,d", [
+    (32, 8, 2048, 128),     # two workgroups on every CU, complementary lengths
+    (8, 8, 6144, 64),       # 48 items per XCD: 16 CUs with one, 16 with two
+    (8, 8, 2048, 128),      # fewer items than CUs
+    (8, 8, 12288, 64),      # beyond two per CU: longest first
+])
+def test_causal_item_order_without_pairing(nne, cuda, hq, hkv, t, d):
+    """Causal problems too small for paired items run one item per workgroup
+    in the longest-first order, with complementary lengths on the CUs that
+    take two.  Sampled rows (start, middle, end) of sampled heads against the
+    oracle, every output finite, row 0 = V[0]."""
+    print("case causal item order", hq, hkv, t, d, flush=True)
+    rng = np.random.default_rng(hq * t + d)
+    q, k, v = (rng.standard_normal((1, h, t, d), dtype=np.float32) for h in (hq, hkv, hkv))
+    got = host(nne.attention_forward(dev(q, cuda), dev(k, cuda), dev(v, cuda), True))
+    assert np.isfinite(got).all()
+    g = hq // hkv
+    np.testing.assert_allclose(got[0, :, 0], v[0, np.arange(hq) // g, 0], rtol=1e-6, atol=1e-6)
+    for h in (0, hq - 1):
+        for r0 in (0, t // 2 - 32, t - 64):
+            rows = slice(r0, r0 + 64)
+            ref = T.ref_standard(q[:, h:h + 1, rows], k[:, h // g:h // g + 1],
+                                 v[:, h // g:h // g + 1], True, start_pos=r0)
+            T.assert_close(got[:, h:h + 1, rows], ref, what="order head %d rows %d" % (h, r0))
+
+
 # Problems of at most one workgroup per CU (one per sequence, query head and
 # 16-row block) with at most two 16-key tiles per wave run on the small
 # prefill kernel: the waves of a workgroup take one row block's key tiles and
