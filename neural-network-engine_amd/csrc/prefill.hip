@@ -259,17 +259,29 @@ __global__ __launch_bounds__(256, (D >= 128 && (SPLIT || !VEC)) ? 1 : 2) void pr
         for (int r = 0; r < 16; ++r) o[b][r] = 0.f;
     float m_run = kNegInf, l_run = 0.f;
 
+    // The second item of a causal pair walks its key tiles backwards.  The
+    // workgroups of an XCD then stand at only two key positions at any time
+    // -- t on their first (long) items, total - t on their second (short)
+    // ones, whatever their ranks -- so the head's K/V tiles they read stay in
+    // the XCD's L2.  Walked forwards, every second item restarts at key 0 at
+    // its own time and the walks spread over the whole head: config 4 read
+    // 284 MB from HBM, 249 MB backwards (201 MB algorithmic); same time.
+    const bool rev = !SPLIT && p.pairing && (j & 1);
+    const int kstep = rev ? -1 : 1;
+    const int kfirst = rev ? t1 - 1 : t0;
+    const int n_it = t1 - t0;
     TileLoader<D, VEC> ld;
-    if (t1 > t0) {
-        ld.load(p, kb, vb, t0 * 32, tid);
+    if (n_it > 0) {
+        ld.load(p, kb, vb, kfirst * 32, tid);
         ld.store(lds, lds + 32 * KS, tid);
     }
     __syncthreads();
 
-    for (int kt = t0; kt < t1; ++kt) {
-        const bool has_next = kt + 1 < t1;
+    for (int it = 0; it < n_it; ++it) {
+        const int kt = kfirst + kstep * it;
+        const bool has_next = it + 1 < n_it;
         const bool mine = kt < wave_tiles;
-        const float* Ks = lds + ((kt - t0) & 1) * STAGE;
+        const float* Ks = lds + (it & 1) * STAGE;
         const float* Vs = Ks + 32 * KS;
         floatx16 s;
         if (mine) {
@@ -303,7 +315,7 @@ __global__ __launch_bounds__(256, (D >= 128 && (SPLIT || !VEC)) ? 1 : 2) void pr
         }
         // The next tile's loads are issued after the QK^T MFMAs, so their
         // registers and the K operands are never live at the same time.
-        if (has_next) ld.load(p, kb, vb, (kt + 1) * 32, tid);
+        if (has_next) ld.load(p, kb, vb, (kt + kstep) * 32, tid);
         if (mine) {
             // Mask keys past T_k and (causal) keys after row + q_offset.
             const int key0 = kt * 32;
@@ -369,7 +381,7 @@ __global__ __launch_bounds__(256, (D >= 128 && (SPLIT || !VEC)) ? 1 : 2) void pr
         }
 
         if (has_next) {
-            float* ks = lds + ((kt - t0 + 1) & 1) * STAGE;
+            float* ks = lds + ((it + 1) & 1) * STAGE;
             ld.store(ks, ks + 32 * KS, tid);
         }
         __syncthreads();
@@ -554,19 +566,26 @@ __global__ __launch_bounds__(512, 1) void prefill_wide_kernel(const PrefillParam
         for (int r = 0; r < 16; ++r) o[b][r] = 0.f;
     float m_run = kNegInf, l_run = 0.f;
 
+    // Second items of causal pairs walk their key tiles backwards, as in the
+    // d <= 128 kernel (a head's K/V tiles stay in the XCD's L2: 688 -> 260 MB
+    // read at B = 1, H = 16, T = 4096).
+    const bool rev = p.pairing && (j & 1);
+    const int kstep = rev ? -1 : 1;
+    const int kfirst = rev ? n_tiles - 1 : 0;
     TileLoader<D, true, 512> ld;
     if (n_tiles > 0) {
-        ld.load(p, kb, vb, 0, tid);
+        ld.load(p, kb, vb, kfirst * 32, tid);
         ld.store(lds, lds + 32 * KS, tid);
     }
     __syncthreads();
 
-    for (int kt = 0; kt < n_tiles; ++kt) {
-        const bool has_next = kt + 1 < n_tiles;
+    for (int it = 0; it < n_tiles; ++it) {
+        const int kt = kfirst + kstep * it;
+        const bool has_next = it + 1 < n_tiles;
         const bool mine = kt < wave_tiles;
-        const float* Ks = lds + (kt & 1) * STAGE;
+        const float* Ks = lds + (it & 1) * STAGE;
         const float* Vs = Ks + 32 * KS;
-        float* other = lds + ((kt + 1) & 1) * STAGE;   // idle until the next tile's store
+        float* other = lds + ((it + 1) & 1) * STAGE;   // idle until the next tile's store
         floatx16 s;
         if (mine) {
             // Partial S^T = K Q^T over this wave's 128 dims, log2 domain.
@@ -599,7 +618,7 @@ __global__ __launch_bounds__(512, 1) void prefill_wide_kernel(const PrefillParam
                 *reinterpret_cast<float4*>(xo + 256 * i) =
                     make_float4(s[4 * i], s[4 * i + 1], s[4 * i + 2], s[4 * i + 3]);
         }
-        if (has_next) ld.load(p, kb, vb, (kt + 1) * 32, tid);
+        if (has_next) ld.load(p, kb, vb, (kt + kstep) * 32, tid);
         __syncthreads();   // partials visible
         if (mine) {
             // Add the partner's partial: wave w pairs with wave w ^ 4.
