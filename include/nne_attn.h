@@ -119,9 +119,10 @@ int nne_counters_init(uint32_t *counters, uint64_t n, void *stream);
  * only validated (they change the reference's rounding order, not the result).
  * Causal masking is top-left: key c is visible to query row r iff c <= r
  * (:113).  Rows that see no key are zero (:186-194).  `o` has Q's shape.
- * Head dims up to 256; above 128 the tensors must be 16-byte vector views
+ * Any head dim; above 128 the tensors must be 16-byte vector views
  * (d % 4 == 0, unit dim stride, other strides multiples of 4, 16-byte
- * aligned) -- NNE_EINVAL otherwise. */
+ * aligned) -- NNE_EINVAL otherwise.  Above 256 dims a separate kernel runs
+ * (MFMA, K/V read straight into operand layout, no workspace). */
 int nne_flash_attention_forward(const float *q, const int64_t q_shape[4], const int64_t q_strides[4],
                                 const float *k, const int64_t k_shape[4], const int64_t k_strides[4],
                                 const float *v, const int64_t v_shape[4], const int64_t v_strides[4],
@@ -188,19 +189,21 @@ int nne_kv_append(float *k_cache, float *v_cache, int32_t *lens_dev, int32_t *le
                   int64_t d, int64_t t_new, void *stream);
 
 /* Records bytes a decode call of this geometry needs (any cache length; 0
- * for geometry the decode kernel does not take).  Decode calls also need
- * B * Hkv counters: nne_decode_workspace_size gives both. */
+ * for geometry the split-K decode kernel does not take, and for head dims
+ * above 256, whose decode needs no workspace).  Decode calls also need
+ * B * Hkv counters: nne_decode_workspace_size gives both ({0, 0} above 256,
+ * NNE_EINVAL for geometry no decode call takes). */
 uint64_t nne_decode_workspace_bytes(int64_t B, int64_t Hq, int64_t Hkv, int64_t d, int64_t max_len);
 int nne_decode_workspace_size(int64_t B, int64_t Hq, int64_t Hkv, int64_t d,
                               nne_workspace_size_t *out);
 
 /* Single-token decode attention over the cache: q [B, Hq, 1, d] attends to
  * the first lens[b] rows of its sequence, no mask (llama.rs:239-296 with
- * t = 1).  Ragged lengths, any Hq / Hkv, any batch, head dims up to 256
- * (multiples of 4).  With more than 4 query heads per KV head or d > 128, q
- * must be a 16-byte vector view (strides multiples of 4, 16-byte aligned).
- * NNE_EINVAL if capacity * d >= 2^30 (a head's rows are addressed with
- * 32-bit byte offsets).  ws: the caller's
+ * t = 1).  Ragged lengths, any Hq / Hkv, any batch, any head dim that is a
+ * multiple of 4.  With more than 4 query heads per KV head or d > 128, q
+ * must be a 16-byte vector view (strides multiples of 4, 16-byte aligned;
+ * above 256 dims o too).  Up to 256 dims NNE_EINVAL if capacity * d >= 2^30
+ * (a head's rows are addressed with 32-bit byte offsets).  ws: the caller's
  * workspace of at least nne_decode_workspace_size, or NULL for the library's
  * per-stream one. */
 int nne_decode_attention(const float *q, const int64_t q_strides[4], const float *k_cache,
@@ -213,7 +216,8 @@ int nne_decode_attention(const float *q, const int64_t q_strides[4], const float
  * nne_decode_attention -- the append-then-attend order of llama.rs:239-296
  * and attention.rs:79-122 -- fused: the new row is attended from k_new /
  * v_new directly and stored into the cache by the attention kernel, and
- * lens_dev / lens_host advance by one.  ws as for nne_decode_attention.
+ * lens_dev / lens_host advance by one (above 256 dims: the append kernel,
+ * then the attention kernel, in stream order).  ws as for nne_decode_attention.
  * NNE_ECAPACITY (nothing written) if a sequence is full. */
 int nne_decode_step(const float *q, const int64_t q_strides[4], float *k_cache, float *v_cache,
                     int32_t *lens_dev, int32_t *lens_host, const float *k_new,

@@ -525,10 +525,12 @@ class KVCache:
 
 
 def decode_kernel_fits(batch, num_heads, num_kv_heads, head_dim):
-    """True when the fused append + attend kernel takes this geometry (the
-    library reports a workspace size for it)."""
-    return lib().nne_decode_workspace_bytes(max(int(batch), 1), int(num_heads),
-                                            int(num_kv_heads), int(head_dim), 0) > 0
+    """True when the decode step entry point takes this geometry (the library
+    reports a workspace size for it, zero above 256 dims)."""
+    size = NneWorkspaceSize()
+    return lib().nne_decode_workspace_size(max(int(batch), 1), int(num_heads),
+                                           int(num_kv_heads), int(head_dim),
+                                           ctypes.byref(size)) == NNE_OK
 
 
 class FlashAttention:

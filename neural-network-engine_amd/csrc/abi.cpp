@@ -208,11 +208,10 @@ int run_attention(const float* q, const int64_t* qs_, const int64_t* qst, const 
     const int Hkv = (int)ks_[1], Tk = (int)ks_[2];
     if ((int64_t)B * Hq * Tq == 0 || d == 0) return NNE_OK;
     // Head dims above 128 (d <= 256) run on the wave-pair MFMA kernel, or on
-    // the split-K kernel when a KV head has few query rows.
+    // the split-K kernel when a KV head has few query rows; above 256 on the
+    // deep kernel.
     const bool wide = nne::prefill_padded_dim(d) == 0;
-    if (wide && nne::splitk_padded_dim(d) == 0)
-        return fail(NNE_EINVAL, "Invalid configuration or argument: head dim %d > 256 is not "
-                                "supported by the gfx950 attention kernels", d);
+    const bool deep = wide && nne::splitk_padded_dim(d) == 0;
     // Offsets beyond +-2^30 cannot change visibility for int32 lengths.
     const int qoff = (int)std::max<int64_t>(-(1 << 30), std::min<int64_t>(q_offset, 1 << 30));
     const bool vec = d % 4 == 0 && vec_view(q, qst) && vec_view(k, kst) && vec_view(v, vst) &&
@@ -221,6 +220,20 @@ int run_attention(const float* q, const int64_t* qs_, const int64_t* qst, const 
         return fail(NNE_EINVAL, "Invalid configuration or argument: head dim %d > 128 needs a "
                                 "multiple of 4, unit dim strides, strides that are multiples of 4 "
                                 "and 16-byte aligned tensors", d);
+    if (deep) {
+        nne::DeepParams p{};
+        p.q = make_view(q, qst);
+        p.k = make_view(k, kst);
+        p.v = make_view(v, vst);
+        p.o = make_out(o, ost);
+        p.lens = nullptr;
+        p.B = B; p.Hq = Hq; p.Hkv = Hkv; p.G = Hq / Hkv; p.Tq = Tq; p.Tk = Tk; p.d = d;
+        p.q_offset = qoff;
+        p.qscale = scale * nne::kLog2e;
+        hipError_t e = nne::launch_deep(p, causal, stream);
+        if (e != hipSuccess) return hip_fail(e, "deep head-dim attention launch");
+        return NNE_OK;
+    }
     const int G = Hq / Hkv;
     const int64_t rows = (int64_t)G * Tq;
     // Few query rows per KV head (decode-like steps, cross-attention, a few
@@ -392,9 +405,9 @@ int check_kv_cache_args(int64_t B, int64_t Hq, int64_t Hkv, int64_t capacity, in
         return fail(NNE_EINVAL, "Invalid configuration or argument: num_heads (%lld) must be "
                                 "divisible by num_kv_heads (%lld) for GQA",
                     (long long)Hq, (long long)Hkv);
-    if (decode && (d % 4 != 0 || nne::splitk_padded_dim((int)d) == 0))
+    if (decode && d % 4 != 0)
         return fail(NNE_EINVAL, "Invalid configuration or argument: KV cache head dim %lld must be "
-                                "a multiple of 4 and at most 256", (long long)d);
+                                "a multiple of 4", (long long)d);
     return NNE_OK;
 }
 
@@ -659,6 +672,51 @@ uint64_t nne_decode_workspace_bytes(int64_t B, int64_t Hq, int64_t Hkv, int64_t 
 
 namespace nne {
 
+// Decode at head dims above 256 (lengths validated): the step's row is
+// appended by the append kernel (which advances lens_dev), then the deep
+// kernel attends every sequence to its first lens_dev[b] rows.  No workspace.
+int run_decode_deep(const float* q, const int64_t* q_strides, const float* k_cache,
+                    const float* v_cache, const int32_t* lens_dev, int32_t* lens_dev_w,
+                    const float* k_new, const int64_t* kn_strides, const float* v_new,
+                    const int64_t* vn_strides, float* o, const int64_t* o_strides, int64_t B,
+                    int64_t Hq, int64_t Hkv, int64_t capacity, int64_t d, int has_scale,
+                    float scale, hipStream_t s) {
+    const int64_t qshape[4] = {B, Hq, 1, d};
+    const int64_t kvshape[4] = {B, Hkv, 1, d};
+    int64_t c[4], ckv[4];
+    contiguous_strides(qshape, c);
+    contiguous_strides(kvshape, ckv);
+    const int64_t* qst = q_strides ? q_strides : c;
+    const int64_t* ost = o_strides ? o_strides : c;
+    if (!vec_view(q, qst) || !vec_view(o, ost))
+        return fail(NNE_EINVAL, "Invalid configuration or argument: decode q/o at head dim %lld "
+                                "need unit dim stride, 16-byte alignment and strides that are "
+                                "multiples of 4", (long long)d);
+    if (!aligned16(k_cache) || !aligned16(v_cache))
+        return fail(NNE_EINVAL, "Invalid configuration or argument: KV cache must be 16-byte aligned");
+    if (k_new) {
+        const nne::View4 kn = make_view(k_new, kn_strides ? kn_strides : ckv);
+        const nne::View4 vn = make_view(v_new, vn_strides ? vn_strides : ckv);
+        hipError_t e = nne::launch_kv_append(const_cast<float*>(k_cache), const_cast<float*>(v_cache),
+                                             lens_dev_w, kn, vn, (int)B, (int)Hkv, (int)capacity,
+                                             (int)d, 1, s);
+        if (e != hipSuccess) return hip_fail(e, "decode append launch");
+    }
+    nne::DeepParams p{};
+    p.q = make_view(q, qst);
+    const int64_t kst[4] = {Hkv * capacity * d, capacity * d, d, 1};
+    p.k = make_view(k_cache, kst);
+    p.v = make_view(v_cache, kst);
+    p.o = make_out(o, ost);
+    p.lens = lens_dev;
+    p.B = (int)B; p.Hq = (int)Hq; p.Hkv = (int)Hkv; p.G = (int)(Hq / Hkv); p.Tq = 1;
+    p.Tk = (int)capacity; p.d = (int)d;
+    p.qscale = softmax_scale(has_scale, scale, d) * nne::kLog2e;
+    hipError_t e = nne::launch_deep(p, false, s);
+    if (e != hipSuccess) return hip_fail(e, "decode attention launch");
+    return NNE_OK;
+}
+
 // Shared body of the decode entry points.  With a NULL workspace or NULL
 // counters the stream's library-side ones are used.
 int run_decode(const float* q, const int64_t* q_strides, const float* k_cache, const float* v_cache,
@@ -691,6 +749,14 @@ int run_decode(const float* q, const int64_t* q_strides, const float* k_cache, c
         max_len = std::max(max_len, (int)L);
         total_keys += L * Hkv;
         seq_lens[(size_t)b] = (int32_t)L;
+    }
+    if (nne::splitk_padded_dim((int)d) == 0) {
+        rc = run_decode_deep(q, q_strides, k_cache, v_cache, lens_dev, lens_dev_w, k_new,
+                             kn_strides, v_new, vn_strides, o, o_strides, B, Hq, Hkv, capacity, d,
+                             has_scale, scale, s);
+        if (rc == NNE_OK && append)
+            for (int64_t b = 0; b < B; ++b) lens_host[b] += 1;
+        return rc;
     }
     if (capacity * d >= (1LL << 30))
         return fail(NNE_EINVAL, "Invalid configuration or argument: KV cache rows of one head "
@@ -762,6 +828,10 @@ int nne_decode_workspace_size(int64_t B, int64_t Hq, int64_t Hkv, int64_t d,
                               nne_workspace_size_t* out) {
     if (!out) return fail(NNE_EINVAL, "Invalid configuration or argument: null output pointer");
     *out = nne_workspace_size_t{0, 0};
+    // Head dims above 256 (the deep kernel) need no workspace.
+    if (B > 0 && Hkv > 0 && Hq > 0 && Hq % Hkv == 0 && d > 256 && d % 4 == 0 && B <= INT32_MAX &&
+        Hq <= INT32_MAX && d <= INT32_MAX)
+        return NNE_OK;
     const uint64_t bytes = nne_decode_workspace_bytes(B, Hq, Hkv, d, 0);
     if (bytes == 0)
         return fail(NNE_EINVAL, "Invalid configuration or argument: no decode kernel for B=%lld "

@@ -22,6 +22,10 @@ int splitk_rows_per_launch(int d);
 hipError_t launch_prefill(PrefillParams p, bool causal, bool vec, hipStream_t stream);
 // Head dims 129..256 (16-byte vector views): the wave-pair MFMA kernel.
 hipError_t launch_prefill_wide(PrefillParams p, bool causal, hipStream_t stream);
+// Head dims above 256 (deep.hip; d % 4 == 0, 16-byte vector views of Q, K,
+// V and O): prefill, cross-attention and decode over a KV cache (p.lens).
+// Fills the schedule fields of p.
+hipError_t launch_deep(DeepParams p, bool causal, hipStream_t stream);
 // Key-split plan for a prefill problem too small to fill the device (fills
 // p.n_chunks / p.chunk_tiles; n_chunks stays 0 when the problem is large
 // enough).  The caller then sets p.ws (ws_bytes) and p.cnt (n_counters zeroed

@@ -74,6 +74,27 @@ struct PrefillParams {
     uint16_t part_prefix[kMaxSplitItems + 1];
 };
 
+// Head dims above 256 (deep.hip), prefill, cross-attention and decode alike.
+// The G * Tq query rows of a KV head are flattened (row r: query head
+// kvh * G + r / Tq, position r % Tq) and cut into 32-row units; a workgroup
+// serves one unit and one chunk of kDeepChunk output dims.  Sequence b has
+// lens[b] keys when lens != null (a KV cache), else Tk; with `causal`, key c
+// is visible to position t iff c <= t + q_offset.
+constexpr int kDeepChunk = 1024;
+
+struct DeepParams {
+    View4 q, k, v;
+    OutView4 o;
+    const int32_t* lens;
+    int B, Hq, Hkv, G, Tq, Tk, d;
+    int q_offset;
+    float qscale;    // softmax scale * log2(e), folded into Q
+    int n_units;     // ceil(G * Tq / 32) per KV head
+    int n_oc;        // ceil(d / kDeepChunk) output chunks per unit
+    int total;       // B * Hkv * n_units * n_oc workgroups
+    int per_xcd;     // ceil(total / 8)
+};
+
 // Fused decode prologue (qkv.hip): rows m < M of x [M, C] (row stride x_rs,
 // unit column stride) times the packed q/k/v weights (n_tiles tiles of 64
 // output columns, C split into S slices of kc_per_slice 64-wide chunks), plus

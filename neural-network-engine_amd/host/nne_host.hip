@@ -639,9 +639,10 @@ Result<RawTensor> KVCache::decode_step(size_t layer_idx, const RawTensor& q, con
     RawTensor out = RawTensor::zeros(q.shape());
     const auto qst = as_i64(q.strides()), ost = as_i64(out.strides());
     const int64_t hq = (int64_t)q.shape()[1];
-    if (nne_decode_workspace_bytes(std::max<int64_t>((int64_t)batch, 1), hq, (int64_t)num_kv_heads,
-                                   (int64_t)head_dim, 0) == 0) {
-        // Geometry the fused kernel does not take (head dim not a multiple of
+    nne_workspace_size_t fits{0, 0};
+    if (nne_decode_workspace_size(std::max<int64_t>((int64_t)batch, 1), hq, (int64_t)num_kv_heads,
+                                  (int64_t)head_dim, &fits) != NNE_OK) {
+        // Geometry the decode step does not take (head dim not a multiple of
         // 4): append, then attend every sequence to its own first lens[b]
         // rows, no mask (llama.rs:239-296 with t = 1), on the general kernel.
         auto kv = update(layer_idx, k_new, v_new);

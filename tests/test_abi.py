@@ -51,14 +51,22 @@ def test_value_length_mismatch(nne):
     assert rc == nne.NNE_ESHAPE
 
 
-def test_head_dim_too_large_is_invalid_argument(nne):
+def test_wide_head_dims_need_vector_views(nne):
+    """Above 128 dims every kernel (split-K, wave pair, and above 256 the
+    deep kernel) reads 16-byte vector rows; other views are refused before
+    any launch."""
     lib = nne.lib()
+    odd = ctypes.c_void_p(4096 + 4)   # 4-byte, not 16-byte, aligned
     s = i64(1, 1, 4, 260)
+    rc = lib.nne_flash_attention_forward(odd, s, None, FAKE, s, None, FAKE, s, None, FAKE, None,
+                                         0, 0, 0.0, 64, 64, None)
+    assert rc == nne.NNE_EINVAL
+    assert "head dim 260 > 128" in lib.nne_last_error().decode()
+    s = i64(1, 1, 4, 1030)
     rc = lib.nne_flash_attention_forward(FAKE, s, None, FAKE, s, None, FAKE, s, None, FAKE, None,
                                          0, 0, 0.0, 64, 64, None)
     assert rc == nne.NNE_EINVAL
-    assert "head dim 260 > 256" in lib.nne_last_error().decode()
-    # above 128 the split-K kernel serves the call: 16-byte vector rows only
+    assert "multiple of 4" in lib.nne_last_error().decode()
     s = i64(1, 1, 4, 130)
     rc = lib.nne_flash_attention_forward(FAKE, s, None, FAKE, s, None, FAKE, s, None, FAKE, None,
                                          0, 0, 0.0, 64, 64, None)
@@ -87,10 +95,11 @@ def test_decode_rejects_bad_geometry(nne):
     rc = lib.nne_decode_attention(FAKE, None, FAKE, FAKE, FAKE, lp, FAKE, None, 1, 4, 4, 8, 18,
                                   0, 0.0, None, None)
     assert rc == nne.NNE_EINVAL
-    # head dim beyond 256
-    rc = lib.nne_decode_attention(FAKE, None, FAKE, FAKE, FAKE, lp, FAKE, None, 1, 4, 4, 8, 260,
-                                  0, 0.0, None, None)
+    # head dim beyond 256 (the deep kernel): q must be a 16-byte vector view
+    rc = lib.nne_decode_attention(ctypes.c_void_p(4096 + 4), None, FAKE, FAKE, FAKE, lp, FAKE,
+                                  None, 1, 4, 4, 8, 260, 0, 0.0, None, None)
     assert rc == nne.NNE_EINVAL
+    assert "16-byte" in lib.nne_last_error().decode()
     # length beyond capacity
     lens[0] = 9
     rc = lib.nne_decode_attention(FAKE, None, FAKE, FAKE, FAKE, lp, FAKE, None, 1, 4, 4, 8, 16,
@@ -101,7 +110,7 @@ def test_decode_rejects_bad_geometry(nne):
 def test_decode_workspace_size(nne):
     lib = nne.lib()
     assert lib.nne_decode_workspace_bytes(1, 4, 3, 64, 100) == 0   # 3 does not divide 4
-    assert lib.nne_decode_workspace_bytes(1, 4, 4, 260, 100) == 0  # head dim > 256
+    assert lib.nne_decode_workspace_bytes(1, 4, 4, 260, 100) == 0  # > 256: none needed
     assert lib.nne_decode_workspace_bytes(1, 4, 4, 30, 100) == 0   # head dim not a multiple of 4
     assert lib.nne_decode_workspace_bytes(1, 4, 4, 256, 100) > 0
     # any group size: rows beyond one launch's 64 go in further launches that
@@ -277,6 +286,10 @@ def test_workspace_size_queries(nne):
     assert size.n_counters == 32 * 8
     assert size.records_bytes == lib.nne_decode_workspace_bytes(32, 32, 8, 128, 4160)
     assert lib.nne_decode_workspace_size(1, 4, 4, 30, ctypes.byref(size)) == nne.NNE_EINVAL
+    # above 256 dims the decode needs no workspace
+    assert lib.nne_decode_workspace_size(4, 8, 2, 512, ctypes.byref(size)) == nne.NNE_OK
+    assert (size.records_bytes, size.n_counters) == (0, 0)
+    assert lib.nne_decode_workspace_size(4, 8, 3, 512, ctypes.byref(size)) == nne.NNE_EINVAL
     assert lib.nne_qkv_workspace_size(4096, 32, 8, 128, ctypes.byref(size)) == nne.NNE_OK
     assert size.records_bytes > 0 and size.n_counters == 48 * 128 // 64
     assert lib.nne_qkv_workspace_size(100, 4, 2, 64, ctypes.byref(size)) == nne.NNE_EINVAL

@@ -8,7 +8,8 @@ is unbounded.  On the split-K kernel these cases take:
   rows over the same K/V blocks (32- and 64-row tiles);
 * more than 64 rows (32 at d = 256): several launches of row ranges, the
   first appending the new row and the later ones reading it from the cache;
-* d up to 256 (16-row tiles with a one-block ring);
+* d up to 256 (16-row tiles with a one-block ring); above 256 the append
+  kernel, then the deep kernel (8 waves per 32-row unit);
 * more than 2048 sequences: launches of 2048 sequences in stream order.
 
 Bar: |gpu - ref| <= 1e-4 + 1e-3 |ref|; cache contents and lengths bit-exact.
@@ -70,6 +71,51 @@ def test_decode_group_sizes_and_head_dims(nne, cuda, b, hq, hkv, d, append):
     lens = rng.integers(1, 700, size=b)
     lens[0] = 1100                     # one long head split over several workgroups
     run_case(nne, cuda, b, hq, hkv, d, lens, append, seed=hq + d)
+
+
+@pytest.mark.parametrize("b,hq,hkv,d,append", [
+    (3, 8, 2, 512, True),      # G = 4
+    (2, 4, 4, 320, False),     # MHA
+    (2, 16, 1, 1028, True),    # MQA, two output chunks
+    (4, 64, 8, 384, True),     # G = 8
+])
+def test_decode_head_dims_above_256(nne, cuda, b, hq, hkv, d, append):
+    print("case decode deep b=%d hq=%d hkv=%d d=%d append=%s" % (b, hq, hkv, d, append), flush=True)
+    rng = np.random.default_rng(hq * 11 + d)
+    lens = rng.integers(1, 400, size=b)
+    lens[0] = 700
+    if not append:
+        lens[-1] = 0                   # an empty sequence attends to nothing: zeros
+    run_case(nne, cuda, b, hq, hkv, d, lens, append, seed=hq + 3 * d)
+
+
+def test_decode_steps_above_256_dims(nne, cuda):
+    """Four decode steps in a row at d = 512 through the cache: each step's
+    output, the whole cache and the lengths against the oracle's steps."""
+    import torch
+    print("case decode deep steps", flush=True)
+    b, hq, hkv, d, cap = 3, 8, 2, 512, 200
+    rng = np.random.default_rng(64)
+    lens = np.array([5, 120, 33], np.int32)
+    kc, vc = rnd(rng, b, hkv, cap, d), rnd(rng, b, hkv, cap, d)
+    cache = nne.KVCache(1, b, hkv, cap, d, device=cuda)
+    cache.k[0].copy_(torch.from_numpy(kc))
+    cache.v[0].copy_(torch.from_numpy(vc))
+    cache.set_lengths(0, lens)
+    for step in range(4):
+        q, kn, vn = rnd(rng, b, hq, 1, d), rnd(rng, b, hkv, 1, d), rnd(rng, b, hkv, 1, d)
+        out = cache.decode_step(0, dev(q, cuda), dev(kn, cuda), dev(vn, cuda))
+        ref, kc, vc, lens = T.ref_decode_step(q, kc, vc, lens, kn, vn)
+        torch.cuda.synchronize()
+        T.assert_close(out.cpu().numpy(), ref, what="d=512 step %d" % step)
+        assert np.array_equal(cache.lens_host[0], lens)
+        assert np.array_equal(cache.k[0].cpu().numpy(), kc)
+        assert np.array_equal(cache.v[0].cpu().numpy(), vc)
+
+
+def dev(x, cuda):
+    import torch
+    return torch.from_numpy(np.ascontiguousarray(x)).to(cuda)
 
 
 @pytest.mark.parametrize("b,hq,hkv,d", [

@@ -347,6 +347,55 @@ def test_head_dims_above_128(nne, cuda, b, hq, hkv, tq, tk, d, causal, q_off):
         T.assert_close(got, T.ref_flash(q, k, v, causal), what="d=%d flash" % d)
 
 
+@pytest.mark.parametrize("b,hq,hkv,tq,tk,d,causal,q_off", [
+    (1, 2, 2, 200, 200, 512, True, 0),      # flash causal, d = 512
+    (1, 1, 1, 150, 150, 260, False, 0),     # a last chunk with 4 valid dims of 8
+    (2, 4, 2, 70, 90, 320, True, 20),       # GQA, bottom-right offset
+    (1, 2, 1, 40, 64, 384, True, -10),      # rows that see no key
+    (2, 8, 2, 8, 300, 512, False, 0),       # 8 queries x G = 4: one unit per KV head
+    (1, 3, 3, 33, 33, 1024, True, 0),       # Q^T of 128 dims per wave in registers
+    (1, 2, 2, 70, 70, 1028, True, 0),       # two output chunks, Q^T beyond 128 dims re-read
+    (1, 1, 1, 64, 100, 2048, False, 0),
+    (3, 5, 5, 100, 37, 768, False, 0),      # Tk < Tq
+    (2, 4, 4, 3, 300, 640, True, 297),      # a few rows at the end of a long cache
+    (1, 8, 2, 257, 257, 512, True, 0),      # GQA, units that straddle query heads
+])
+def test_head_dims_above_256(nne, cuda, b, hq, hkv, tq, tk, d, causal, q_off):
+    """Above 256 dims (the reference's attention takes any head dim,
+    flash_attention.rs:39-48) the deep kernel runs: 8 waves per 32-row unit
+    split S = Q K^T by dims and O = P V by output blocks."""
+    print("case deep head dim", b, hq, hkv, tq, tk, d, causal, q_off, flush=True)
+    s = 19 * tq + d
+    q, k, v = rnd(s, b, hq, tq, d), rnd(s + 1, b, hkv, tk, d), rnd(s + 2, b, hkv, tk, d)
+    got = host(nne.attention_forward(dev(q, cuda), dev(k, cuda), dev(v, cuda), causal,
+                                     q_offset=q_off))
+    r0 = max(0, -q_off) if causal else 0
+    assert not got[:, :, :r0].any()
+    ref = T.ref_standard(q[:, :, r0:], k, v, causal, start_pos=q_off + r0)
+    T.assert_close(got[:, :, r0:], ref, what="d=%d" % d)
+    if hq == hkv and tq == tk and q_off == 0:
+        T.assert_close(got, T.ref_flash(q, k, v, causal), what="d=%d flash" % d)
+
+
+def test_deep_head_dim_strided_views_and_repeat(nne, cuda):
+    """d = 512 on [B, T, H, d] views, output through a strided view; a second
+    call gives the same bits."""
+    import torch
+    print("case deep head dim strided views", flush=True)
+    b, h, t, d = 2, 3, 90, 512
+    rng = np.random.default_rng(63)
+    qt, kt, vt = (rng.standard_normal((b, t, h, d), dtype=np.float32) for _ in range(3))
+    qv, kv, vv = (dev(x, cuda).transpose(1, 2) for x in (qt, kt, vt))
+    out = torch.zeros(b, t, h, d, device=cuda)
+    nne.attention_forward(qv, kv, vv, True, out=out.transpose(1, 2))
+    first = host(out).copy()
+    nne.attention_forward(qv, kv, vv, True, out=out.transpose(1, 2))
+    assert np.array_equal(host(out), first)
+    ref = T.ref_flash(qt.transpose(0, 2, 1, 3), kt.transpose(0, 2, 1, 3),
+                      vt.transpose(0, 2, 1, 3), True)
+    T.assert_close(first.transpose(0, 2, 1, 3), ref, what="d=512 strided")
+
+
 def test_wide_head_dim_strided_views_and_repeat(nne, cuda):
     """d = 256 on [B, T, H, d] views (the FlashAttention layer's projections),
     output written through a strided view; a second call gives the same bits."""

@@ -62,6 +62,8 @@ def test_noalloc_decode_step_matches_decode_step(nne, cuda, order):
         dict(seed=71, b=32, hq=32, hkv=8, d=128, cap=1200, lo=300, hi=1100),
         # then a smaller input on the same scratch: 16-row tile, d = 64
         dict(seed=72, b=5, hq=16, hkv=2, d=64, cap=700, lo=1, hi=650),
+        # above 256 dims: the append kernel and the deep kernel, no scratch
+        dict(seed=73, b=3, hq=8, hkv=2, d=512, cap=300, lo=1, hi=250),
     ]
     for c in cases:
         print("case noalloc", order, c, flush=True)
