@@ -13,25 +13,31 @@
 // two at a time.  Above 256 dims neither fits: a 32-key K/V tile of 512 dims
 // is 128 KB.  Here a workgroup of 8 waves serves one 32-row unit and reads
 // K and V straight from global memory into MFMA operand layout (every byte of
-// a K/V row once per unit, the unit's waves splitting the row between them):
+// a K/V row once per unit and output chunk, the unit's waves splitting the
+// row between them):
 //  * S^T = K Q^T is split over the waves by dims.  Wave w takes the 8-dim
 //    chunks j = w, w + 8, w + 16, ...; lane half h holds dims 8j + 4h ..
 //    8j + 4h + 3 of its row (one 16-byte load), and MFMA c of a chunk pairs
-//    dims 8j + c and 8j + 4 + c.  Q^T of a wave's first 16 chunks stays in
-//    registers; further chunks (d > 1024) are read again each tile.
+//    dims 8j + c and 8j + 4 + c.  Q^T of a wave's first 16 chunks (128 dims)
+//    stays in registers; further chunks (d > 1024) are read again each tile.
 //  * The 8 partial S^T (4 KB each) meet in LDS, double-buffered so one barrier
 //    per tile suffices; every wave adds them in wave order, so all 8 hold the
 //    same S bit for bit and take the same online-softmax decisions.
 //  * O^T += V^T P^T is split over the waves by 32-dim output blocks: wave w
-//    owns blocks w, w + 8, w + 16, w + 24 of the workgroup's 1024-dim output
-//    chunk (64 accumulator registers).  Each V operand load is one 128-byte
-//    row segment per half-wave.
-//  A unit of more than 1024 dims takes one workgroup per output chunk, each
-//  recomputing S.  Workgroup ids go to the 8 XCDs in turn; XCD x takes the
-//  x-th eighth of the (sequence, KV head, unit, chunk) list, so the units of
-//  a KV head, which read the same K/V rows, share an L2, and causal units
-//  are taken longest first.
+//    owns blocks w and w + 8 of the workgroup's 512-dim output chunk (32
+//    accumulator registers).  Each V operand load is one 128-byte row segment
+//    per half-wave.
+//  * The next tile's K (up to 8 chunks) is loaded during the current tile's
+//    exchange, softmax and P V, and a tile's V at its start, under its S.
+//  A unit of more than 512 dims takes one workgroup per output chunk, each
+//  recomputing S (at d = 1024 that is 1.5x the algorithmic MFMA work; holding
+//  O^T of 1024 dims instead spilled registers in the loop).  Workgroup ids go
+//  to the 8 XCDs in turn; XCD x takes the x-th eighth of the (sequence, KV
+//  head, unit, chunk) list, so the units of a KV head, which read the same
+//  K/V rows, share an L2, and causal units are taken longest first.
 #include <hip/hip_runtime.h>
+
+#include <type_traits>
 
 #include "nne_common.hpp"
 #include "nne_launch.hpp"
@@ -41,7 +47,6 @@ namespace nne {
 namespace {
 
 constexpr int DW = 8;                           // waves per workgroup
-constexpr int OB = kDeepChunk / 32 / DW;        // output blocks per wave
 constexpr int XW = 16 * 64;                     // floats of one wave's partial S^T
 
 __device__ __forceinline__ vf4 load4(const float* p) { return *reinterpret_cast<const vf4*>(p); }
@@ -50,10 +55,16 @@ __device__ __forceinline__ int clamp_keys(int64_t x, int tk) {
     return x < 0 ? 0 : (x > tk ? tk : (int)x);
 }
 
-// QC: chunks per wave whose Q^T stays in registers (8 up to d = 512, 16 up
-// to d = 1024); STREAMQ: further chunks read again each tile.
-template <bool CAUSAL, int QC, bool STREAMQ>
+// Per wave: QC chunks of S whose Q^T stays in registers (STREAMQ: further
+// chunks read again each tile) and OB output blocks (the workgroup's output
+// chunk is 32 * DW * OB dims).  KP chunks of the next tile's K are loaded
+// during the current tile, and VP key steps of a tile's V at its start;
+// the rest is loaded in groups of 4 inside its phase.
+template <bool CAUSAL, int QC, int OB, bool STREAMQ>
 __global__ __launch_bounds__(64 * DW, 1) void deep_attention_kernel(const DeepParams p) {
+    constexpr int KP = QC < 8 ? QC : 8;
+    constexpr int VP = OB <= 2 ? 16 : 4;
+    constexpr int CB = 32 * DW;          // dims between a wave's output blocks
     __shared__ __attribute__((aligned(16))) float xs[2 * DW * XW];
 
     const int idx = (blockIdx.x & 7) * p.per_xcd + (blockIdx.x >> 3);
@@ -96,7 +107,7 @@ __global__ __launch_bounds__(64 * DW, 1) void deep_attention_kernel(const DeepPa
     const int nj = (p.d + 7) >> 3;
     const int nq = wave < nj ? ((nj - 1 - wave) >> 3) + 1 : 0;
     const int nbt = (p.d + 31) >> 5;
-    const int gb0 = oc * (kDeepChunk / 32) + wave;
+    const int gb0 = oc * (CB * OB / 32) + wave;
     const int nob = gb0 < nbt ? min(OB, ((nbt - 1 - gb0) >> 3) + 1) : 0;
 
     const float* qp = p.q.p + bi * p.q.sb + hq * p.q.sh + (int64_t)t * p.q.st;
@@ -109,7 +120,45 @@ __global__ __launch_bounds__(64 * DW, 1) void deep_attention_kernel(const DeepPa
 
     const float* kb = p.k.p + bi * p.k.sb + kvh * p.k.sh;
     const float* vb = p.v.p + bi * p.v.sb + kvh * p.v.sh;
-    const int od = oc * kDeepChunk + 32 * wave + l32;   // this lane's dim of output block 0
+    const int od = oc * CB * OB + 32 * wave + l32;   // this lane's dim of output block 0
+
+    // K and V of a tile are read through buffer ranges that start at the
+    // tile's first key and end with the last key of the unit (rows past it
+    // read as zero without a memory access), so no load needs a predicate
+    // and the byte offsets are a lane constant plus a small uniform part.
+    // K columns past d (the odd half of a last 8-dim chunk when d % 8 == 4)
+    // are read from memory next to the row and zeroed; V columns past d read
+    // the row's last float and only reach O columns never stored.
+    auto range = [&](const float* base, int64_t st, int key0) {
+        const int nk = kend - key0 < 32 ? kend - key0 : 32;
+        return __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(base + key0 * st), 0,
+                                                 (uint32_t)nk * (uint32_t)st * 4u, 0x00020000);
+    };
+    const uint32_t k_lane = ((uint32_t)l32 * (uint32_t)p.k.st + 8 * wave + 4 * half) * 4u;
+    auto load_k = [&](__amdgpu_buffer_rsrc_t rk, int i) -> vf4 {
+        if (i >= nq) return vf4{0.f, 0.f, 0.f, 0.f};   // wave-uniform: past the wave's chunks
+        vf4 x = __builtin_bit_cast(
+            vf4, __builtin_amdgcn_raw_buffer_load_b128(rk, k_lane + (uint32_t)(32 * DW * i), 0, 0));
+        if (p.d & 4) {
+            const int c = 8 * (wave + DW * i) + 4 * half;
+            if (c >= p.d) x = vf4{0.f, 0.f, 0.f, 0.f};
+        }
+        return x;
+    };
+    uint32_t v_lane[OB];
+#pragma unroll
+    for (int b = 0; b < OB; ++b) {
+        const int c = od + CB * b < p.d ? od + CB * b : p.d - 1;
+        v_lane[b] = ((uint32_t)(4 * half) * (uint32_t)p.v.st + (uint32_t)c) * 4u;
+    }
+    // (Blocks past the wave's last valid one read clamped columns too: the
+    // loads stay branch-free, and those operands are never used.)
+    auto load_v = [&](__amdgpu_buffer_rsrc_t rv, int j, float (&dst)[OB]) {
+        const uint32_t uni = (uint32_t)(8 * (j >> 2) + (j & 3)) * (uint32_t)p.v.st * 4u;
+#pragma unroll
+        for (int b = 0; b < OB; ++b)
+            dst[b] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rv, v_lane[b], uni, 0));
+    };
 
     floatx16 o[OB];
 #pragma unroll
@@ -118,44 +167,68 @@ __global__ __launch_bounds__(64 * DW, 1) void deep_attention_kernel(const DeepPa
         for (int rr = 0; rr < 16; ++rr) o[b][rr] = 0.f;
     float m_run = kNegInf, l_run = 0.f;
 
+    vf4 kq[KP];
+    if (n_tiles > 0) {
+        const __amdgpu_buffer_rsrc_t rk = range(kb, p.k.st, 0);
+#pragma unroll
+        for (int i = 0; i < KP; ++i)
+            kq[i] = load_k(rk, i);
+    }
+
     for (int it = 0; it < n_tiles; ++it) {
         const int key0 = it * 32;
         float* xb = xs + (it & 1) * (DW * XW);
+
+        // V of the tile's first VP key steps: in flight under the S MFMAs,
+        // the exchange and the softmax.
+        const __amdgpu_buffer_rsrc_t rk = range(kb, p.k.st, key0);
+        const __amdgpu_buffer_rsrc_t rv = range(vb, p.v.st, key0);
+        float vp[VP][OB];
+#pragma unroll
+        for (int j = 0; j < VP; ++j) load_v(rv, j, vp[j]);
+        __builtin_amdgcn_sched_barrier(0);
 
         // Partial S^T = K Q^T over this wave's chunks, log2 domain.
         floatx16 s;
 #pragma unroll
         for (int rr = 0; rr < 16; ++rr) s[rr] = 0.f;
         {
-            // Chunks in groups of 4 (16 registers of K each), the next group's
-            // loads issued before the current group's MFMAs; the scheduling
-            // barriers keep the compiler from hoisting every load of the tile.
-            const bool kok = key0 + l32 < kend;
-            const float* krow = kb + (int64_t)(key0 + l32) * p.k.st;
-            vf4 kq[2][4];
+            vf4 kg[2][4];
+            if (QC > KP) {
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int c = 8 * (wave + DW * i) + 4 * half;
-                kq[0][i] = (kok && i < nq && c < p.d) ? load4(krow + c) : vf4{0.f, 0.f, 0.f, 0.f};
+                for (int i = 0; i < 4; ++i)
+                    kg[0][i] = load_k(rk, KP + i);
             }
+            // Chunks in pairs behind one wave-uniform branch each (a branch
+            // around every accumulating MFMA would copy s each time); chunks
+            // past the wave's count have zero K and Q^T.
 #pragma unroll
-            for (int gi = 0; gi < QC / 4; ++gi) {
-                if (4 * gi < nq) {
-                    if (gi + 1 < QC / 4) {
+            for (int g2 = 0; g2 < KP; g2 += 2) {
+                if (g2 < nq) {
 #pragma unroll
-                        for (int i = 0; i < 4; ++i) {
-                            const int ii = 4 * (gi + 1) + i;
-                            const int c = 8 * (wave + DW * ii) + 4 * half;
-                            kq[(gi + 1) & 1][i] = (kok && ii < nq && c < p.d)
-                                                      ? load4(krow + c)
-                                                      : vf4{0.f, 0.f, 0.f, 0.f};
-                        }
+                    for (int i = g2; i < g2 + 2 && i < KP; ++i) {
+                        s = __builtin_amdgcn_mfma_f32_32x32x2f32(kq[i][0], qf[i][0], s, 0, 0, 0);
+                        s = __builtin_amdgcn_mfma_f32_32x32x2f32(kq[i][1], qf[i][1], s, 0, 0, 0);
+                        s = __builtin_amdgcn_mfma_f32_32x32x2f32(kq[i][2], qf[i][2], s, 0, 0, 0);
+                        s = __builtin_amdgcn_mfma_f32_32x32x2f32(kq[i][3], qf[i][3], s, 0, 0, 0);
+                    }
+                }
+            }
+            __builtin_amdgcn_sched_barrier(0);
+            // Chunks KP.. in groups of 4, the next group's loads issued first.
+#pragma unroll
+            for (int gi = 0; gi < (QC - KP) / 4; ++gi) {
+                if (KP + 4 * gi < nq) {
+                    if (gi + 1 < (QC - KP) / 4) {
+#pragma unroll
+                        for (int i = 0; i < 4; ++i)
+                            kg[(gi + 1) & 1][i] = load_k(rk, KP + 4 * (gi + 1) + i);
                     }
                     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
                     for (int i = 0; i < 4; ++i) {
-                        const vf4 kk = kq[gi & 1][i];
-                        const vf4 qq = qf[4 * gi + i];
+                        const vf4 kk = kg[gi & 1][i];
+                        const vf4 qq = qf[KP + 4 * gi + i];
                         s = __builtin_amdgcn_mfma_f32_32x32x2f32(kk[0], qq[0], s, 0, 0, 0);
                         s = __builtin_amdgcn_mfma_f32_32x32x2f32(kk[1], qq[1], s, 0, 0, 0);
                         s = __builtin_amdgcn_mfma_f32_32x32x2f32(kk[2], qq[2], s, 0, 0, 0);
@@ -169,7 +242,7 @@ __global__ __launch_bounds__(64 * DW, 1) void deep_attention_kernel(const DeepPa
                     const int c = 8 * (wave + DW * i) + 4 * half;
                     const vf4 qq = (active && c < p.d) ? load4(qp + c) * p.qscale
                                                        : vf4{0.f, 0.f, 0.f, 0.f};
-                    const vf4 kk = (kok && c < p.d) ? load4(krow + c) : vf4{0.f, 0.f, 0.f, 0.f};
+                    const vf4 kk = load_k(rk, i);
                     s = __builtin_amdgcn_mfma_f32_32x32x2f32(kk[0], qq[0], s, 0, 0, 0);
                     s = __builtin_amdgcn_mfma_f32_32x32x2f32(kk[1], qq[1], s, 0, 0, 0);
                     s = __builtin_amdgcn_mfma_f32_32x32x2f32(kk[2], qq[2], s, 0, 0, 0);
@@ -177,6 +250,15 @@ __global__ __launch_bounds__(64 * DW, 1) void deep_attention_kernel(const DeepPa
                 }
             }
         }
+        // The next tile's first KP chunks of K: in flight under the exchange,
+        // the softmax and P V.
+        if (it + 1 < n_tiles) {
+            const __amdgpu_buffer_rsrc_t rk1 = range(kb, p.k.st, key0 + 32);
+#pragma unroll
+            for (int i = 0; i < KP; ++i)
+                kq[i] = load_k(rk1, i);
+        }
+        __builtin_amdgcn_sched_barrier(0);
         // Register-group major (each store one contiguous 1 KB wave access).
         {
             float* xo = xb + wave * XW + 4 * lane;
@@ -188,7 +270,8 @@ __global__ __launch_bounds__(64 * DW, 1) void deep_attention_kernel(const DeepPa
         __syncthreads();   // the tile's partials visible
         if (nob == 0) continue;   // no output dims here; the wave still adds its partial
 
-        // S = the partials added in wave order (the same bits in every wave).
+        // S = the partials added in wave order (the same bits in every wave),
+        // one register group (8 LDS reads) at a time.
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             vf4 a = load4(xb + 4 * lane + 256 * i);
@@ -198,6 +281,7 @@ __global__ __launch_bounds__(64 * DW, 1) void deep_attention_kernel(const DeepPa
             s[4 * i + 1] = a[1];
             s[4 * i + 2] = a[2];
             s[4 * i + 3] = a[3];
+            __builtin_amdgcn_sched_barrier(0);
         }
         if (key0 + 32 > kall) {
 #pragma unroll
@@ -232,37 +316,44 @@ __global__ __launch_bounds__(64 * DW, 1) void deep_attention_kernel(const DeepPa
         }
         l_run += ls;
 
-        // O^T += V^T P^T over this wave's output blocks, keys in groups of 4
-        // register steps (16 V operands), the next group's loads issued first.
-        {
-            float vq[2][4][OB];
-            auto load_v = [&](int rg, float (&dst)[4][OB]) {
+        // O^T += V^T P^T over this wave's output blocks: the first VP key
+        // steps from registers, the rest in groups of 4 loaded one group ahead.
+        // One copy of the loop per count of valid blocks, so the MFMAs carry
+        // no per-block branch (a branch around an accumulating MFMA costs a
+        // copy of its 16 accumulator registers).
+        auto pv = [&](auto nbk) {
+            constexpr int NBK = decltype(nbk)::value;
+            float vg[2][4][OB];
+            if (VP < 16) {
 #pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    const int rr = 4 * rg + j;
-                    const int key = key0 + 8 * (rr >> 2) + 4 * half + (rr & 3);
-                    const bool vok = key < kend;
-                    const float* vrow = vb + (int64_t)key * p.v.st + od;
+                for (int j = 0; j < 4; ++j) load_v(rv, VP + j, vg[0][j]);
+            }
 #pragma unroll
-                    for (int b = 0; b < OB; ++b)
-                        dst[j][b] = (vok && b < nob && od + 256 * b < p.d) ? vrow[256 * b] : 0.f;
+            for (int j = 0; j < VP; ++j)
+#pragma unroll
+                for (int b = 0; b < NBK; ++b)
+                    o[b] = __builtin_amdgcn_mfma_f32_32x32x2f32(vp[j][b], s[j], o[b], 0, 0, 0);
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int gi = 0; gi < (16 - VP) / 4; ++gi) {
+                if (gi + 1 < (16 - VP) / 4) {
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) load_v(rv, VP + 4 * (gi + 1) + j, vg[(gi + 1) & 1][j]);
                 }
-            };
-            load_v(0, vq[0]);
-#pragma unroll
-            for (int rg = 0; rg < 4; ++rg) {
-                if (rg + 1 < 4) load_v(rg + 1, vq[(rg + 1) & 1]);
                 __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
                 for (int j = 0; j < 4; ++j)
 #pragma unroll
-                    for (int b = 0; b < OB; ++b)
-                        if (b < nob)
-                            o[b] = __builtin_amdgcn_mfma_f32_32x32x2f32(vq[rg & 1][j][b],
-                                                                        s[4 * rg + j], o[b], 0, 0, 0);
+                    for (int b = 0; b < NBK; ++b)
+                        o[b] = __builtin_amdgcn_mfma_f32_32x32x2f32(vg[gi & 1][j][b],
+                                                                    s[VP + 4 * gi + j], o[b], 0, 0, 0);
                 __builtin_amdgcn_sched_barrier(0);
             }
-        }
+        };
+        if (nob >= OB) pv(std::integral_constant<int, OB>{});
+        else if (OB > 1 && nob == 1) pv(std::integral_constant<int, 1>{});
+        else if (OB > 2 && nob == 2) pv(std::integral_constant<int, (OB > 2 ? 2 : 1)>{});
+        else if (OB > 3 && nob == 3) pv(std::integral_constant<int, (OB > 3 ? 3 : 1)>{});
     }
 
     // ---- normalise and write O[row][dim], dim = 32 gb + 8 (rr/4) + 4 half + rr%4 ----
@@ -275,7 +366,7 @@ __global__ __launch_bounds__(64 * DW, 1) void deep_attention_kernel(const DeepPa
             if (b < nob) {
 #pragma unroll
                 for (int qq = 0; qq < 4; ++qq) {
-                    const int c = od - l32 + 256 * b + 8 * qq + 4 * half;
+                    const int c = od - l32 + CB * b + 8 * qq + 4 * half;
                     if (c < p.d)
                         *reinterpret_cast<vf4*>(op + c) =
                             vf4{o[b][4 * qq] * inv, o[b][4 * qq + 1] * inv,
@@ -286,25 +377,12 @@ __global__ __launch_bounds__(64 * DW, 1) void deep_attention_kernel(const DeepPa
     }
 }
 
-template <bool CAUSAL>
-hipError_t launch_deep_t(const DeepParams& p, hipStream_t stream) {
-    const dim3 grid(8 * p.per_xcd), block(64 * DW);
-    if (p.d <= 8 * DW * 8)
-        hipLaunchKernelGGL((deep_attention_kernel<CAUSAL, 8, false>), grid, block, 0, stream, p);
-    else if (p.d <= 8 * DW * 16)
-        hipLaunchKernelGGL((deep_attention_kernel<CAUSAL, 16, false>), grid, block, 0, stream, p);
-    else
-        hipLaunchKernelGGL((deep_attention_kernel<CAUSAL, 16, true>), grid, block, 0, stream, p);
-    return hipGetLastError();
-}
-
-}  // namespace
-
-hipError_t launch_deep(DeepParams p, bool causal, hipStream_t stream) {
-    if (p.d <= 256 || p.d % 4 != 0 || p.Hkv <= 0 || p.G <= 0) return hipErrorInvalidValue;
+template <bool CAUSAL, int QC, int OB, bool STREAMQ>
+hipError_t launch_deep_v(DeepParams p, hipStream_t stream) {
+    constexpr int CH = 32 * DW * OB;   // output dims per workgroup
     const int64_t rows = (int64_t)p.G * p.Tq;
     const int64_t units = (rows + 31) / 32;
-    const int64_t n_oc = (p.d + kDeepChunk - 1) / kDeepChunk;
+    const int64_t n_oc = (p.d + CH - 1) / CH;
     const int64_t total = (int64_t)p.B * p.Hkv * units * n_oc;
     if (total == 0) return hipSuccess;
     if (total > INT32_MAX - 8) return hipErrorInvalidValue;
@@ -312,6 +390,22 @@ hipError_t launch_deep(DeepParams p, bool causal, hipStream_t stream) {
     p.n_oc = (int)n_oc;
     p.total = (int)total;
     p.per_xcd = (int)((total + 7) / 8);
+    hipLaunchKernelGGL((deep_attention_kernel<CAUSAL, QC, OB, STREAMQ>), dim3(8 * p.per_xcd),
+                       dim3(64 * DW), 0, stream, p);
+    return hipGetLastError();
+}
+
+template <bool CAUSAL>
+hipError_t launch_deep_t(const DeepParams& p, hipStream_t stream) {
+    if (p.d <= 8 * DW * 8) return launch_deep_v<CAUSAL, 8, 2, false>(p, stream);
+    if (p.d <= 8 * DW * 16) return launch_deep_v<CAUSAL, 16, 2, false>(p, stream);
+    return launch_deep_v<CAUSAL, 16, 2, true>(p, stream);
+}
+
+}  // namespace
+
+hipError_t launch_deep(DeepParams p, bool causal, hipStream_t stream) {
+    if (p.d <= 256 || p.d % 4 != 0 || p.Hkv <= 0 || p.G <= 0) return hipErrorInvalidValue;
     return causal ? launch_deep_t<true>(p, stream) : launch_deep_t<false>(p, stream);
 }
 
