@@ -20,9 +20,13 @@
 //    8j + 4h + 3 of its row (one 16-byte load), and MFMA c of a chunk pairs
 //    dims 8j + c and 8j + 4 + c.  Q^T of a wave's first 16 chunks (128 dims)
 //    stays in registers; further chunks (d > 1024) are read again each tile.
-//  * The 8 partial S^T (4 KB each) meet in LDS, double-buffered so one barrier
-//    per tile suffices; every wave adds them in wave order, so all 8 hold the
-//    same S bit for bit and take the same online-softmax decisions.
+//  * The 8 partial S^T (4 KB each) meet in LDS: wave w adds elements
+//    [128w, 128w + 128) of all 8 in wave order and stores the sum, and every
+//    wave then reads the whole S, so all 8 hold the same S bit for bit and
+//    take the same online-softmax decisions.  (Every wave adding all 8
+//    partials itself read 8x the LDS bytes: d = 512 prefill 2.92 -> 2.75 ms
+//    with the split sum.)  Both buffers are double-buffered: two barriers
+//    per tile.
 //  * O^T += V^T P^T is split over the waves by 32-dim output blocks: wave w
 //    owns blocks w and w + 8 of the workgroup's 512-dim output chunk (32
 //    accumulator registers).  Each V operand load is one 128-byte row segment
@@ -66,6 +70,7 @@ __global__ __launch_bounds__(64 * DW, 1) void deep_attention_kernel(const DeepPa
     constexpr int VP = OB <= 2 ? 16 : 4;
     constexpr int CB = 32 * DW;          // dims between a wave's output blocks
     __shared__ __attribute__((aligned(16))) float xs[2 * DW * XW];
+    __shared__ __attribute__((aligned(16))) float red[2 * XW];
 
     const int idx = (blockIdx.x & 7) * p.per_xcd + (blockIdx.x >> 3);
     if (idx >= p.total) return;   // whole workgroup: no barrier is skipped
@@ -268,20 +273,29 @@ __global__ __launch_bounds__(64 * DW, 1) void deep_attention_kernel(const DeepPa
                     vf4{s[4 * i], s[4 * i + 1], s[4 * i + 2], s[4 * i + 3]};
         }
         __syncthreads();   // the tile's partials visible
-        if (nob == 0) continue;   // no output dims here; the wave still adds its partial
-
-        // S = the partials added in wave order (the same bits in every wave),
-        // one register group (8 LDS reads) at a time.
+        // Wave w adds elements [128w, 128w + 128) of the 8 partials in wave
+        // order, then every wave reads the whole sum.
+        {
+            float* rb = red + (it & 1) * XW;
+            const int e = 128 * wave + 2 * lane;
+            float2 a = *reinterpret_cast<const float2*>(xb + e);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            vf4 a = load4(xb + 4 * lane + 256 * i);
+            for (int w = 1; w < DW; ++w) {
+                const float2 x = *reinterpret_cast<const float2*>(xb + w * XW + e);
+                a.x += x.x;
+                a.y += x.y;
+            }
+            *reinterpret_cast<float2*>(rb + e) = a;
+            __syncthreads();
+            if (nob == 0) continue;
 #pragma unroll
-            for (int w = 1; w < DW; ++w) a += load4(xb + w * XW + 4 * lane + 256 * i);
-            s[4 * i] = a[0];
-            s[4 * i + 1] = a[1];
-            s[4 * i + 2] = a[2];
-            s[4 * i + 3] = a[3];
-            __builtin_amdgcn_sched_barrier(0);
+            for (int i = 0; i < 4; ++i) {
+                const vf4 t4 = load4(rb + 4 * lane + 256 * i);
+                s[4 * i] = t4[0];
+                s[4 * i + 1] = t4[1];
+                s[4 * i + 2] = t4[2];
+                s[4 * i + 3] = t4[3];
+            }
         }
         if (key0 + 32 > kall) {
 #pragma unroll
