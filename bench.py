@@ -52,7 +52,9 @@ PEAK_HBM_GBS = 8000.0
 # its 8.4 MB of K/V, more than the XCD's 4 MB L2).  Config 5a: 187.2 + 61.4
 # (algorithmic 184.3 + 61.4).  G = 8 decode step: 677.2 + 3.25 (algorithmic
 # 681.3 + 1.3, plus the 16-row partial records of split heads).  d = 256 causal
-# prefill (B = 1, H = 16, T = 4096): 260.3 + 67.8 (algorithmic 201.3 + 67.1).
+# prefill (B = 1, H = 16, T = 4096): 260.3 + 67.8 (algorithmic 201.3 + 67.1).  d = 512
+# causal prefill (deep kernel, same shape): 1244.7 + 134.2 (algorithmic 402.7 + 134.2;
+# the units of a KV head re-fetch its 16.8 MB of K/V, more than the XCD's 4 MB L2).
 TRAFFIC_PREFILL_CONFIG2 = round(224.5e6 + 134.2e6)
 TRAFFIC_DECODE_CONFIG3_STEP = round(646.0e6 + 1.8e6)
 TRAFFIC_CROSS_CONFIG5B = round(123.4e6 + 0.33e6)
@@ -63,6 +65,7 @@ TRAFFIC_PREFILL_CONFIG4 = round(272.9e6 + 67.1e6)
 TRAFFIC_PREFILL_CONFIG5A = round(187.2e6 + 61.4e6)
 TRAFFIC_DECODE_G8_STEP = round(677.2e6 + 3.25e6)
 TRAFFIC_PREFILL_D256 = round(260.3e6 + 67.8e6)
+TRAFFIC_PREFILL_D512 = round(1244.7e6 + 134.2e6)
 
 
 def cpu_threads():
@@ -581,7 +584,8 @@ def probe(nne, torch, dev):
     del q1, k1, v1, o1
     for (bb, h, tt, dd, causal, std, calls) in ((1, 16, 16384, 64, True, 0.5, 2),   # config 4
                                                 (8, 20, 1500, 64, False, 1.0, 3),   # config 5a
-                                                (1, 16, 4096, 256, True, 1.0, 3)):  # d = 256
+                                                (1, 16, 4096, 256, True, 1.0, 3),   # d = 256
+                                                (1, 16, 4096, 512, True, 1.0, 3)):  # d = 512
         q, k, v = (torch.randn(bb, h, tt, dd, generator=g, device=dev) * std for _ in range(3))
         o = torch.empty_like(q)
         for _ in range(calls):
@@ -608,8 +612,8 @@ def main():
                     help="counter-collection run: a 1 GiB device copy (calibrates FETCH_SIZE/"
                          "WRITE_SIZE), 3 config-2 prefills, 8 config-3 decode steps, 6 "
                          "config-5b cross-attention calls, 6 config-3 and 6 GPT-2 decode layer "
-                         "steps, 6 config-1 prefills, 2 config-4, 3 config-5a and 3 d=256 "
-                         "prefills, 8 G=8 decode steps")
+                         "steps, 6 config-1 prefills, 2 config-4, 3 config-5a, 3 d=256 and 3 "
+                         "d=512 prefills, 8 G=8 decode steps")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
@@ -668,6 +672,7 @@ def main():
             "config4": (1, 16, 16384, 64, True, 0.5),
             "config5a": (8, 20, 1500, 64, False, 1.0),
             "d256": (1, 16, 4096, 256, True, 1.0),
+            "d512": (1, 16, 4096, 512, True, 1.0),
         }.items():
             q = torch.randn(bb, h, tt, dd, generator=g, device=dev) * std
             k = torch.randn(bb, h, tt, dd, generator=g, device=dev) * std
@@ -675,8 +680,10 @@ def main():
             o = torch.empty_like(q)
             ms_c, kms_c = time_prefill(nne, torch, q, k, v, causal, max(3, args.steps // 2), 2, o)
             fl = causal_flops(bb, h, tt, dd) if causal else full_flops(bb, h, tt, tt, dd)
-            rec = {"workload": name if name != "d256" else
-                   "d256: causal prefill, head dim 256 (wave-pair kernel), B=1 H=16 T=4096 f32"}
+            rec = {"workload": {
+                "d256": "d256: causal prefill, head dim 256 (wave-pair kernel), B=1 H=16 T=4096 f32",
+                "d512": "d512: causal prefill, head dim 512 (deep kernel), B=1 H=16 T=4096 f32",
+            }.get(name, name)}
             if name == "config1":
                 # A ~15 us call: host-paced events measure Python's issue
                 # rate, so the device rate is taken with the calls queued.
@@ -697,7 +704,8 @@ def main():
                                      "traffic": {"config1": TRAFFIC_PREFILL_CONFIG1,
                                                  "config4": TRAFFIC_PREFILL_CONFIG4,
                                                  "config5a": TRAFFIC_PREFILL_CONFIG5A,
-                                                 "d256": TRAFFIC_PREFILL_D256}[name]}})
+                                                 "d256": TRAFFIC_PREFILL_D256,
+                                                 "d512": TRAFFIC_PREFILL_D512}[name]}})
             if not args.no_cpu:
                 # Bounded samples of the same workload (a few seconds each).
                 cpu_jobs.append((rec, {
@@ -713,6 +721,9 @@ def main():
                     "d256": lambda: flash_cpu_baseline(1, 16, 2048, 256, True, 1.0,
                                                        "the d = 256 line at half its length "
                                                        "(B=1, H=16, T=2048, d=256)"),
+                    "d512": lambda: flash_cpu_baseline(1, 16, 1024, 512, True, 1.0,
+                                                       "the d = 512 line at a quarter of its "
+                                                       "length (B=1, H=16, T=1024, d=512)"),
                 }[name]))
             extra.append(rec)
             if name == "config5a":
