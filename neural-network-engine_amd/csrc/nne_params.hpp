@@ -77,10 +77,9 @@ struct PrefillParams {
 // Head dims above 256 (deep.hip), prefill, cross-attention and decode alike.
 // The G * Tq query rows of a KV head are flattened (row r: query head
 // kvh * G + r / Tq, position r % Tq) and cut into 32-row units; a workgroup
-// serves one unit and one chunk of kDeepChunk output dims.  Sequence b has
+// serves one unit and one 512-dim chunk of the output dims.  Sequence b has
 // lens[b] keys when lens != null (a KV cache), else Tk; with `causal`, key c
 // is visible to position t iff c <= t + q_offset.
-constexpr int kDeepChunk = 1024;
 
 struct DeepParams {
     View4 q, k, v;
@@ -90,7 +89,7 @@ struct DeepParams {
     int q_offset;
     float qscale;    // softmax scale * log2(e), folded into Q
     int n_units;     // ceil(G * Tq / 32) per KV head
-    int n_oc;        // ceil(d / kDeepChunk) output chunks per unit
+    int n_oc;        // ceil(d / 512) output chunks per unit
     int total;       // B * Hkv * n_units * n_oc workgroups
     int per_xcd;     // ceil(total / 8)
 };
@@ -172,7 +171,9 @@ struct SplitKParams {
     float* ws_o;             // [slots][R][D] unnormalised partial O
     // Whole-head packing (packed != 0, arg_pref_valid launches): workgroup w
     // streams the heads pack_head[w] .. pack_head[w+1]-1 (flattened order
-    // b * Hkv + kvh) whole, so no head is split and no records exist.
+    // b * Hkv + kvh) whole, so no head is split and no records exist.  With
+    // packed == 2 (paired), workgroup w streams head pack_head[2w], then head
+    // pack_head[2w+1] unless that is 0xFFFF.
     union {
     uint16_t pack_head[kMaxPackWg + 1];
     // Cut chunks (cut != 0, fused launches): workgroup w streams the

@@ -327,10 +327,12 @@ __global__ __launch_bounds__(256, (D >= 128 && ROWS >= 16) ? 1 : 2) void splitk_
     const int arg_pref_tid = p.arg_pref[min(tid, kArgSeqs)];
     const int ph0 = p.pack_head[min(wg, kMaxPackWg - 1)];
     const int ph1 = p.pack_head[min(wg + 1, kMaxPackWg)];
+    const int pa = p.pack_head[min(2 * wg, kMaxPackWg - 1)];
+    const int pb = p.pack_head[min(2 * wg + 1, kMaxPackWg - 1)];
     const int cut_tid = p.chunk_end[min(tid, kMaxCutWg - 1)];
     warm_kernargs<0, offsetof(SplitKParams, arg_pref), offsetof(SplitKParams, fused),
                   offsetof(SplitKParams, pack_head)>();
-    asm volatile("" ::"v"(arg_pref_tid), "v"(ph0), "v"(ph1), "v"(cut_tid));   // loaded by now, in one wait
+    asm volatile("" ::"v"(arg_pref_tid), "v"(ph0), "v"(ph1), "v"(pa), "v"(pb), "v"(cut_tid));   // one wait
 
     build_prefix<APPEND>(p, pref, tid, lane, wave, arg_pref_tid);
     if (p.cut) {
@@ -353,13 +355,20 @@ __global__ __launch_bounds__(256, (D >= 128 && ROWS >= 16) ? 1 : 2) void splitk_
             }
         }
     }
-    int g, g_end;
-    if (p.packed) {
-        // Flattened start of head h (h = B * Hkv: the end of the last head).
-        auto head_key = [&](int h) {
-            const int bb = h / p.Hkv, kk = h % p.Hkv;
-            return bb >= p.B ? total : pref[bb] + kk * ((pref[bb + 1] - pref[bb]) / p.Hkv);
-        };
+    int g, g_end, g2 = 0, g2_end = 0;
+    // Flattened start of head h (h = B * Hkv: the end of the last head).
+    auto head_key = [&](int h) {
+        const int bb = h / p.Hkv, kk = h % p.Hkv;
+        return bb >= p.B ? total : pref[bb] + kk * ((pref[bb + 1] - pref[bb]) / p.Hkv);
+    };
+    if (p.packed == 2) {                 // paired: head pa, then head pb
+        g = head_key(pa);
+        g_end = head_key(pa + 1);
+        if (pb != 0xFFFF) {
+            g2 = head_key(pb);
+            g2_end = head_key(pb + 1);
+        }
+    } else if (p.packed) {
         g = head_key(ph0);
         g_end = head_key(ph1);
     } else if (p.cut) {
@@ -380,16 +389,16 @@ __global__ __launch_bounds__(256, (D >= 128 && ROWS >= 16) ? 1 : 2) void splitk_
         return lo;
     };
     if (g >= g_end) return;
-    // first sequence whose keys reach past g
-    int b = 0;
-    {
+    // first sequence whose keys reach past flattened key k
+    auto seq_of = [&](int k) {
         int lo = 0, hi = p.B - 1;
         while (lo < hi) {
             const int mid = (lo + hi + 1) >> 1;
-            if (pref[mid] <= g) lo = mid; else hi = mid - 1;
+            if (pref[mid] <= k) lo = mid; else hi = mid - 1;
         }
-        b = lo;
-    }
+        return lo;
+    };
+    int b = seq_of(g);
 
     float* Kw = lds + wave * KB * KS;    // this wave's K slice
     int v_col[NH];
@@ -764,6 +773,12 @@ __global__ __launch_bounds__(256, (D >= 128 && ROWS >= 16) ? 1 : 2) void splitk_
         }
         __syncthreads();                  // LDS is reused by the next segment
         g = h_start + key_end;
+        if (g >= g_end && g2 < g2_end) {  // paired packing: the second head
+            g = g2;
+            g_end = g2_end;
+            g2 = g2_end;
+            b = seq_of(g);
+        }
     }
     const int n_pend = n_pend_s;
     for (int i = 0; i < n_pend; ++i) {

@@ -5,6 +5,8 @@
 
 #include <algorithm>
 #include <climits>
+#include <utility>
+#include <vector>
 
 namespace nne {
 
@@ -52,6 +54,39 @@ constexpr double kSplitUs = 9.0;           // chunked over packed, past the stre
                                            // arrivals, merges and more segments per CU
                                            // (config 5b: 29.3 us chunked, 25.0 us packed)
 
+// At most two whole heads per workgroup, in any order: the longest heads
+// alone and the rest paired longest with shortest (the largest-first
+// assignment, when there are at most twice as many heads as slots).  Returns
+// the costliest workgroup (INT64_MAX when there are more heads than that),
+// with `pairs` the two heads of each workgroup (0xFFFF: none) and *n_wg.
+int64_t pair_heads(const SplitKParams& p, int slots, int64_t ovh, uint16_t* pairs, int* n_wg) {
+    std::vector<std::pair<int64_t, int>> h;   // (cost, head) of the heads with keys
+    for (int b = 0; b < p.B; ++b) {
+        const int64_t L = (p.arg_pref[b + 1] - p.arg_pref[b]) / p.Hkv;
+        if (L > 0)
+            for (int k = 0; k < p.Hkv; ++k) h.emplace_back(L + ovh, b * p.Hkv + k);
+    }
+    const int n = (int)h.size();
+    if (n == 0 || n > 2 * slots || slots > kMaxCutWg) return INT64_MAX;
+    std::stable_sort(h.begin(), h.end(),
+                     [](const std::pair<int64_t, int>& a, const std::pair<int64_t, int>& b) {
+                         return a.first > b.first;
+                     });
+    const int singles = n <= slots ? n : 2 * slots - n;
+    int64_t worst = 0;
+    int w = 0;
+    for (int i = 0; i < singles; ++i, ++w) {
+        worst = std::max(worst, h[i].first);
+        if (pairs) { pairs[2 * w] = (uint16_t)h[i].second; pairs[2 * w + 1] = 0xFFFF; }
+    }
+    for (int i = singles, j = n - 1; i < j; ++i, --j, ++w) {
+        worst = std::max(worst, h[i].first + h[j].first);
+        if (pairs) { pairs[2 * w] = (uint16_t)h[i].second; pairs[2 * w + 1] = (uint16_t)h[j].second; }
+    }
+    *n_wg = w;
+    return worst;
+}
+
 bool plan_packing(SplitKParams& p, int slots, int64_t total_keys) {
     const int n_heads = p.B * p.Hkv;
     if (!p.arg_pref_valid || !p.fused || slots > kMaxPackWg || n_heads == 0 || n_heads > 65535 ||
@@ -70,11 +105,19 @@ bool plan_packing(SplitKParams& p, int slots, int64_t total_keys) {
         const int64_t mid = (lo + hi) / 2;
         if (pack_groups(p, mid, ovh, nullptr) <= slots) hi = mid; else lo = mid + 1;
     }
+    int pair_wg = 0;
+    const int64_t pair_x = pair_heads(p, slots, ovh, nullptr, &pair_wg);
+    const int64_t x = std::min(lo, pair_x);
     const double stream_us = (double)total_keys * key_bytes / kDevBytesPerUs;
-    const double packed_us = std::max((double)lo * key_bytes / kCuBytesPerUs, stream_us);
+    const double packed_us = std::max((double)x * key_bytes / kCuBytesPerUs, stream_us);
     if (packed_us > stream_us + kSplitUs) return false;
-    p.n_wg = pack_groups(p, lo, ovh, p.pack_head);
-    p.packed = 1;
+    if (pair_x < lo) {
+        pair_heads(p, slots, ovh, p.pack_head, &p.n_wg);
+        p.packed = 2;
+    } else {
+        p.n_wg = pack_groups(p, lo, ovh, p.pack_head);
+        p.packed = 1;
+    }
     return true;
 }
 

@@ -13,8 +13,14 @@ namespace nne {
 // (keys + ovh per head) is at most x: the number of groups, and with `first`
 // their first heads (first[groups] = B * Hkv).
 int pack_groups(const SplitKParams& p, int64_t x, int64_t ovh, uint16_t* first);
+// At most two whole heads per workgroup, the longest alone and the rest
+// paired longest with shortest: the costliest workgroup (INT64_MAX if the
+// heads with keys outnumber twice the slots), with `pairs` (2 per workgroup,
+// 0xFFFF: none) and *n_wg.
+int64_t pair_heads(const SplitKParams& p, int slots, int64_t ovh, uint16_t* pairs, int* n_wg);
 // Whole-head packing when its estimate beats chunks (fused launches with the
-// prefix in the arguments): sets packed, n_wg, pack_head.
+// prefix in the arguments): sets packed (1: flattened runs, 2: pairs), n_wg,
+// pack_head.
 bool plan_packing(SplitKParams& p, int slots, int64_t total_keys);
 // The cut with budget x: its workgroup count (with `ends`, their chunk ends),
 // or max_wg + 1 if it needs more workgroups or gives a head more than

@@ -5,7 +5,10 @@
 //     ending at the total), with at most `slots` workgroups; only a packed
 //     group of empty heads may have an empty range;
 //   * packed: whole heads in flattened runs, no empty group, each group's
-//     keys plus the per-head cost within the planned bottleneck;
+//     keys plus the per-head cost within the planned bottleneck; or paired:
+//     every head with keys in exactly one workgroup, at most two per
+//     workgroup, no empty head, the costliest pair cheaper than the
+//     flattened runs' bottleneck;
 //   * cut: every workgroup's keys plus the per-segment cost within the
 //     budget, no workgroup closed with room for another segment (except the
 //     last), no head shared by more than max_parts workgroups, the budget the
@@ -87,6 +90,43 @@ static char check_layout(const Shape& s) {
     // Workgroup ranges [start[w], start[w+1]).
     std::vector<int64_t> start;
     char mode;
+    if (p.packed == 2) {
+        CHECK(p.n_wg <= s.slots && p.n_wg <= kMaxCutWg, "paired n_wg %d > slots %d", p.n_wg, s.slots);
+        const int64_t ovh = (int64_t)(2.5 * 37e3 / (8.0 * s.d) + 0.5);
+        std::vector<int> seen(heads.size(), 0);
+        int64_t worst = 0;
+        for (int w = 0; w < p.n_wg; ++w) {
+            int64_t cost = 0;
+            for (int j = 0; j < 2; ++j) {
+                const int h = p.pack_head[2 * w + j];
+                if (j == 1 && h == 0xFFFF) continue;
+                CHECK(h < (int)heads.size(), "workgroup %d head %d out of range", w, h);
+                if (h >= (int)heads.size()) continue;
+                CHECK(heads[h].second > heads[h].first, "workgroup %d streams empty head %d", w, h);
+                ++seen[h];
+                cost += heads[h].second - heads[h].first + ovh;
+            }
+            worst = std::max(worst, cost);
+        }
+        for (size_t h = 0; h < heads.size(); ++h)
+            CHECK(seen[h] == (heads[h].second > heads[h].first ? 1 : 0), "head %zu streamed %d times", h,
+                  seen[h]);
+        // chosen only when cheaper than the flattened runs' bottleneck
+        int64_t longest = 0, total_cost = 0;
+        for (const auto& h : heads) {
+            longest = std::max<int64_t>(longest, h.second - h.first + ovh);
+            total_cost += h.second - h.first + ovh;
+        }
+        int64_t lo = std::max<int64_t>(longest, (total_cost + s.slots - 1) / s.slots), hi = lo;
+        while (pack_groups(p, hi, ovh, nullptr) > s.slots) hi *= 2;
+        while (lo < hi) {
+            const int64_t mid = (lo + hi) / 2;
+            if (pack_groups(p, mid, ovh, nullptr) <= s.slots) hi = mid; else lo = mid + 1;
+        }
+        const int64_t x = lo;
+        CHECK(worst < x, "paired bottleneck %lld not below the runs' %lld", (long long)worst, (long long)x);
+        return 'p';
+    }
     if (p.packed) {
         mode = 'p';
         CHECK(p.n_wg <= s.slots, "packed n_wg %d > slots %d", p.n_wg, s.slots);
@@ -191,7 +231,7 @@ int main() {
         named.push_back({"config5b", c5b, 'p'});
         Shape gpt2{32, 12, 64, 4, {}, 256};   // GPT-2-small decode attend
         for (int b = 0; b < 32; ++b) gpt2.lens.push_back(128 + (int)(rng() % 897) + 1);
-        named.push_back({"gpt2", gpt2, 'p'});
+        named.push_back({"gpt2", gpt2, 'p'});   // paired (checked below)
         Shape big{150, 2, 128, 4, {}, 256};   // prefix not in the arguments: equal chunks
         for (int b = 0; b < 150; ++b) big.lens.push_back((int)(rng() % 3000));
         named.push_back({"b150", big, 'e'});
@@ -200,6 +240,16 @@ int main() {
         g_case = n.name;
         const char mode = check_layout(n.s);
         CHECK(mode == n.mode, "mode %c, expected %c", mode, n.mode);
+        SplitKParams p;
+        setup(p, n.s);
+        int64_t total = 0, max_len = 0;
+        for (int L : n.s.lens) {
+            total += (int64_t)n.s.Hkv * L;
+            max_len = std::max<int64_t>(max_len, L);
+        }
+        plan_split_layout(p, n.s.slots, total, (int)max_len);
+        if (std::string(n.name) == "gpt2") CHECK(p.packed == 2, "gpt2 packed %d, expected pairs", p.packed);
+        if (std::string(n.name) == "config5b") CHECK(p.packed == 1, "5b packed %d, expected runs", p.packed);
     }
 
     // Seeded sweep: ragged batches with empty sequences, one long head among

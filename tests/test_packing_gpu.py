@@ -8,8 +8,8 @@ no partial records, arrivals or merges exist.  The choice is a cost estimate
 hand-off of split heads); the shapes below sit far on one side of it:
 
 * the GPT-2-small decode attend (B = 32, 12 heads, d = 64, L ~ U[128, 1024]):
-  384 heads in about 256 groups of 1-3 heads, packed ~15 us against ~21 us
-  chunked;
+  384 heads paired into 256 workgroups (the 128 longest alone, the rest
+  longest with shortest), packed ~15 us against ~21 us chunked;
 * a uniform batch (B = 32, Hkv = 8, d = 128, L = 1000): one head per CU;
 * short ragged heads with empty sequences among them (zero rows out);
 * config 3's ragged lengths stay chunked (its longest head alone would take a
