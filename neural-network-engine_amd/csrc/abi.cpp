@@ -221,6 +221,10 @@ int run_attention(const float* q, const int64_t* qs_, const int64_t* qst, const 
                                 "multiple of 4, unit dim strides, strides that are multiples of 4 "
                                 "and 16-byte aligned tensors", d);
     if (deep) {
+        // The deep kernel addresses 32 K/V rows of a tile with 32-bit byte offsets.
+        if (kst[2] < 0 || vst[2] < 0 || kst[2] >= (1 << 25) || vst[2] >= (1 << 25))
+            return fail(NNE_EINVAL, "Invalid configuration or argument: K/V row strides must lie in "
+                                    "[0, 2^25) floats at head dim %d", d);
         nne::DeepParams p{};
         p.q = make_view(q, qst);
         p.k = make_view(k, kst);
@@ -694,6 +698,8 @@ int run_decode_deep(const float* q, const int64_t* q_strides, const float* k_cac
                                 "multiples of 4", (long long)d);
     if (!aligned16(k_cache) || !aligned16(v_cache))
         return fail(NNE_EINVAL, "Invalid configuration or argument: KV cache must be 16-byte aligned");
+    if (d >= (1 << 25))   // 32 cache rows of a tile are addressed with 32-bit byte offsets
+        return fail(NNE_EINVAL, "Invalid configuration or argument: KV cache head dim %lld", (long long)d);
     if (k_new) {
         const nne::View4 kn = make_view(k_new, kn_strides ? kn_strides : ckv);
         const nne::View4 vn = make_view(v_new, vn_strides ? vn_strides : ckv);
