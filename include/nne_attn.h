@@ -122,7 +122,9 @@ int nne_counters_init(uint32_t *counters, uint64_t n, void *stream);
  * Any head dim; above 128 the tensors must be 16-byte vector views
  * (d % 4 == 0, unit dim stride, other strides multiples of 4, 16-byte
  * aligned) -- NNE_EINVAL otherwise.  Above 256 dims a separate kernel runs
- * (MFMA, K/V read straight into operand layout, no workspace). */
+ * (MFMA, K/V read straight into operand layout); problems with too few
+ * query rows to fill the device split their keys over several workgroups,
+ * with records in the workspace. */
 int nne_flash_attention_forward(const float *q, const int64_t q_shape[4], const int64_t q_strides[4],
                                 const float *k, const int64_t k_shape[4], const int64_t k_strides[4],
                                 const float *v, const int64_t v_shape[4], const int64_t v_strides[4],
@@ -188,11 +190,14 @@ int nne_kv_append(float *k_cache, float *v_cache, int32_t *lens_dev, int32_t *le
                   const int64_t v_new_strides[4], int64_t B, int64_t Hkv, int64_t capacity,
                   int64_t d, int64_t t_new, void *stream);
 
-/* Records bytes a decode call of this geometry needs (any cache length; 0
- * for geometry the split-K decode kernel does not take, and for head dims
- * above 256, whose decode needs no workspace).  Decode calls also need
- * B * Hkv counters: nne_decode_workspace_size gives both ({0, 0} above 256,
- * NNE_EINVAL for geometry no decode call takes). */
+/* Records bytes a decode call of this geometry needs (any cache length, or
+ * cache lengths up to max_len when max_len > 0 above 256 dims; 0 for
+ * geometry no decode kernel takes).  Above 256 dims the records serve the
+ * deep kernel's key split, used when the batch has too few (sequence, KV
+ * head) pairs to fill the device: a smaller caller workspace gives fewer key
+ * parts, never an error, and no counters are needed.  Up to 256 dims decode
+ * calls also need B * Hkv counters: nne_decode_workspace_size gives both
+ * (NNE_EINVAL for geometry no decode call takes). */
 uint64_t nne_decode_workspace_bytes(int64_t B, int64_t Hq, int64_t Hkv, int64_t d, int64_t max_len);
 int nne_decode_workspace_size(int64_t B, int64_t Hq, int64_t Hkv, int64_t d,
                               nne_workspace_size_t *out);

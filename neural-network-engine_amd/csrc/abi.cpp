@@ -199,6 +199,39 @@ int wide_rows_per_launch(int d, bool causal) {
     return causal ? 16 : nne::splitk_rows_per_launch(d);
 }
 
+// Key tiles of the longest unit of a deep-kernel problem: the keys some row
+// can see.
+int deep_max_tiles(int64_t Tk, bool causal, int64_t qoff, int64_t Tq) {
+    const int64_t tk = causal ? std::max<int64_t>(0, std::min<int64_t>(Tk, qoff + Tq)) : Tk;
+    return (int)std::min<int64_t>((tk + 31) / 32, INT32_MAX);
+}
+
+// Key split of a deep-kernel launch and its records: the caller's workspace
+// caps the split (a smaller workspace gives fewer parts, never an error for
+// its size), the stream's own workspace is grown to the plan.
+int deep_workspace(nne::DeepParams& p, int max_tiles, const nne_workspace_t* wsp,
+                   hipStream_t stream) {
+    const uint64_t avail = wsp ? (wsp->records ? wsp->records_bytes : 0) : UINT64_MAX;
+    const uint64_t bytes = nne::deep_split_plan(p, max_tiles, device_cus(), avail);
+    if (bytes == 0) return NNE_OK;
+    void* ws = nullptr;
+    uint32_t* counters = nullptr;
+    const int rc = call_workspace(wsp, bytes, 0, stream, &ws, &counters, "deep attention key split");
+    if (rc != NNE_OK) return rc;
+    p.ws = static_cast<float*>(ws);
+    return NNE_OK;
+}
+
+// Records of the largest key split a deep-kernel problem of these shapes
+// takes (max_tiles: tiles of its longest unit; 0 when unknown).
+uint64_t deep_workspace_bytes(int64_t B, int64_t Hq, int64_t Hkv, int64_t Tq, int64_t d,
+                              int max_tiles) {
+    nne::DeepParams p{};
+    p.B = (int)B; p.Hq = (int)Hq; p.Hkv = (int)Hkv; p.G = (int)(Hq / Hkv); p.Tq = (int)Tq;
+    p.d = (int)d;
+    return nne::deep_split_plan(p, max_tiles > 0 ? max_tiles : (1 << 24), device_cus(), UINT64_MAX);
+}
+
 // Shared body of the two prefill entry points.  Shapes were validated.
 int run_attention(const float* q, const int64_t* qs_, const int64_t* qst, const float* k,
                   const int64_t* ks_, const int64_t* kst, const float* v, const int64_t* vst,
@@ -234,6 +267,8 @@ int run_attention(const float* q, const int64_t* qs_, const int64_t* qst, const 
         p.B = B; p.Hq = Hq; p.Hkv = Hkv; p.G = Hq / Hkv; p.Tq = Tq; p.Tk = Tk; p.d = d;
         p.q_offset = qoff;
         p.qscale = scale * nne::kLog2e;
+        const int rc = deep_workspace(p, deep_max_tiles(Tk, causal, qoff, Tq), wsp, stream);
+        if (rc != NNE_OK) return rc;
         hipError_t e = nne::launch_deep(p, causal, stream);
         if (e != hipSuccess) return hip_fail(e, "deep head-dim attention launch");
         return NNE_OK;
@@ -353,9 +388,14 @@ nne_workspace_size_t attention_workspace(const int64_t* qs_, const int64_t* ks_,
     nne_workspace_size_t r{0, 0};
     const int B = (int)qs_[0], Hq = (int)qs_[1], Tq = (int)qs_[2], d = (int)qs_[3];
     const int Hkv = (int)ks_[1], Tk = (int)ks_[2];
-    if ((int64_t)B * Hq * Tq == 0 || d == 0 || Hkv == 0 || nne::splitk_padded_dim(d) == 0) return r;
-    const bool wide = nne::prefill_padded_dim(d) == 0;
+    if ((int64_t)B * Hq * Tq == 0 || d == 0 || Hkv == 0) return r;
     const int qoff = (int)std::max<int64_t>(-(1 << 30), std::min<int64_t>(q_offset, 1 << 30));
+    if (nne::splitk_padded_dim(d) == 0) {   // above 256 dims: the deep kernel's key split
+        if (d % 4 == 0 && Hq % Hkv == 0)
+            r.records_bytes = deep_workspace_bytes(B, Hq, Hkv, Tq, d, deep_max_tiles(Tk, causal, qoff, Tq));
+        return r;
+    }
+    const bool wide = nne::prefill_padded_dim(d) == 0;
     const int64_t rows = (int64_t)(Hq / Hkv) * Tq;
     const int64_t tk = causal ? std::min<int64_t>(Tk, (int64_t)qoff + Tq) : Tk;
     // Wide head dims with more rows per KV head take the wave-pair kernel,
@@ -663,8 +703,10 @@ int nne_kv_append(float* k_cache, float* v_cache, int32_t* lens_dev, int32_t* le
 
 uint64_t nne_decode_workspace_bytes(int64_t B, int64_t Hq, int64_t Hkv, int64_t d, int64_t max_len) {
     if (B <= 0 || Hkv <= 0 || Hq <= 0 || Hq % Hkv != 0 || d <= 0 || d % 4 != 0 || max_len < 0 ||
-        B > INT32_MAX || Hq > INT32_MAX || nne::splitk_padded_dim((int)d) == 0)
+        B > INT32_MAX || Hq > INT32_MAX || d > INT32_MAX)
         return 0;
+    if (nne::splitk_padded_dim((int)d) == 0)   // above 256 dims: the deep kernel's key split
+        return deep_workspace_bytes(B, Hq, Hkv, 1, d, max_len > 0 ? (int)((max_len + 31) / 32) : 0);
     // One launch's worth: batches and rows beyond one launch run as several.
     const int Bl = (int)std::min<int64_t>(B, nne::splitk_max_seqs());
     const int Rl = (int)std::min<int64_t>(Hq / Hkv, nne::splitk_rows_per_launch((int)d));
@@ -676,15 +718,17 @@ uint64_t nne_decode_workspace_bytes(int64_t B, int64_t Hq, int64_t Hkv, int64_t 
 
 namespace nne {
 
-// Decode at head dims above 256 (lengths validated): the step's row is
-// appended by the append kernel (which advances lens_dev), then the deep
-// kernel attends every sequence to its first lens_dev[b] rows.  No workspace.
+// Decode at head dims above 256 (lengths validated, max_len the longest
+// sequence after the step): the step's row is appended by the append kernel
+// (which advances lens_dev), then the deep kernel attends every sequence to
+// its first lens_dev[b] rows, its keys split over several workgroups when the
+// batch has too few (sequence, KV head) pairs to fill the device.
 int run_decode_deep(const float* q, const int64_t* q_strides, const float* k_cache,
                     const float* v_cache, const int32_t* lens_dev, int32_t* lens_dev_w,
                     const float* k_new, const int64_t* kn_strides, const float* v_new,
                     const int64_t* vn_strides, float* o, const int64_t* o_strides, int64_t B,
                     int64_t Hq, int64_t Hkv, int64_t capacity, int64_t d, int has_scale,
-                    float scale, hipStream_t s) {
+                    float scale, int max_len, const nne_workspace_t* wsp, hipStream_t s) {
     const int64_t qshape[4] = {B, Hq, 1, d};
     const int64_t kvshape[4] = {B, Hkv, 1, d};
     int64_t c[4], ckv[4];
@@ -718,6 +762,8 @@ int run_decode_deep(const float* q, const int64_t* q_strides, const float* k_cac
     p.B = (int)B; p.Hq = (int)Hq; p.Hkv = (int)Hkv; p.G = (int)(Hq / Hkv); p.Tq = 1;
     p.Tk = (int)capacity; p.d = (int)d;
     p.qscale = softmax_scale(has_scale, scale, d) * nne::kLog2e;
+    const int rc = deep_workspace(p, (max_len + 31) / 32, wsp, s);
+    if (rc != NNE_OK) return rc;
     hipError_t e = nne::launch_deep(p, false, s);
     if (e != hipSuccess) return hip_fail(e, "decode attention launch");
     return NNE_OK;
@@ -759,7 +805,7 @@ int run_decode(const float* q, const int64_t* q_strides, const float* k_cache, c
     if (nne::splitk_padded_dim((int)d) == 0) {
         rc = run_decode_deep(q, q_strides, k_cache, v_cache, lens_dev, lens_dev_w, k_new,
                              kn_strides, v_new, vn_strides, o, o_strides, B, Hq, Hkv, capacity, d,
-                             has_scale, scale, s);
+                             has_scale, scale, max_len, wsp, s);
         if (rc == NNE_OK && append)
             for (int64_t b = 0; b < B; ++b) lens_host[b] += 1;
         return rc;
@@ -834,10 +880,13 @@ int nne_decode_workspace_size(int64_t B, int64_t Hq, int64_t Hkv, int64_t d,
                               nne_workspace_size_t* out) {
     if (!out) return fail(NNE_EINVAL, "Invalid configuration or argument: null output pointer");
     *out = nne_workspace_size_t{0, 0};
-    // Head dims above 256 (the deep kernel) need no workspace.
+    // Head dims above 256 (the deep kernel): records of its key split (zero
+    // for batches that fill the device without one), no counters.
     if (B > 0 && Hkv > 0 && Hq > 0 && Hq % Hkv == 0 && d > 256 && d % 4 == 0 && B <= INT32_MAX &&
-        Hq <= INT32_MAX && d <= INT32_MAX)
+        Hq <= INT32_MAX && d <= INT32_MAX) {
+        out->records_bytes = nne_decode_workspace_bytes(B, Hq, Hkv, d, 0);
         return NNE_OK;
+    }
     const uint64_t bytes = nne_decode_workspace_bytes(B, Hq, Hkv, d, 0);
     if (bytes == 0)
         return fail(NNE_EINVAL, "Invalid configuration or argument: no decode kernel for B=%lld "

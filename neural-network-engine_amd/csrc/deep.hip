@@ -51,6 +51,7 @@ namespace nne {
 namespace {
 
 constexpr int DW = 8;                           // waves per workgroup
+constexpr int kDeepMaxSplit = 8;                // key parts per unit
 constexpr int XW = 16 * 64;                     // floats of one wave's partial S^T
 
 __device__ __forceinline__ vf4 load4(const float* p) { return *reinterpret_cast<const vf4*>(p); }
@@ -64,7 +65,7 @@ __device__ __forceinline__ int clamp_keys(int64_t x, int tk) {
 // chunk is 32 * DW * OB dims).  KP chunks of the next tile's K are loaded
 // during the current tile, and VP key steps of a tile's V at its start;
 // the rest is loaded in groups of 4 inside its phase.
-template <bool CAUSAL, int QC, int OB, bool STREAMQ>
+template <bool CAUSAL, int QC, int OB, bool STREAMQ, bool SPLIT>
 __global__ __launch_bounds__(64 * DW, 1) void deep_attention_kernel(const DeepParams p) {
     constexpr int KP = QC < 8 ? QC : 8;
     constexpr int VP = OB <= 2 ? 16 : 4;
@@ -72,10 +73,15 @@ __global__ __launch_bounds__(64 * DW, 1) void deep_attention_kernel(const DeepPa
     __shared__ __attribute__((aligned(16))) float xs[2 * DW * XW];
     __shared__ __attribute__((aligned(16))) float red[2 * XW];
 
-    const int idx = (blockIdx.x & 7) * p.per_xcd + (blockIdx.x >> 3);
+    static_assert(32 * DW * OB == kDeepChunk, "output chunk of one workgroup");
+    // Key-split launches (few units, no K/V sharing between them worth an
+    // L2) deal the workgroups round-robin over the XCDs instead, so that the
+    // parts of ragged sequences spread over the whole device.
+    const int idx = SPLIT ? (int)blockIdx.x : (blockIdx.x & 7) * p.per_xcd + (blockIdx.x >> 3);
     if (idx >= p.total) return;   // whole workgroup: no barrier is skipped
-    const int oc = idx % p.n_oc;
-    const int hu = idx / p.n_oc;
+    const int split = SPLIT ? idx % p.n_split : 0;
+    const int oc = (SPLIT ? idx / p.n_split : idx) % p.n_oc;
+    const int hu = (SPLIT ? idx / p.n_split : idx) / p.n_oc;
     const int ui = hu % p.n_units, head = hu / p.n_units;
     const int unit = CAUSAL ? p.n_units - 1 - ui : ui;
     const int bi = head / p.Hkv, kvh = head % p.Hkv;
@@ -107,6 +113,10 @@ __global__ __launch_bounds__(64 * DW, 1) void deep_attention_kernel(const DeepPa
         kall = clamp_keys((int64_t)t_min + p.q_offset + 1, tk);
     }
     const int n_tiles = (kend + 31) >> 5;
+    // This workgroup's key tiles (all of the unit's without a key split).
+    const int t_begin = SPLIT ? split * p.split_tiles : 0;
+    int t_end = SPLIT ? t_begin + p.split_tiles : n_tiles;
+    if (t_end > n_tiles) t_end = n_tiles;
 
     // This wave's chunks of S (8 dims each) and output blocks (32 dims each).
     const int nj = (p.d + 7) >> 3;
@@ -172,15 +182,27 @@ __global__ __launch_bounds__(64 * DW, 1) void deep_attention_kernel(const DeepPa
         for (int rr = 0; rr < 16; ++rr) o[b][rr] = 0.f;
     float m_run = kNegInf, l_run = 0.f;
 
+    // Key-split launches (decode steps and few-query problems) stream K/V from
+    // HBM, not from an L2 shared with other units: V is loaded a whole tile
+    // ahead there (the first tile's here), where at the tile's start it would
+    // wait at P V for the HBM latency.
+    constexpr bool VAHEAD = SPLIT && QC <= 8;   // (above 512 dims the registers do not hold it)
+    static_assert(!VAHEAD || VP == 16, "V a tile ahead needs all key steps in registers");
+    float vn[VAHEAD ? VP : 1][OB];
+    if (VAHEAD && t_begin < t_end) {
+        const __amdgpu_buffer_rsrc_t rv0 = range(vb, p.v.st, 32 * t_begin);
+#pragma unroll
+        for (int j = 0; j < VP; ++j) load_v(rv0, j, vn[j]);
+    }
     vf4 kq[KP];
-    if (n_tiles > 0) {
-        const __amdgpu_buffer_rsrc_t rk = range(kb, p.k.st, 0);
+    if (t_begin < t_end) {
+        const __amdgpu_buffer_rsrc_t rk = range(kb, p.k.st, 32 * t_begin);
 #pragma unroll
         for (int i = 0; i < KP; ++i)
             kq[i] = load_k(rk, i);
     }
 
-    for (int it = 0; it < n_tiles; ++it) {
+    for (int it = t_begin; it < t_end; ++it) {
         const int key0 = it * 32;
         float* xb = xs + (it & 1) * (DW * XW);
 
@@ -189,8 +211,20 @@ __global__ __launch_bounds__(64 * DW, 1) void deep_attention_kernel(const DeepPa
         const __amdgpu_buffer_rsrc_t rk = range(kb, p.k.st, key0);
         const __amdgpu_buffer_rsrc_t rv = range(vb, p.v.st, key0);
         float vp[VP][OB];
+        if (VAHEAD) {
 #pragma unroll
-        for (int j = 0; j < VP; ++j) load_v(rv, j, vp[j]);
+            for (int j = 0; j < VP; ++j)
+#pragma unroll
+                for (int b = 0; b < OB; ++b) vp[j][b] = vn[j][b];
+            if (it + 1 < t_end) {
+                const __amdgpu_buffer_rsrc_t rv1 = range(vb, p.v.st, key0 + 32);
+#pragma unroll
+                for (int j = 0; j < VP; ++j) load_v(rv1, j, vn[j]);
+            }
+        } else {
+#pragma unroll
+            for (int j = 0; j < VP; ++j) load_v(rv, j, vp[j]);
+        }
         __builtin_amdgcn_sched_barrier(0);
 
         // Partial S^T = K Q^T over this wave's chunks, log2 domain.
@@ -257,7 +291,7 @@ __global__ __launch_bounds__(64 * DW, 1) void deep_attention_kernel(const DeepPa
         }
         // The next tile's first KP chunks of K: in flight under the exchange,
         // the softmax and P V.
-        if (it + 1 < n_tiles) {
+        if (it + 1 < t_end) {
             const __amdgpu_buffer_rsrc_t rk1 = range(kb, p.k.st, key0 + 32);
 #pragma unroll
             for (int i = 0; i < KP; ++i)
@@ -370,11 +404,29 @@ __global__ __launch_bounds__(64 * DW, 1) void deep_attention_kernel(const DeepPa
         else if (OB > 3 && nob == 3) pv(std::integral_constant<int, (OB > 3 ? 3 : 1)>{});
     }
 
-    // ---- normalise and write O[row][dim], dim = 32 gb + 8 (rr/4) + 4 half + rr%4 ----
+    // ---- write O[row][dim], dim = 32 gb + 8 (rr/4) + 4 half + rr%4: normalised,
+    // or with a key split the partial record -- (max, sum) of the rows, then
+    // their unnormalised O over this chunk ----
     const float l_tot = pair_sum(l_run);
-    const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
-    if (active) {
-        float* op = p.o.p + bi * p.o.sb + hq * p.o.sh + (int64_t)t * p.o.st;
+    float* op;
+    float mul;
+    bool wr;
+    if (SPLIT) {
+        const int64_t rec = ((int64_t)(head * p.n_units + unit) * p.n_oc + oc) * p.n_split + split;
+        float* rb = p.ws + rec * p.rpu * (kDeepChunk + 2);
+        wr = l32 < p.rpu;
+        if (wr && wave == 0 && half == 0) {
+            rb[2 * l32] = m_run;
+            rb[2 * l32 + 1] = l_tot;
+        }
+        op = rb + 2 * p.rpu + (int64_t)l32 * kDeepChunk - oc * kDeepChunk;
+        mul = 1.f;
+    } else {
+        op = p.o.p + bi * p.o.sb + hq * p.o.sh + (int64_t)t * p.o.st;
+        mul = l_tot > 0.f ? 1.f / l_tot : 0.f;
+        wr = active;
+    }
+    if (wr) {
 #pragma unroll
         for (int b = 0; b < OB; ++b) {
             if (b < nob) {
@@ -383,29 +435,84 @@ __global__ __launch_bounds__(64 * DW, 1) void deep_attention_kernel(const DeepPa
                     const int c = od - l32 + CB * b + 8 * qq + 4 * half;
                     if (c < p.d)
                         *reinterpret_cast<vf4*>(op + c) =
-                            vf4{o[b][4 * qq] * inv, o[b][4 * qq + 1] * inv,
-                                o[b][4 * qq + 2] * inv, o[b][4 * qq + 3] * inv};
+                            vf4{o[b][4 * qq] * mul, o[b][4 * qq + 1] * mul,
+                                o[b][4 * qq + 2] * mul, o[b][4 * qq + 3] * mul};
                 }
             }
         }
     }
 }
 
+// Merges the n_split partial records of one (unit, chunk) of a key-split
+// launch: O = sum_s 2^(m_s - M) O_s / sum_s 2^(m_s - M) l_s (M the largest
+// m_s; rows with no visible key stay zero), the records added in split order.
+__global__ __launch_bounds__(256) void deep_combine_kernel(const DeepParams p) {
+    __shared__ float w_s[kDeepMaxSplit][32];   // weight of part s for row r
+    __shared__ float inv_s[32];
+    const int c = blockIdx.x;      // (head * n_units + unit) * n_oc + chunk
+    const int oc = c % p.n_oc, hu = c / p.n_oc;
+    const int unit = hu % p.n_units, head = hu / p.n_units;
+    const int bi = head / p.Hkv, kvh = head % p.Hkv;
+    const int tid = threadIdx.x;
+    const int64_t rstride = (int64_t)p.rpu * (kDeepChunk + 2);
+    const float* rb = p.ws + (int64_t)c * p.n_split * rstride;
+    if (tid < p.rpu) {
+        float M = kNegInf;
+        for (int sp = 0; sp < p.n_split; ++sp) M = fmaxf(M, rb[sp * rstride + 2 * tid]);
+        const float M_use = M == kNegInf ? 0.f : M;
+        float l = 0.f;
+        for (int sp = 0; sp < p.n_split; ++sp) {
+            const float w = fast_exp2(rb[sp * rstride + 2 * tid] - M_use);
+            w_s[sp][tid] = w;
+            l += w * rb[sp * rstride + 2 * tid + 1];
+        }
+        inv_s[tid] = l > 0.f ? 1.f / l : 0.f;
+    }
+    __syncthreads();
+    const int rows = p.G * p.Tq;
+    const int ndim = p.d - oc * kDeepChunk < kDeepChunk ? p.d - oc * kDeepChunk : kDeepChunk;
+    for (int e = tid; e < p.rpu * (kDeepChunk / 4); e += 256) {
+        const int rr = e / (kDeepChunk / 4), c4 = 4 * (e % (kDeepChunk / 4));
+        const int r = unit * 32 + rr;
+        if (r >= rows || c4 >= ndim) continue;
+        vf4 acc = vf4{0.f, 0.f, 0.f, 0.f};
+        for (int sp = 0; sp < p.n_split; ++sp)
+            acc += w_s[sp][rr] * *reinterpret_cast<const vf4*>(rb + sp * rstride + 2 * p.rpu +
+                                                               (int64_t)rr * kDeepChunk + c4);
+        const int g = r / p.Tq, t = r % p.Tq;
+        float* op = p.o.p + bi * p.o.sb + (kvh * p.G + g) * p.o.sh + (int64_t)t * p.o.st;
+        *reinterpret_cast<vf4*>(op + oc * kDeepChunk + c4) = acc * inv_s[rr];
+    }
+}
+
 template <bool CAUSAL, int QC, int OB, bool STREAMQ>
 hipError_t launch_deep_v(DeepParams p, hipStream_t stream) {
-    constexpr int CH = 32 * DW * OB;   // output dims per workgroup
+    // (The split is a template parameter: its tile range and record path cost
+    // the unsplit kernel 35 VGPRs and 7 % at d = 512 when shared.)
     const int64_t rows = (int64_t)p.G * p.Tq;
     const int64_t units = (rows + 31) / 32;
-    const int64_t n_oc = (p.d + CH - 1) / CH;
-    const int64_t total = (int64_t)p.B * p.Hkv * units * n_oc;
+    const int64_t n_oc = (p.d + kDeepChunk - 1) / kDeepChunk;
+    if (p.n_split < 1 || (p.n_split > 1 && (!p.ws || p.n_split > kDeepMaxSplit || p.split_tiles < 1 ||
+                                            p.rpu != (int)(rows < 32 ? rows : 32))))
+        return hipErrorInvalidValue;
+    const int64_t base = (int64_t)p.B * p.Hkv * units * n_oc;
+    const int64_t total = base * p.n_split;
     if (total == 0) return hipSuccess;
     if (total > INT32_MAX - 8) return hipErrorInvalidValue;
     p.n_units = (int)units;
     p.n_oc = (int)n_oc;
     p.total = (int)total;
     p.per_xcd = (int)((total + 7) / 8);
-    hipLaunchKernelGGL((deep_attention_kernel<CAUSAL, QC, OB, STREAMQ>), dim3(8 * p.per_xcd),
+    if (p.n_split == 1) {
+        hipLaunchKernelGGL((deep_attention_kernel<CAUSAL, QC, OB, STREAMQ, false>),
+                           dim3(8 * p.per_xcd), dim3(64 * DW), 0, stream, p);
+        return hipGetLastError();
+    }
+    hipLaunchKernelGGL((deep_attention_kernel<CAUSAL, QC, OB, STREAMQ, true>), dim3(8 * p.per_xcd),
                        dim3(64 * DW), 0, stream, p);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(deep_combine_kernel, dim3((unsigned)base), dim3(256), 0, stream, p);
     return hipGetLastError();
 }
 
@@ -417,6 +524,31 @@ hipError_t launch_deep_t(const DeepParams& p, hipStream_t stream) {
 }
 
 }  // namespace
+
+// Problems with at most half as many workgroups as CUs (decode steps of
+// small batches, few-query cross-attention) split each unit's keys into up to
+// kDeepMaxSplit parts of at least 4 tiles, one round of workgroups over the
+// CUs, as far as max_bytes of records allow.  (Measured at d = 512, decode
+// over L ~ U[512, 4096]: B = 8 601 -> 190 us with 4 parts; at B = 32, where
+// every CU already has a head, 4 parts per head cost 667 -> 775 us: each
+// extra workgroup pays its cold start, its record and the merge.)
+uint64_t deep_split_plan(DeepParams& p, int max_tiles, int cus, uint64_t max_bytes) {
+    p.n_split = 1;
+    p.split_tiles = 0;
+    const int64_t rows = (int64_t)p.G * p.Tq;
+    p.rpu = (int)(rows < 32 ? rows : 32);
+    const int64_t wg = (int64_t)p.B * p.Hkv * ((rows + 31) / 32) * ((p.d + kDeepChunk - 1) / kDeepChunk);
+    if (wg == 0 || 2 * wg > (int64_t)cus || max_tiles < 8) return 0;
+    int64_t sp = (int64_t)cus / wg;
+    if (sp > kDeepMaxSplit) sp = kDeepMaxSplit;
+    if (sp > max_tiles / 4) sp = max_tiles / 4;
+    const uint64_t per = (uint64_t)wg * (uint64_t)p.rpu * (kDeepChunk + 2) * 4u;
+    while (sp > 1 && per * (uint64_t)sp > max_bytes) --sp;
+    if (sp <= 1) return 0;
+    p.n_split = (int)sp;
+    p.split_tiles = (int)((max_tiles + sp - 1) / sp);
+    return per * (uint64_t)sp;
+}
 
 hipError_t launch_deep(DeepParams p, bool causal, hipStream_t stream) {
     if (p.d <= 256 || p.d % 4 != 0 || p.Hkv <= 0 || p.G <= 0) return hipErrorInvalidValue;

@@ -24,7 +24,12 @@ hipError_t launch_prefill(PrefillParams p, bool causal, bool vec, hipStream_t st
 hipError_t launch_prefill_wide(PrefillParams p, bool causal, hipStream_t stream);
 // Head dims above 256 (deep.hip; d % 4 == 0, 16-byte vector views of Q, K,
 // V and O): prefill, cross-attention and decode over a KV cache (p.lens).
-// Fills the schedule fields of p.
+// deep_split_plan fills p.n_split / p.split_tiles / p.rpu for a problem whose
+// units have at most max_tiles 32-key tiles, with records of at most
+// max_bytes, and returns the record bytes (0: no split); the caller sets p.ws
+// when that is non-zero.  launch_deep fills the schedule fields and runs the
+// kernel (and the combine kernel after a split).
+uint64_t deep_split_plan(DeepParams& p, int max_tiles, int cus, uint64_t max_bytes);
 hipError_t launch_deep(DeepParams p, bool causal, hipStream_t stream);
 // Key-split plan for a prefill problem too small to fill the device (fills
 // p.n_chunks / p.chunk_tiles; n_chunks stays 0 when the problem is large

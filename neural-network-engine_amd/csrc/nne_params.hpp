@@ -77,9 +77,10 @@ struct PrefillParams {
 // Head dims above 256 (deep.hip), prefill, cross-attention and decode alike.
 // The G * Tq query rows of a KV head are flattened (row r: query head
 // kvh * G + r / Tq, position r % Tq) and cut into 32-row units; a workgroup
-// serves one unit and one 512-dim chunk of the output dims.  Sequence b has
-// lens[b] keys when lens != null (a KV cache), else Tk; with `causal`, key c
-// is visible to position t iff c <= t + q_offset.
+// serves one unit and one kDeepChunk-dim chunk of the output dims.  Sequence
+// b has lens[b] keys when lens != null (a KV cache), else Tk; with `causal`,
+// key c is visible to position t iff c <= t + q_offset.
+constexpr int kDeepChunk = 512;
 
 struct DeepParams {
     View4 q, k, v;
@@ -89,9 +90,19 @@ struct DeepParams {
     int q_offset;
     float qscale;    // softmax scale * log2(e), folded into Q
     int n_units;     // ceil(G * Tq / 32) per KV head
-    int n_oc;        // ceil(d / 512) output chunks per unit
-    int total;       // B * Hkv * n_units * n_oc workgroups
+    int n_oc;        // ceil(d / kDeepChunk) output chunks per unit
+    int total;       // B * Hkv * n_units * n_oc * n_split workgroups
     int per_xcd;     // ceil(total / 8)
+    // Key split (n_split > 1, up to 8 parts; problems with too few units to
+    // fill the device): workgroup s of a (unit, chunk) streams the unit's key tiles
+    // [s * split_tiles, (s + 1) * split_tiles) and leaves a partial record in
+    // ws -- (max, sum) of its rpu rows, then their unnormalised O over the
+    // chunk -- at record ((head * n_units + unit) * n_oc + chunk) * n_split + s;
+    // the combine kernel merges the records of each (unit, chunk).
+    int n_split;
+    int split_tiles;
+    int rpu;         // rows per record: min(32, G * Tq)
+    float* ws;
 };
 
 // Fused decode prologue (qkv.hip): rows m < M of x [M, C] (row stride x_rs,

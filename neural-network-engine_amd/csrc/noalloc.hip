@@ -81,7 +81,10 @@ extern "C" int nne_decode_step_noalloc(const float* q, const int64_t q_strides[4
     const uint64_t ws_bytes =
         nne_decode_workspace_size(B, Hq, Hkv, d, &need) == NNE_OK ? need.records_bytes : 0;
     const uint64_t cnt_bytes = ws_bytes ? (need.n_counters * 4 + 255) / 256 * 256 : 0;
-    if (cnt_bytes + ws_bytes > kScratchBytes) {
+    // Above 256 dims the records only allow a key split: a smaller scratch
+    // gives fewer parts (none at worst), so those steps are never refused.
+    const bool deep = d > 256;
+    if (!deep && cnt_bytes + ws_bytes > kScratchBytes) {
         char msg[256];
         snprintf(msg, sizeof(msg),
                  "Invalid configuration or argument: decode step needs %llu bytes of scratch, more "

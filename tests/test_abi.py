@@ -110,7 +110,7 @@ def test_decode_rejects_bad_geometry(nne):
 def test_decode_workspace_size(nne):
     lib = nne.lib()
     assert lib.nne_decode_workspace_bytes(1, 4, 3, 64, 100) == 0   # 3 does not divide 4
-    assert lib.nne_decode_workspace_bytes(1, 4, 4, 260, 100) == 0  # > 256: none needed
+    assert lib.nne_decode_workspace_bytes(1, 4, 4, 260, 100) == 0  # > 256, 4 tiles: no split
     assert lib.nne_decode_workspace_bytes(1, 4, 4, 30, 100) == 0   # head dim not a multiple of 4
     assert lib.nne_decode_workspace_bytes(1, 4, 4, 256, 100) > 0
     # any group size: rows beyond one launch's 64 go in further launches that
@@ -286,8 +286,13 @@ def test_workspace_size_queries(nne):
     assert size.n_counters == 32 * 8
     assert size.records_bytes == lib.nne_decode_workspace_bytes(32, 32, 8, 128, 4160)
     assert lib.nne_decode_workspace_size(1, 4, 4, 30, ctypes.byref(size)) == nne.NNE_EINVAL
-    # above 256 dims the decode needs no workspace
+    # above 256 dims: the records of the deep kernel's key split (up to 8 parts
+    # of each (sequence, KV head): 8 pairs x 8 parts x 4 rows x (512 + 2)
+    # floats), no counters; none for a batch that fills the device
     assert lib.nne_decode_workspace_size(4, 8, 2, 512, ctypes.byref(size)) == nne.NNE_OK
+    assert (size.records_bytes, size.n_counters) == (8 * 8 * 4 * 514 * 4, 0)
+    assert lib.nne_decode_workspace_bytes(4, 8, 2, 512, 100) == 0     # 4 tiles: no split
+    assert lib.nne_decode_workspace_size(1024, 8, 2, 512, ctypes.byref(size)) == nne.NNE_OK
     assert (size.records_bytes, size.n_counters) == (0, 0)
     assert lib.nne_decode_workspace_size(4, 8, 3, 512, ctypes.byref(size)) == nne.NNE_EINVAL
     assert lib.nne_qkv_workspace_size(4096, 32, 8, 128, ctypes.byref(size)) == nne.NNE_OK

@@ -89,6 +89,16 @@ def test_decode_head_dims_above_256(nne, cuda, b, hq, hkv, d, append):
     run_case(nne, cuda, b, hq, hkv, d, lens, append, seed=hq + 3 * d)
 
 
+def test_decode_long_sequences_above_256_dims(nne, cuda):
+    """Few (sequence, KV head) pairs with long caches at d = 512: each head's
+    keys split over workgroups, merged by the combine kernel."""
+    print("case decode deep long", flush=True)
+    rng = np.random.default_rng(65)
+    lens = rng.integers(1000, 3000, size=4)
+    run_case(nne, cuda, 4, 16, 4, 512, lens, True, seed=66)
+    run_case(nne, cuda, 4, 16, 4, 512, lens, False, seed=67)
+
+
 def test_decode_steps_above_256_dims(nne, cuda):
     """Four decode steps in a row at d = 512 through the cache: each step's
     output, the whole cache and the lengths against the oracle's steps."""

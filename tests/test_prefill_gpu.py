@@ -377,6 +377,41 @@ def test_head_dims_above_256(nne, cuda, b, hq, hkv, tq, tk, d, causal, q_off):
         T.assert_close(got, T.ref_flash(q, k, v, causal), what="d=%d flash" % d)
 
 
+@pytest.mark.parametrize("b,hq,hkv,tq,tk,d,causal,q_off", [
+    (2, 4, 4, 8, 3000, 512, False, 0),      # cross-attention: 8 queries, keys split in 8
+    (1, 8, 2, 4, 2500, 384, True, 2496),    # 4 new rows at the end of a long cache, G = 4
+    (1, 2, 1, 3, 1200, 1028, False, 0),     # two output chunks, each split
+])
+def test_deep_key_split(nne, cuda, b, hq, hkv, tq, tk, d, causal, q_off):
+    """Problems with too few query rows to fill the device split each unit's
+    keys over up to 8 workgroups (partial records, then the combine kernel);
+    with a workspace too small for any record the same call runs unsplit."""
+    import torch
+    print("case deep key split", b, hq, hkv, tq, tk, d, causal, q_off, flush=True)
+    s = 23 * tq + d
+    q, k, v = rnd(s, b, hq, tq, d), rnd(s + 1, b, hkv, tk, d), rnd(s + 2, b, hkv, tk, d)
+    size = nne.attention_workspace_size(q.shape, k.shape, causal, q_off)
+    assert size.records_bytes > 0 and size.n_counters == 0
+    qd, kd, vd = dev(q, cuda), dev(k, cuda), dev(v, cuda)
+    split = host(nne.attention_forward(qd, kd, vd, causal, q_offset=q_off,
+                                       workspace=nne.Workspace(cuda)))
+    ref = T.ref_standard(q, k, v, causal, start_pos=q_off)
+    T.assert_close(split, ref, what="d=%d split" % d)
+    # Through the C ABI with a 256-byte workspace: no record fits, no error.
+    import ctypes
+    i64 = lambda v: (ctypes.c_int64 * 4)(*[int(x) for x in v])
+    buf = torch.empty(256, dtype=torch.uint8, device=cuda)
+    tiny = nne.NneWorkspace(buf.data_ptr(), 256, None, 0)
+    out = torch.empty_like(qd)
+    rc = nne.lib().nne_attention_forward_ws(
+        qd.data_ptr(), i64(qd.shape), i64(qd.stride()), kd.data_ptr(), i64(kd.shape),
+        i64(kd.stride()), vd.data_ptr(), i64(vd.shape), i64(vd.stride()), out.data_ptr(),
+        i64(out.stride()), int(causal), q_off, 0, 0.0, ctypes.byref(tiny),
+        ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+    assert rc == nne.NNE_OK, nne.lib().nne_last_error()
+    T.assert_close(host(out), ref, what="d=%d unsplit" % d)
+
+
 def test_deep_head_dim_strided_views_and_repeat(nne, cuda):
     """d = 512 on [B, T, H, d] views, output through a strided view; a second
     call gives the same bits."""
