@@ -248,7 +248,9 @@ int nne_decode_step(const float *q, const int64_t q_strides[4], float *k_cache, 
  * lengths, and does not advance to later steps.  NNE_EINVAL if the step needs
  * more scratch than that (at
  * d = 128 it holds about 7800 (sequence, KV head) pairs with up to 4 query
- * heads per KV head, about 1700 with up to 16).  Every
+ * heads per KV head, about 1700 with up to 16); above 256 dims the scratch
+ * holds the key split's records, and a step whose records do not fit takes
+ * fewer key parts instead.  Every
  * call on a GPU shares that GPU's array: calls that overlap in time on one
  * GPU (any stream, any thread) race, and the caller must serialise them. */
 int nne_decode_step_noalloc(const float *q, const int64_t q_strides[4], float *k_cache,
