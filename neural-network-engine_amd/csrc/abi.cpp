@@ -210,9 +210,10 @@ int deep_max_tiles(int64_t Tk, bool causal, int64_t qoff, int64_t Tq) {
 // caps the split (a smaller workspace gives fewer parts, never an error for
 // its size), the stream's own workspace is grown to the plan.
 int deep_workspace(nne::DeepParams& p, int max_tiles, const nne_workspace_t* wsp,
-                   hipStream_t stream) {
+                   hipStream_t stream, const int32_t* seq_keys = nullptr) {
     const uint64_t avail = wsp ? (wsp->records ? wsp->records_bytes : 0) : UINT64_MAX;
-    const uint64_t bytes = nne::deep_split_plan(p, max_tiles, device_cus(), avail);
+    uint64_t bytes = seq_keys ? nne::deep_ragged_plan(p, seq_keys, device_cus(), avail) : 0;
+    if (bytes == 0) bytes = nne::deep_split_plan(p, max_tiles, device_cus(), avail);
     if (bytes == 0) return NNE_OK;
     void* ws = nullptr;
     uint32_t* counters = nullptr;
@@ -223,13 +224,21 @@ int deep_workspace(nne::DeepParams& p, int max_tiles, const nne_workspace_t* wsp
 }
 
 // Records of the largest key split a deep-kernel problem of these shapes
-// takes (max_tiles: tiles of its longest unit; 0 when unknown).
+// takes (max_tiles: tiles of its longest unit; 0 when unknown).  A decode
+// step (Tq = 1) may take the ragged split instead: at most one record of its
+// rows per CU.
 uint64_t deep_workspace_bytes(int64_t B, int64_t Hq, int64_t Hkv, int64_t Tq, int64_t d,
-                              int max_tiles) {
+                              int max_tiles, bool decode = false) {
     nne::DeepParams p{};
     p.B = (int)B; p.Hq = (int)Hq; p.Hkv = (int)Hkv; p.G = (int)(Hq / Hkv); p.Tq = (int)Tq;
     p.d = (int)d;
-    return nne::deep_split_plan(p, max_tiles > 0 ? max_tiles : (1 << 24), device_cus(), UINT64_MAX);
+    uint64_t bytes = nne::deep_split_plan(p, max_tiles > 0 ? max_tiles : (1 << 24), device_cus(), UINT64_MAX);
+    const int64_t rows = (Hq / Hkv) * Tq;
+    if (decode && rows <= 32 && d <= nne::kDeepChunk && B * Hkv <= nne::kDeepMaxHeads &&
+        (max_tiles <= 0 || max_tiles >= 5))   // shorter sequences never split
+        bytes = std::max<uint64_t>(bytes, (uint64_t)device_cus() * (uint64_t)rows *
+                                              (nne::kDeepChunk + 2) * 4u);
+    return bytes;
 }
 
 // Shared body of the two prefill entry points.  Shapes were validated.
@@ -706,7 +715,7 @@ uint64_t nne_decode_workspace_bytes(int64_t B, int64_t Hq, int64_t Hkv, int64_t 
         B > INT32_MAX || Hq > INT32_MAX || d > INT32_MAX)
         return 0;
     if (nne::splitk_padded_dim((int)d) == 0)   // above 256 dims: the deep kernel's key split
-        return deep_workspace_bytes(B, Hq, Hkv, 1, d, max_len > 0 ? (int)((max_len + 31) / 32) : 0);
+        return deep_workspace_bytes(B, Hq, Hkv, 1, d, max_len > 0 ? (int)((max_len + 31) / 32) : 0, true);
     // One launch's worth: batches and rows beyond one launch run as several.
     const int Bl = (int)std::min<int64_t>(B, nne::splitk_max_seqs());
     const int Rl = (int)std::min<int64_t>(Hq / Hkv, nne::splitk_rows_per_launch((int)d));
@@ -728,7 +737,8 @@ int run_decode_deep(const float* q, const int64_t* q_strides, const float* k_cac
                     const float* k_new, const int64_t* kn_strides, const float* v_new,
                     const int64_t* vn_strides, float* o, const int64_t* o_strides, int64_t B,
                     int64_t Hq, int64_t Hkv, int64_t capacity, int64_t d, int has_scale,
-                    float scale, int max_len, const nne_workspace_t* wsp, hipStream_t s) {
+                    float scale, int max_len, const int32_t* seq_keys, const nne_workspace_t* wsp,
+                    hipStream_t s) {
     const int64_t qshape[4] = {B, Hq, 1, d};
     const int64_t kvshape[4] = {B, Hkv, 1, d};
     int64_t c[4], ckv[4];
@@ -762,7 +772,7 @@ int run_decode_deep(const float* q, const int64_t* q_strides, const float* k_cac
     p.B = (int)B; p.Hq = (int)Hq; p.Hkv = (int)Hkv; p.G = (int)(Hq / Hkv); p.Tq = 1;
     p.Tk = (int)capacity; p.d = (int)d;
     p.qscale = softmax_scale(has_scale, scale, d) * nne::kLog2e;
-    const int rc = deep_workspace(p, (max_len + 31) / 32, wsp, s);
+    const int rc = deep_workspace(p, (max_len + 31) / 32, wsp, s, seq_keys);
     if (rc != NNE_OK) return rc;
     hipError_t e = nne::launch_deep(p, false, s);
     if (e != hipSuccess) return hip_fail(e, "decode attention launch");
@@ -805,7 +815,7 @@ int run_decode(const float* q, const int64_t* q_strides, const float* k_cache, c
     if (nne::splitk_padded_dim((int)d) == 0) {
         rc = run_decode_deep(q, q_strides, k_cache, v_cache, lens_dev, lens_dev_w, k_new,
                              kn_strides, v_new, vn_strides, o, o_strides, B, Hq, Hkv, capacity, d,
-                             has_scale, scale, max_len, wsp, s);
+                             has_scale, scale, max_len, seq_lens.data(), wsp, s);
         if (rc == NNE_OK && append)
             for (int64_t b = 0; b < B; ++b) lens_host[b] += 1;
         return rc;

@@ -79,9 +79,18 @@ __global__ __launch_bounds__(64 * DW, 1) void deep_attention_kernel(const DeepPa
     // parts of ragged sequences spread over the whole device.
     const int idx = SPLIT ? (int)blockIdx.x : (blockIdx.x & 7) * p.per_xcd + (blockIdx.x >> 3);
     if (idx >= p.total) return;   // whole workgroup: no barrier is skipped
-    const int split = SPLIT ? idx % p.n_split : 0;
-    const int oc = (SPLIT ? idx / p.n_split : idx) % p.n_oc;
-    const int hu = (SPLIT ? idx / p.n_split : idx) / p.n_oc;
+    int split = SPLIT ? idx % p.n_split : 0;
+    int oc = (SPLIT ? idx / p.n_split : idx) % p.n_oc;
+    int hu = (SPLIT ? idx / p.n_split : idx) / p.n_oc;
+    if (SPLIT && p.ragged) {
+        // Pair of workgroup idx: the pairs whose first part is at most idx,
+        // counted over the workgroup (part_prefix rises strictly).
+        const int nh = p.B * p.Hkv;
+        const int t = threadIdx.x;
+        hu = __syncthreads_count(t < nh && (int)p.part_prefix[t < nh ? t : 0] <= idx) - 1;
+        split = idx - (int)p.part_prefix[hu];
+        oc = 0;
+    }
     const int ui = hu % p.n_units, head = hu / p.n_units;
     const int unit = CAUSAL ? p.n_units - 1 - ui : ui;
     const int bi = head / p.Hkv, kvh = head % p.Hkv;
@@ -412,7 +421,8 @@ __global__ __launch_bounds__(64 * DW, 1) void deep_attention_kernel(const DeepPa
     float mul;
     bool wr;
     if (SPLIT) {
-        const int64_t rec = ((int64_t)(head * p.n_units + unit) * p.n_oc + oc) * p.n_split + split;
+        const int64_t rec = p.ragged ? (int64_t)idx
+                                     : ((int64_t)(head * p.n_units + unit) * p.n_oc + oc) * p.n_split + split;
         float* rb = p.ws + rec * p.rpu * (kDeepChunk + 2);
         wr = l32 < p.rpu;
         if (wr && wave == 0 && half == 0) {
@@ -455,13 +465,15 @@ __global__ __launch_bounds__(256) void deep_combine_kernel(const DeepParams p) {
     const int bi = head / p.Hkv, kvh = head % p.Hkv;
     const int tid = threadIdx.x;
     const int64_t rstride = (int64_t)p.rpu * (kDeepChunk + 2);
-    const float* rb = p.ws + (int64_t)c * p.n_split * rstride;
+    // ragged: pair c's records part_prefix[c] .. part_prefix[c + 1] - 1
+    const int n_parts = p.ragged ? (int)p.part_prefix[c + 1] - (int)p.part_prefix[c] : p.n_split;
+    const float* rb = p.ws + (p.ragged ? (int64_t)p.part_prefix[c] : (int64_t)c * p.n_split) * rstride;
     if (tid < p.rpu) {
         float M = kNegInf;
-        for (int sp = 0; sp < p.n_split; ++sp) M = fmaxf(M, rb[sp * rstride + 2 * tid]);
+        for (int sp = 0; sp < n_parts; ++sp) M = fmaxf(M, rb[sp * rstride + 2 * tid]);
         const float M_use = M == kNegInf ? 0.f : M;
         float l = 0.f;
-        for (int sp = 0; sp < p.n_split; ++sp) {
+        for (int sp = 0; sp < n_parts; ++sp) {
             const float w = fast_exp2(rb[sp * rstride + 2 * tid] - M_use);
             w_s[sp][tid] = w;
             l += w * rb[sp * rstride + 2 * tid + 1];
@@ -476,7 +488,7 @@ __global__ __launch_bounds__(256) void deep_combine_kernel(const DeepParams p) {
         const int r = unit * 32 + rr;
         if (r >= rows || c4 >= ndim) continue;
         vf4 acc = vf4{0.f, 0.f, 0.f, 0.f};
-        for (int sp = 0; sp < p.n_split; ++sp)
+        for (int sp = 0; sp < n_parts; ++sp)
             acc += w_s[sp][rr] * *reinterpret_cast<const vf4*>(rb + sp * rstride + 2 * p.rpu +
                                                                (int64_t)rr * kDeepChunk + c4);
         const int g = r / p.Tq, t = r % p.Tq;
@@ -496,7 +508,9 @@ hipError_t launch_deep_v(DeepParams p, hipStream_t stream) {
                                             p.rpu != (int)(rows < 32 ? rows : 32))))
         return hipErrorInvalidValue;
     const int64_t base = (int64_t)p.B * p.Hkv * units * n_oc;
-    const int64_t total = base * p.n_split;
+    if (p.ragged && (p.n_split < 2 || units != 1 || n_oc != 1 || base > kDeepMaxHeads))
+        return hipErrorInvalidValue;
+    const int64_t total = p.ragged ? (int64_t)p.part_prefix[base] : base * p.n_split;
     if (total == 0) return hipSuccess;
     if (total > INT32_MAX - 8) return hipErrorInvalidValue;
     p.n_units = (int)units;
@@ -548,6 +562,60 @@ uint64_t deep_split_plan(DeepParams& p, int max_tiles, int cus, uint64_t max_byt
     p.n_split = (int)sp;
     p.split_tiles = (int)((max_tiles + sp - 1) / sp);
     return per * (uint64_t)sp;
+}
+
+// Decode over ragged lengths (one unit and one output chunk per (sequence,
+// KV head) pair, at most kDeepMaxHeads pairs): each pair's keys are cut into
+// parts of `target` tiles -- at least 4, at most kDeepMaxSplit parts per pair,
+// all parts in one round of workgroups over the CUs -- so a long sequence no
+// longer sets the step's time on one CU while the others idle.  Used when
+// that shortens the longest workgroup by a quarter or more.  (Measured at
+// d = 512, L ~ U[512, 4096], Hq = 32, Hkv = 8: B = 8 571 -> 148 us, against
+// 190 us for equal parts per pair; allowing two rounds, so that B = 32 could
+// split too, made B = 8 261 us and B = 32 916 against 628 us unsplit: a part
+// dispatched in the second round starts only when a CU's first one ends.)
+uint64_t deep_ragged_plan(DeepParams& p, const int32_t* seq_keys, int cus, uint64_t max_bytes) {
+    p.ragged = 0;
+    const int64_t rows = (int64_t)p.G * p.Tq;
+    const int64_t heads = (int64_t)p.B * p.Hkv;
+    if (rows > 32 || p.d > kDeepChunk || heads == 0 || heads > kDeepMaxHeads || !seq_keys) return 0;
+    int64_t total = 0, longest = 0;
+    for (int b = 0; b < p.B; ++b) {
+        const int64_t t = ((int64_t)seq_keys[b] + 31) / 32;
+        total += t * p.Hkv;
+        longest = longest > t ? longest : t;
+    }
+    auto parts_of = [&](int64_t target) {
+        int64_t n = 0;
+        for (int b = 0; b < p.B; ++b) {
+            const int64_t t = ((int64_t)seq_keys[b] + 31) / 32;
+            n += (t > target ? (t + target - 1) / target : 1) * p.Hkv;
+        }
+        return n;
+    };
+    int64_t target = (total + cus - 1) / cus;
+    if (target < 4) target = 4;
+    if (target < (longest + kDeepMaxSplit - 1) / kDeepMaxSplit) target = (longest + kDeepMaxSplit - 1) / kDeepMaxSplit;
+    while (parts_of(target) > cus) ++target;
+    if (4 * longest < 5 * target) return 0;   // no pair's time shrinks enough to pay the split
+    const int64_t n = parts_of(target);
+    p.rpu = (int)(rows < 32 ? rows : 32);
+    const uint64_t bytes = (uint64_t)n * (uint64_t)p.rpu * (kDeepChunk + 2) * 4u;
+    if (bytes > max_bytes || n > 65535) return 0;
+    int64_t at = 0;
+    for (int b = 0; b < p.B; ++b) {
+        const int64_t t = ((int64_t)seq_keys[b] + 31) / 32;
+        const int64_t parts = t > target ? (t + target - 1) / target : 1;
+        for (int k = 0; k < p.Hkv; ++k) {
+            p.part_prefix[b * p.Hkv + k] = (uint16_t)at;
+            at += parts;
+        }
+    }
+    p.part_prefix[heads] = (uint16_t)at;
+    p.ragged = 1;
+    p.n_split = kDeepMaxSplit;   // marks a split launch; parts per pair come from part_prefix
+    p.split_tiles = (int)target;
+    return bytes;
 }
 
 hipError_t launch_deep(DeepParams p, bool causal, hipStream_t stream) {

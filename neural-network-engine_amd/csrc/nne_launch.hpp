@@ -30,6 +30,10 @@ hipError_t launch_prefill_wide(PrefillParams p, bool causal, hipStream_t stream)
 // when that is non-zero.  launch_deep fills the schedule fields and runs the
 // kernel (and the combine kernel after a split).
 uint64_t deep_split_plan(DeepParams& p, int max_tiles, int cus, uint64_t max_bytes);
+// Ragged key split of a decode step (seq_keys: host key counts per sequence
+// after the step): fills p.ragged / p.part_prefix / p.split_tiles / p.rpu and
+// returns the record bytes, or 0 when the step does not gain from it.
+uint64_t deep_ragged_plan(DeepParams& p, const int32_t* seq_keys, int cus, uint64_t max_bytes);
 hipError_t launch_deep(DeepParams p, bool causal, hipStream_t stream);
 // Key-split plan for a prefill problem too small to fill the device (fills
 // p.n_chunks / p.chunk_tiles; n_chunks stays 0 when the problem is large

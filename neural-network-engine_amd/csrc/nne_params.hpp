@@ -81,6 +81,7 @@ struct PrefillParams {
 // b has lens[b] keys when lens != null (a KV cache), else Tk; with `causal`,
 // key c is visible to position t iff c <= t + q_offset.
 constexpr int kDeepChunk = 512;
+constexpr int kDeepMaxHeads = 512;   // (sequence, KV head) pairs of a ragged key split
 
 struct DeepParams {
     View4 q, k, v;
@@ -103,6 +104,12 @@ struct DeepParams {
     int split_tiles;
     int rpu;         // rows per record: min(32, G * Tq)
     float* ws;
+    // Ragged key split (decode over ragged lengths, one unit and one chunk per
+    // (sequence, KV head) pair h): pair h takes workgroups and records
+    // part_prefix[h] .. part_prefix[h + 1] - 1, each split_tiles tiles of its
+    // keys, so long sequences get more parts than short ones.
+    int ragged;
+    uint16_t part_prefix[kDeepMaxHeads + 1];
 };
 
 // Fused decode prologue (qkv.hip): rows m < M of x [M, C] (row stride x_rs,

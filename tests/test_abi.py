@@ -286,11 +286,13 @@ def test_workspace_size_queries(nne):
     assert size.n_counters == 32 * 8
     assert size.records_bytes == lib.nne_decode_workspace_bytes(32, 32, 8, 128, 4160)
     assert lib.nne_decode_workspace_size(1, 4, 4, 30, ctypes.byref(size)) == nne.NNE_EINVAL
-    # above 256 dims: the records of the deep kernel's key split (up to 8 parts
-    # of each (sequence, KV head): 8 pairs x 8 parts x 4 rows x (512 + 2)
-    # floats), no counters; none for a batch that fills the device
+    # above 256 dims: the records of the deep kernel's key split, no counters --
+    # up to 8 parts of each (sequence, KV head) (8 pairs x 8 parts x 4 rows x
+    # (512 + 2) floats), or for ragged lengths one record of 4 rows per CU
+    # (256 CUs, the count assumed without a device); none for a batch too
+    # large for either split
     assert lib.nne_decode_workspace_size(4, 8, 2, 512, ctypes.byref(size)) == nne.NNE_OK
-    assert (size.records_bytes, size.n_counters) == (8 * 8 * 4 * 514 * 4, 0)
+    assert (size.records_bytes, size.n_counters) == (max(8 * 8, 256) * 4 * 514 * 4, 0)
     assert lib.nne_decode_workspace_bytes(4, 8, 2, 512, 100) == 0     # 4 tiles: no split
     assert lib.nne_decode_workspace_size(1024, 8, 2, 512, ctypes.byref(size)) == nne.NNE_OK
     assert (size.records_bytes, size.n_counters) == (0, 0)
