@@ -39,6 +39,11 @@
 //  to the 8 XCDs in turn; XCD x takes the x-th eighth of the (sequence, KV
 //  head, unit, chunk) list, so the units of a KV head, which read the same
 //  K/V rows, share an L2, and causal units are taken longest first.
+//  Problems with too few units to fill the device (decode steps of small
+//  batches, few-query cross-attention) cut each unit's keys into parts, one
+//  workgroup each, equal parts or (ragged decode) parts by length; every part
+//  leaves a partial record -- the online softmax's (max, sum) and unnormalised
+//  O -- and deep_combine_kernel merges them.
 #include <hip/hip_runtime.h>
 
 #include <type_traits>
