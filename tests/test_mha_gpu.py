@@ -59,7 +59,7 @@ def oracle_self(w, x, k_cache, v_cache, h, causal):
     return y.reshape(b, t, c), k_all, v_all
 
 
-@pytest.mark.parametrize("c,h", [(256, 4), (192, 6)])   # d = 64 (fused decode), d = 32 (GEMM path)
+@pytest.mark.parametrize("c,h", [(256, 4), (192, 6), (1024, 2)])   # d = 64 (fused decode), 32 (GEMM path), 512 (deep kernel)
 def test_mha_self_attention_cached_steps_match_oracle(nne, cuda, c, h):
     rng = np.random.default_rng(c + h)
     b, t0, steps = 3, 9, 4

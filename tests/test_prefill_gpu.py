@@ -282,20 +282,22 @@ def test_linearity_in_v_full_config4_shape(nne, cuda):
     T.assert_close(host(o1)[:, :, -4:], ref_rows, what="config4 last rows")
 
 
-def test_flash_layer_matches_composition(nne, cuda):
-    layer = nne.FlashAttention(64, 4, True, device=cuda, seed=3)
-    x = dev(rnd(60, 2, 16, 64), cuda)
+@pytest.mark.parametrize("c,h,t", [(64, 4, 16), (1024, 2, 40)])   # d = 16; d = 512 (deep kernel)
+def test_flash_layer_matches_composition(nne, cuda, c, h, t):
+    layer = nne.FlashAttention(c, h, True, device=cuda, seed=3)
+    x = dev(rnd(60, 2, t, c), cuda)
     got = host(layer(x))
     # reference composition (flash_attention.rs:254-275) with the oracle core
-    xs = host(x)
+    xs = host(x).astype(np.float64)
     def lin(p, a):
-        return a @ host(p[0]).T + host(p[1])
-    b, t, c = xs.shape
-    q = lin(layer.q_proj, xs).reshape(b, t, 4, 16).transpose(0, 2, 1, 3)
-    k = lin(layer.k_proj, xs).reshape(b, t, 4, 16).transpose(0, 2, 1, 3)
-    v = lin(layer.v_proj, xs).reshape(b, t, 4, 16).transpose(0, 2, 1, 3)
+        return (a @ host(p[0]).astype(np.float64).T + host(p[1])).astype(np.float32)
+    b, d = xs.shape[0], c // h
+    q = lin(layer.q_proj, xs).reshape(b, t, h, d).transpose(0, 2, 1, 3)
+    k = lin(layer.k_proj, xs).reshape(b, t, h, d).transpose(0, 2, 1, 3)
+    v = lin(layer.v_proj, xs).reshape(b, t, h, d).transpose(0, 2, 1, 3)
     core = T.ref_flash(q, k, v, True).transpose(0, 2, 1, 3).reshape(b, t, c)
-    T.assert_close(got, lin(layer.out_proj, core), atol=2e-4, rtol=2e-3, what="layer")
+    T.assert_close(got, lin(layer.out_proj, core.astype(np.float64)), atol=2e-4, rtol=2e-3,
+                   what="layer d=%d" % d)
 
 
 def test_stream_release_frees_and_reallocates(nne, cuda):
