@@ -19,7 +19,7 @@ LIB_DIR = os.path.join(PKG, "lib")
 LIB = os.path.join(LIB_DIR, "libnne_attn.so")
 HOST_LIB = os.path.join(LIB_DIR, "libnne_host.so")
 
-SOURCES = ["prefill.hip", "small.hip", "splitk.hip", "splitk_plan.cpp", "qkv.hip", "deep.hip", "abi.cpp", "noalloc.hip"]
+SOURCES = ["prefill.hip", "small.hip", "splitk.hip", "splitk_plan.cpp", "qkv.hip", "deep.hip", "deep_plan.cpp", "abi.cpp", "noalloc.hip"]
 
 HIPCC_FLAGS = [
     "--offload-arch=gfx950",

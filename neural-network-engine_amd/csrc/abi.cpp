@@ -235,7 +235,7 @@ uint64_t deep_workspace_bytes(int64_t B, int64_t Hq, int64_t Hkv, int64_t Tq, in
     uint64_t bytes = nne::deep_split_plan(p, max_tiles > 0 ? max_tiles : (1 << 24), device_cus(), UINT64_MAX);
     const int64_t rows = (Hq / Hkv) * Tq;
     if (decode && rows <= 32 && d <= nne::kDeepChunk && B * Hkv <= nne::kDeepMaxHeads &&
-        (max_tiles <= 0 || max_tiles >= 5))   // shorter sequences never split
+        B * Hkv <= device_cus() && (max_tiles <= 0 || max_tiles >= 5))   // shorter sequences never split
         bytes = std::max<uint64_t>(bytes, (uint64_t)device_cus() * (uint64_t)rows *
                                               (nne::kDeepChunk + 2) * 4u);
     return bytes;
@@ -278,7 +278,7 @@ int run_attention(const float* q, const int64_t* qs_, const int64_t* qst, const 
         p.qscale = scale * nne::kLog2e;
         const int rc = deep_workspace(p, deep_max_tiles(Tk, causal, qoff, Tq), wsp, stream);
         if (rc != NNE_OK) return rc;
-        hipError_t e = nne::launch_deep(p, causal, stream);
+        hipError_t e = nne::launch_deep(p, causal, device_cus(), stream);
         if (e != hipSuccess) return hip_fail(e, "deep head-dim attention launch");
         return NNE_OK;
     }
@@ -774,7 +774,7 @@ int run_decode_deep(const float* q, const int64_t* q_strides, const float* k_cac
     p.qscale = softmax_scale(has_scale, scale, d) * nne::kLog2e;
     const int rc = deep_workspace(p, (max_len + 31) / 32, wsp, s, seq_keys);
     if (rc != NNE_OK) return rc;
-    hipError_t e = nne::launch_deep(p, false, s);
+    hipError_t e = nne::launch_deep(p, false, device_cus(), s);
     if (e != hipSuccess) return hip_fail(e, "decode attention launch");
     return NNE_OK;
 }

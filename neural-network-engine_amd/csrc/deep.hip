@@ -33,12 +33,18 @@
 //    per half-wave.
 //  * The next tile's K (up to 8 chunks) is loaded during the current tile's
 //    exchange, softmax and P V, and a tile's V at its start, under its S.
+//  Prefill problems with more workgroups than CUs use a 4-wave form
+//  instead, two workgroups per CU: each wave takes twice the chunks and
+//  output blocks (S from 4 partials, Q^T of its last 8 chunks in LDS), so a
+//  tile's MFMAs per wave double against the same exchange and softmax, and
+//  one workgroup's exchange overlaps the other's MFMAs.
 //  A unit of more than 512 dims takes one workgroup per output chunk, each
 //  recomputing S (at d = 1024 that is 1.5x the algorithmic MFMA work; holding
 //  O^T of 1024 dims instead spilled registers in the loop).  Workgroup ids go
 //  to the 8 XCDs in turn; XCD x takes the x-th eighth of the (sequence, KV
 //  head, unit, chunk) list, so the units of a KV head, which read the same
-//  K/V rows, share an L2, and causal units are taken longest first.
+//  K/V rows, share an L2, and causal units are taken longest first (on the
+//  8-wave form across the XCD's KV heads when each XCD holds whole heads).
 //  Problems with too few units to fill the device (decode steps of small
 //  batches, few-query cross-attention) cut each unit's keys into parts, one
 //  workgroup each, equal parts or (ragged decode) parts by length; every part
@@ -55,8 +61,6 @@ namespace nne {
 
 namespace {
 
-constexpr int DW = 8;                           // waves per workgroup
-constexpr int kDeepMaxSplit = 8;                // key parts per unit
 constexpr int XW = 16 * 64;                     // floats of one wave's partial S^T
 
 __device__ __forceinline__ vf4 load4(const float* p) { return *reinterpret_cast<const vf4*>(p); }
@@ -65,18 +69,24 @@ __device__ __forceinline__ int clamp_keys(int64_t x, int tk) {
     return x < 0 ? 0 : (x > tk ? tk : (int)x);
 }
 
-// Per wave: QC chunks of S whose Q^T stays in registers (STREAMQ: further
-// chunks read again each tile) and OB output blocks (the workgroup's output
-// chunk is 32 * DW * OB dims).  KP chunks of the next tile's K are loaded
-// during the current tile, and VP key steps of a tile's V at its start;
-// the rest is loaded in groups of 4 inside its phase.
-template <bool CAUSAL, int QC, int OB, bool STREAMQ, bool SPLIT>
-__global__ __launch_bounds__(64 * DW, 1) void deep_attention_kernel(const DeepParams p) {
-    constexpr int KP = QC < 8 ? QC : 8;
+// DW waves per workgroup.  Per wave: QC chunks of S (STREAMQ: further chunks
+// read again each tile) and OB output blocks (the workgroup's output chunk is
+// 32 * DW * OB dims).  Q^T of the chunks stays in registers, except that the
+// 4-wave form keeps its last 8 chunks in LDS.  KP chunks of the next tile's K
+// are loaded during the current tile, and VP key steps of a tile's V at its
+// start; the rest is loaded in groups of 4 inside its phase.  8 waves: one
+// workgroup per CU; 4 waves: two per CU, whose exchanges and softmaxes
+// interleave with each other's MFMAs.
+template <bool CAUSAL, int DW, int QC, int OB, bool STREAMQ, bool SPLIT>
+__global__ __launch_bounds__(64 * DW, 8 / DW) void deep_attention_kernel(const DeepParams p) {
+    static_assert(DW == 8 || (DW == 4 && QC == 16 && !SPLIT && !STREAMQ), "the two workgroup forms");
+    constexpr int KP = DW == 4 ? 4 : (QC < 8 ? QC : 8);
     constexpr int VP = OB <= 2 ? 16 : 4;
+    constexpr int QL = DW == 4 ? 8 : 0;  // Q^T chunks in LDS (the last QL of QC)
     constexpr int CB = 32 * DW;          // dims between a wave's output blocks
     __shared__ __attribute__((aligned(16))) float xs[2 * DW * XW];
     __shared__ __attribute__((aligned(16))) float red[2 * XW];
+    __shared__ __attribute__((aligned(16))) float qs[QL > 0 ? DW * QL * 256 : 4];
 
     static_assert(32 * DW * OB == kDeepChunk, "output chunk of one workgroup");
     // Key-split launches (few units, no K/V sharing between them worth an
@@ -87,6 +97,13 @@ __global__ __launch_bounds__(64 * DW, 1) void deep_attention_kernel(const DeepPa
     int split = SPLIT ? idx % p.n_split : 0;
     int oc = (SPLIT ? idx / p.n_split : idx) % p.n_oc;
     int hu = (SPLIT ? idx / p.n_split : idx) / p.n_oc;
+    if (!SPLIT && p.order_hpx) {
+        // Causal units of the XCD's order_hpx whole KV heads, longest first
+        // across those heads (rank-major).
+        const int pos = blockIdx.x >> 3, cols = p.order_hpx * p.n_oc;
+        oc = (pos % cols) % p.n_oc;
+        hu = ((blockIdx.x & 7) * p.order_hpx + (pos % cols) / p.n_oc) * p.n_units + pos / cols;
+    }
     if (SPLIT && p.ragged) {
         // Pair of workgroup idx: the pairs whose first part is at most idx,
         // counted over the workgroup (part_prefix rises strictly).
@@ -97,7 +114,13 @@ __global__ __launch_bounds__(64 * DW, 1) void deep_attention_kernel(const DeepPa
         oc = 0;
     }
     const int ui = hu % p.n_units, head = hu / p.n_units;
-    const int unit = CAUSAL ? p.n_units - 1 - ui : ui;
+    // Causal units by rank ui, longest first: by their last query position,
+    // the G query heads of one position block in turn when units do not
+    // straddle heads.
+    const int ntb = p.Tq >> 5;
+    const int unit = !CAUSAL ? ui
+                   : (p.G > 1 && (p.Tq & 31) == 0) ? (ui % p.G) * ntb + (ntb - 1 - ui / p.G)
+                                                  : p.n_units - 1 - ui;
     const int bi = head / p.Hkv, kvh = head % p.Hkv;
 
     const int tid = threadIdx.x, lane = tid & 63;
@@ -134,18 +157,21 @@ __global__ __launch_bounds__(64 * DW, 1) void deep_attention_kernel(const DeepPa
 
     // This wave's chunks of S (8 dims each) and output blocks (32 dims each).
     const int nj = (p.d + 7) >> 3;
-    const int nq = wave < nj ? ((nj - 1 - wave) >> 3) + 1 : 0;
+    const int nq = wave < nj ? (nj - 1 - wave) / DW + 1 : 0;
     const int nbt = (p.d + 31) >> 5;
     const int gb0 = oc * (CB * OB / 32) + wave;
-    const int nob = gb0 < nbt ? min(OB, ((nbt - 1 - gb0) >> 3) + 1) : 0;
+    const int nob = gb0 < nbt ? min(OB, (nbt - 1 - gb0) / DW + 1) : 0;
 
     const float* qp = p.q.p + bi * p.q.sb + hq * p.q.sh + (int64_t)t * p.q.st;
-    vf4 qf[QC];
+    vf4 qf[QC - QL];
 #pragma unroll
     for (int i = 0; i < QC; ++i) {
         const int c = 8 * (wave + DW * i) + 4 * half;
-        qf[i] = (active && c < p.d) ? load4(qp + c) * p.qscale : vf4{0.f, 0.f, 0.f, 0.f};
+        const vf4 x = (active && c < p.d) ? load4(qp + c) * p.qscale : vf4{0.f, 0.f, 0.f, 0.f};
+        if (i < QC - QL) qf[i < QC - QL ? i : 0] = x;
+        else *reinterpret_cast<vf4*>(qs + ((wave * QL + i - (QC - QL)) * 64 + lane) * 4) = x;
     }
+    if (QL > 0) __syncthreads();
 
     const float* kb = p.k.p + bi * p.k.sb + kvh * p.k.sh;
     const float* vb = p.v.p + bi * p.v.sb + kvh * p.v.sh;
@@ -281,7 +307,9 @@ __global__ __launch_bounds__(64 * DW, 1) void deep_attention_kernel(const DeepPa
 #pragma unroll
                     for (int i = 0; i < 4; ++i) {
                         const vf4 kk = kg[gi & 1][i];
-                        const vf4 qq = qf[KP + 4 * gi + i];
+                        const int ci = KP + 4 * gi + i;
+                        const vf4 qq = ci >= QC - QL ? load4(qs + ((wave * QL + ci - (QC - QL)) * 64 + lane) * 4)
+                                                     : qf[ci < QC - QL ? ci : 0];
                         s = __builtin_amdgcn_mfma_f32_32x32x2f32(kk[0], qq[0], s, 0, 0, 0);
                         s = __builtin_amdgcn_mfma_f32_32x32x2f32(kk[1], qq[1], s, 0, 0, 0);
                         s = __builtin_amdgcn_mfma_f32_32x32x2f32(kk[2], qq[2], s, 0, 0, 0);
@@ -321,19 +349,27 @@ __global__ __launch_bounds__(64 * DW, 1) void deep_attention_kernel(const DeepPa
                     vf4{s[4 * i], s[4 * i + 1], s[4 * i + 2], s[4 * i + 3]};
         }
         __syncthreads();   // the tile's partials visible
-        // Wave w adds elements [128w, 128w + 128) of the 8 partials in wave
-        // order, then every wave reads the whole sum.
+        // Wave w adds elements [XW/DW w, XW/DW (w + 1)) of the DW partials in
+        // wave order, then every wave reads the whole sum.
         {
             float* rb = red + (it & 1) * XW;
-            const int e = 128 * wave + 2 * lane;
-            float2 a = *reinterpret_cast<const float2*>(xb + e);
+            if (DW == 8) {
+                const int e = 128 * wave + 2 * lane;
+                float2 a = *reinterpret_cast<const float2*>(xb + e);
 #pragma unroll
-            for (int w = 1; w < DW; ++w) {
-                const float2 x = *reinterpret_cast<const float2*>(xb + w * XW + e);
-                a.x += x.x;
-                a.y += x.y;
+                for (int w = 1; w < DW; ++w) {
+                    const float2 x = *reinterpret_cast<const float2*>(xb + w * XW + e);
+                    a.x += x.x;
+                    a.y += x.y;
+                }
+                *reinterpret_cast<float2*>(rb + e) = a;
+            } else {
+                const int e = 256 * wave + 4 * lane;
+                vf4 a = load4(xb + e);
+#pragma unroll
+                for (int w = 1; w < DW; ++w) a += load4(xb + w * XW + e);
+                *reinterpret_cast<vf4*>(rb + e) = a;
             }
-            *reinterpret_cast<float2*>(rb + e) = a;
             __syncthreads();
             if (nob == 0) continue;
 #pragma unroll
@@ -502,7 +538,7 @@ __global__ __launch_bounds__(256) void deep_combine_kernel(const DeepParams p) {
     }
 }
 
-template <bool CAUSAL, int QC, int OB, bool STREAMQ>
+template <bool CAUSAL, int DW, int QC, int OB, bool STREAMQ>
 hipError_t launch_deep_v(DeepParams p, hipStream_t stream) {
     // (The split is a template parameter: its tile range and record path cost
     // the unsplit kernel 35 VGPRs and 7 % at d = 512 when shared.)
@@ -522,110 +558,51 @@ hipError_t launch_deep_v(DeepParams p, hipStream_t stream) {
     p.n_oc = (int)n_oc;
     p.total = (int)total;
     p.per_xcd = (int)((total + 7) / 8);
+    // Causal units longest first across the XCD's KV heads on the 8-wave form
+    // (its one or two rounds then end together: B = 1, H = 16, T = 1024, d =
+    // 512 185 -> 176 us).  The 4-wave form runs many rounds and keeps a KV
+    // head's units together in the XCD's L2: across heads it read 2.4x the
+    // bytes from beyond the L2 (d = 512 line 3.9 against 1.6 GB) for 0.7 %.
+    p.order_hpx = DW == 8 && CAUSAL && p.n_split == 1 && ((int64_t)p.B * p.Hkv) % 8 == 0 ? p.B * p.Hkv / 8 : 0;
     if (p.n_split == 1) {
-        hipLaunchKernelGGL((deep_attention_kernel<CAUSAL, QC, OB, STREAMQ, false>),
+        hipLaunchKernelGGL((deep_attention_kernel<CAUSAL, DW, QC, OB, STREAMQ, false>),
                            dim3(8 * p.per_xcd), dim3(64 * DW), 0, stream, p);
         return hipGetLastError();
     }
-    hipLaunchKernelGGL((deep_attention_kernel<CAUSAL, QC, OB, STREAMQ, true>), dim3(8 * p.per_xcd),
-                       dim3(64 * DW), 0, stream, p);
-    hipError_t e = hipGetLastError();
-    if (e != hipSuccess) return e;
-    hipLaunchKernelGGL(deep_combine_kernel, dim3((unsigned)base), dim3(256), 0, stream, p);
-    return hipGetLastError();
+    if constexpr (DW == 8) {
+        hipLaunchKernelGGL((deep_attention_kernel<CAUSAL, DW, QC, OB, STREAMQ, true>), dim3(8 * p.per_xcd),
+                           dim3(64 * DW), 0, stream, p);
+        hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+        hipLaunchKernelGGL(deep_combine_kernel, dim3((unsigned)base), dim3(256), 0, stream, p);
+        return hipGetLastError();
+    }
+    return hipErrorInvalidValue;   // (the 4-wave form serves unsplit launches only)
 }
 
+// Up to 512 dims, problems of full 32-row units with more workgroups than
+// CUs (causal: more than two per CU) run the 4-wave form.  Fewer workgroups
+// keep 8 waves busy on a CU to the end (a causal launch of 2 workgroups per
+// CU ran 10 % slower on the 4-wave form: once a CU's short unit ends, its
+// long one runs alone with one wave per SIMD), and so do decode steps (a few
+// rows per unit, streaming their caches: B = 32, d = 512 634 us with 8
+// waves, 781 us with 4).
 template <bool CAUSAL>
-hipError_t launch_deep_t(const DeepParams& p, hipStream_t stream) {
-    if (p.d <= 8 * DW * 8) return launch_deep_v<CAUSAL, 8, 2, false>(p, stream);
-    if (p.d <= 8 * DW * 16) return launch_deep_v<CAUSAL, 16, 2, false>(p, stream);
-    return launch_deep_v<CAUSAL, 16, 2, true>(p, stream);
+hipError_t launch_deep_t(const DeepParams& p, int cus, hipStream_t stream) {
+    const int64_t rows = (int64_t)p.G * p.Tq, units = (rows + 31) / 32;
+    const int64_t wg = (int64_t)p.B * p.Hkv * units * ((p.d + kDeepChunk - 1) / kDeepChunk);
+    if (p.d <= 512 && p.n_split == 1 && rows >= 32 && wg > (CAUSAL ? 2 : 1) * (int64_t)cus)
+        return launch_deep_v<CAUSAL, 4, 16, 4, false>(p, stream);
+    if (p.d <= 512) return launch_deep_v<CAUSAL, 8, 8, 2, false>(p, stream);
+    if (p.d <= 1024) return launch_deep_v<CAUSAL, 8, 16, 2, false>(p, stream);
+    return launch_deep_v<CAUSAL, 8, 16, 2, true>(p, stream);
 }
 
 }  // namespace
 
-// Problems with at most half as many workgroups as CUs (decode steps of
-// small batches, few-query cross-attention) split each unit's keys into up to
-// kDeepMaxSplit parts of at least 4 tiles, one round of workgroups over the
-// CUs, as far as max_bytes of records allow.  (Measured at d = 512, decode
-// over L ~ U[512, 4096]: B = 8 601 -> 190 us with 4 parts; at B = 32, where
-// every CU already has a head, 4 parts per head cost 667 -> 775 us: each
-// extra workgroup pays its cold start, its record and the merge.)
-uint64_t deep_split_plan(DeepParams& p, int max_tiles, int cus, uint64_t max_bytes) {
-    p.n_split = 1;
-    p.split_tiles = 0;
-    const int64_t rows = (int64_t)p.G * p.Tq;
-    p.rpu = (int)(rows < 32 ? rows : 32);
-    const int64_t wg = (int64_t)p.B * p.Hkv * ((rows + 31) / 32) * ((p.d + kDeepChunk - 1) / kDeepChunk);
-    if (wg == 0 || 2 * wg > (int64_t)cus || max_tiles < 8) return 0;
-    int64_t sp = (int64_t)cus / wg;
-    if (sp > kDeepMaxSplit) sp = kDeepMaxSplit;
-    if (sp > max_tiles / 4) sp = max_tiles / 4;
-    const uint64_t per = (uint64_t)wg * (uint64_t)p.rpu * (kDeepChunk + 2) * 4u;
-    while (sp > 1 && per * (uint64_t)sp > max_bytes) --sp;
-    if (sp <= 1) return 0;
-    p.n_split = (int)sp;
-    p.split_tiles = (int)((max_tiles + sp - 1) / sp);
-    return per * (uint64_t)sp;
-}
-
-// Decode over ragged lengths (one unit and one output chunk per (sequence,
-// KV head) pair, at most kDeepMaxHeads pairs): each pair's keys are cut into
-// parts of `target` tiles -- at least 4, at most kDeepMaxSplit parts per pair,
-// all parts in one round of workgroups over the CUs -- so a long sequence no
-// longer sets the step's time on one CU while the others idle.  Used when
-// that shortens the longest workgroup by a quarter or more.  (Measured at
-// d = 512, L ~ U[512, 4096], Hq = 32, Hkv = 8: B = 8 571 -> 148 us, against
-// 190 us for equal parts per pair; allowing two rounds, so that B = 32 could
-// split too, made B = 8 261 us and B = 32 916 against 628 us unsplit: a part
-// dispatched in the second round starts only when a CU's first one ends.)
-uint64_t deep_ragged_plan(DeepParams& p, const int32_t* seq_keys, int cus, uint64_t max_bytes) {
-    p.ragged = 0;
-    const int64_t rows = (int64_t)p.G * p.Tq;
-    const int64_t heads = (int64_t)p.B * p.Hkv;
-    if (rows > 32 || p.d > kDeepChunk || heads == 0 || heads > kDeepMaxHeads || !seq_keys) return 0;
-    int64_t total = 0, longest = 0;
-    for (int b = 0; b < p.B; ++b) {
-        const int64_t t = ((int64_t)seq_keys[b] + 31) / 32;
-        total += t * p.Hkv;
-        longest = longest > t ? longest : t;
-    }
-    auto parts_of = [&](int64_t target) {
-        int64_t n = 0;
-        for (int b = 0; b < p.B; ++b) {
-            const int64_t t = ((int64_t)seq_keys[b] + 31) / 32;
-            n += (t > target ? (t + target - 1) / target : 1) * p.Hkv;
-        }
-        return n;
-    };
-    int64_t target = (total + cus - 1) / cus;
-    if (target < 4) target = 4;
-    if (target < (longest + kDeepMaxSplit - 1) / kDeepMaxSplit) target = (longest + kDeepMaxSplit - 1) / kDeepMaxSplit;
-    while (parts_of(target) > cus) ++target;
-    if (4 * longest < 5 * target) return 0;   // no pair's time shrinks enough to pay the split
-    const int64_t n = parts_of(target);
-    p.rpu = (int)(rows < 32 ? rows : 32);
-    const uint64_t bytes = (uint64_t)n * (uint64_t)p.rpu * (kDeepChunk + 2) * 4u;
-    if (bytes > max_bytes || n > 65535) return 0;
-    int64_t at = 0;
-    for (int b = 0; b < p.B; ++b) {
-        const int64_t t = ((int64_t)seq_keys[b] + 31) / 32;
-        const int64_t parts = t > target ? (t + target - 1) / target : 1;
-        for (int k = 0; k < p.Hkv; ++k) {
-            p.part_prefix[b * p.Hkv + k] = (uint16_t)at;
-            at += parts;
-        }
-    }
-    p.part_prefix[heads] = (uint16_t)at;
-    p.ragged = 1;
-    p.n_split = kDeepMaxSplit;   // marks a split launch; parts per pair come from part_prefix
-    p.split_tiles = (int)target;
-    return bytes;
-}
-
-hipError_t launch_deep(DeepParams p, bool causal, hipStream_t stream) {
+hipError_t launch_deep(DeepParams p, bool causal, int cus, hipStream_t stream) {
     if (p.d <= 256 || p.d % 4 != 0 || p.Hkv <= 0 || p.G <= 0) return hipErrorInvalidValue;
-    return causal ? launch_deep_t<true>(p, stream) : launch_deep_t<false>(p, stream);
+    return causal ? launch_deep_t<true>(p, cus, stream) : launch_deep_t<false>(p, cus, stream);
 }
 
 }  // namespace nne

@@ -4,6 +4,7 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "deep_plan.hpp"
 #include "nne_common.hpp"
 
 namespace nne {
@@ -24,17 +25,10 @@ hipError_t launch_prefill(PrefillParams p, bool causal, bool vec, hipStream_t st
 hipError_t launch_prefill_wide(PrefillParams p, bool causal, hipStream_t stream);
 // Head dims above 256 (deep.hip; d % 4 == 0, 16-byte vector views of Q, K,
 // V and O): prefill, cross-attention and decode over a KV cache (p.lens).
-// deep_split_plan fills p.n_split / p.split_tiles / p.rpu for a problem whose
-// units have at most max_tiles 32-key tiles, with records of at most
-// max_bytes, and returns the record bytes (0: no split); the caller sets p.ws
-// when that is non-zero.  launch_deep fills the schedule fields and runs the
-// kernel (and the combine kernel after a split).
-uint64_t deep_split_plan(DeepParams& p, int max_tiles, int cus, uint64_t max_bytes);
-// Ragged key split of a decode step (seq_keys: host key counts per sequence
-// after the step): fills p.ragged / p.part_prefix / p.split_tiles / p.rpu and
-// returns the record bytes, or 0 when the step does not gain from it.
-uint64_t deep_ragged_plan(DeepParams& p, const int32_t* seq_keys, int cus, uint64_t max_bytes);
-hipError_t launch_deep(DeepParams p, bool causal, hipStream_t stream);
+// The key-split plans (deep_plan.hpp) fill p.n_split and its fields first;
+// launch_deep fills the schedule fields and runs the kernel (and the combine
+// kernel after a split) on a device of `cus` CUs.
+hipError_t launch_deep(DeepParams p, bool causal, int cus, hipStream_t stream);
 // Key-split plan for a prefill problem too small to fill the device (fills
 // p.n_chunks / p.chunk_tiles; n_chunks stays 0 when the problem is large
 // enough).  The caller then sets p.ws (ws_bytes) and p.cnt (n_counters zeroed

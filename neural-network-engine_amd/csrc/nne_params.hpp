@@ -82,6 +82,7 @@ struct PrefillParams {
 // key c is visible to position t iff c <= t + q_offset.
 constexpr int kDeepChunk = 512;
 constexpr int kDeepMaxHeads = 512;   // (sequence, KV head) pairs of a ragged key split
+constexpr int kDeepMaxSplit = 8;     // key parts per unit of a key split
 
 struct DeepParams {
     View4 q, k, v;
@@ -94,6 +95,9 @@ struct DeepParams {
     int n_oc;        // ceil(d / kDeepChunk) output chunks per unit
     int total;       // B * Hkv * n_units * n_oc * n_split workgroups
     int per_xcd;     // ceil(total / 8)
+    // Causal launches over whole KV heads per XCD (B * Hkv % 8 == 0):
+    // order_hpx heads per XCD, units taken longest first across them.
+    int order_hpx;
     // Key split (n_split > 1, up to 8 parts; problems with too few units to
     // fill the device): workgroup s of a (unit, chunk) streams the unit's key tiles
     // [s * split_tiles, (s + 1) * split_tiles) and leaves a partial record in

@@ -79,6 +79,7 @@ def test_decode_group_sizes_and_head_dims(nne, cuda, b, hq, hkv, d, append):
     (2, 16, 1, 1028, True),    # MQA, two output chunks
     (4, 64, 8, 384, True),     # G = 8
     (32, 16, 4, 384, True),    # 128 ragged pairs: the long sequence in several parts
+    (40, 32, 8, 512, True),    # 320 pairs, more than the CUs: no ragged split
 ])
 def test_decode_head_dims_above_256(nne, cuda, b, hq, hkv, d, append):
     print("case decode deep b=%d hq=%d hkv=%d d=%d append=%s" % (b, hq, hkv, d, append), flush=True)

@@ -361,6 +361,7 @@ def test_head_dims_above_128(nne, cuda, b, hq, hkv, tq, tk, d, causal, q_off):
     (3, 5, 5, 100, 37, 768, False, 0),      # Tk < Tq
     (2, 4, 4, 3, 300, 640, True, 297),      # a few rows at the end of a long cache
     (1, 8, 2, 257, 257, 512, True, 0),      # GQA, units that straddle query heads
+    (1, 8, 2, 64, 96, 512, True, 32),       # GQA, units by query position blocks
 ])
 def test_head_dims_above_256(nne, cuda, b, hq, hkv, tq, tk, d, causal, q_off):
     """Above 256 dims (the reference's attention takes any head dim,
@@ -377,6 +378,34 @@ def test_head_dims_above_256(nne, cuda, b, hq, hkv, tq, tk, d, causal, q_off):
     T.assert_close(got[:, :, r0:], ref, what="d=%d" % d)
     if hq == hkv and tq == tk and q_off == 0:
         T.assert_close(got, T.ref_flash(q, k, v, causal), what="d=%d flash" % d)
+
+
+@pytest.mark.parametrize("b,hq,hkv,tq,tk,d,causal,q_off,layout", [
+    (1, 24, 24, 1024, 1024, 512, True, 0, 0),    # 768 units, causal
+    (1, 24, 24, 1024, 1024, 512, True, 0, 1),    # the same on [B, T, H, d] views
+    (2, 32, 8, 512, 700, 320, True, 188, 0),     # GQA by query position blocks, offset
+    (8, 32, 8, 100, 100, 512, True, 0, 0),       # GQA, units straddling query heads
+    (1, 32, 32, 512, 600, 260, False, 0, 0),     # a last chunk with 4 valid dims of 8
+    (2, 64, 8, 256, 256, 384, True, -10, 0),     # G = 8, rows that see no key
+    (3, 24, 24, 230, 77, 448, False, 0, 1),      # Tk < Tq, a partial last unit, views
+])
+def test_deep_four_wave_form(nne, cuda, b, hq, hkv, tq, tk, d, causal, q_off, layout):
+    """Prefill problems of more workgroups than CUs (causal: more than two
+    per CU; 257+ and 513+ units on the 256-CU MI355X) run the deep kernel's
+    4-wave form: two workgroups per CU, S from 4 partials, half of each
+    wave's Q^T in LDS."""
+    print("case deep four-wave", b, hq, hkv, tq, tk, d, causal, q_off, layout, flush=True)
+    s = 29 * tq + d
+    q, k, v = rnd(s, b, hq, tq, d), rnd(s + 1, b, hkv, tk, d), rnd(s + 2, b, hkv, tk, d)
+    if layout == 0:
+        qd, kd, vd = dev(q, cuda), dev(k, cuda), dev(v, cuda)
+    else:
+        qd, kd, vd = (dev(x.transpose(0, 2, 1, 3), cuda).transpose(1, 2) for x in (q, k, v))
+    got = host(nne.attention_forward(qd, kd, vd, causal, q_offset=q_off))
+    r0 = max(0, -q_off) if causal else 0
+    assert not got[:, :, :r0].any()
+    ref = T.ref_standard(q[:, :, r0:], k, v, causal, start_pos=q_off + r0)
+    T.assert_close(got[:, :, r0:], ref, what="d=%d four-wave" % d)
 
 
 @pytest.mark.parametrize("b,hq,hkv,tq,tk,d,causal,q_off", [
