@@ -47,13 +47,13 @@ PEAK_HBM_GBS = 8000.0
 # of split heads).  Config 5b: 123.4 + 0.33 (algorithmic 123.2 + 0.33).  Config-3
 # decode prologue: 109.2 + 4.7 (algorithmic 101.2 + 0.8; partial tiles and x per
 # XCD).  GPT-2 decode attend: 104.4 + 0.3 (algorithmic 104.2 + 0.3).  Config 1:
-# 1.1 + 0.26 (algorithmic 0.79 + 0.26).  Config 4: 272.1 + 67.1 (algorithmic
+# 1.1 + 0.26 (algorithmic 0.79 + 0.26).  Config 4: 272.2 + 67.1 (algorithmic
 # 201.3 + 67.1; the persistent workgroups of a KV head on one XCD re-fetch part of
 # its 8.4 MB of K/V, more than the XCD's 4 MB L2).  Config 5a: 187.0 + 61.4
 # (algorithmic 184.3 + 61.4).  G = 8 decode step: 677.2 + 3.25 (algorithmic
 # 681.3 + 1.3, plus the 16-row partial records of split heads).  d = 256 causal
 # prefill (B = 1, H = 16, T = 4096): 260.3 + 67.8 (algorithmic 201.3 + 67.1).  d = 512
-# causal prefill (deep kernel, same shape): 1236.7 + 134.2 (algorithmic 402.7 + 134.2;
+# causal prefill (deep kernel, same shape): 1585.6 + 134.2 (algorithmic 402.7 + 134.2;
 # the units of a KV head re-fetch its 16.8 MB of K/V, more than the XCD's 4 MB L2).
 TRAFFIC_PREFILL_CONFIG2 = round(224.4e6 + 134.2e6)
 TRAFFIC_DECODE_CONFIG3_STEP = round(646.0e6 + 1.8e6)
@@ -61,11 +61,11 @@ TRAFFIC_CROSS_CONFIG5B = round(123.4e6 + 0.33e6)
 TRAFFIC_PROLOGUE_CONFIG3 = round(109.2e6 + 4.7e6)
 TRAFFIC_ATTEND_GPT2 = round(104.4e6 + 0.3e6)
 TRAFFIC_PREFILL_CONFIG1 = round(1.1e6 + 0.26e6)
-TRAFFIC_PREFILL_CONFIG4 = round(272.1e6 + 67.1e6)
+TRAFFIC_PREFILL_CONFIG4 = round(272.2e6 + 67.1e6)
 TRAFFIC_PREFILL_CONFIG5A = round(187.0e6 + 61.4e6)
 TRAFFIC_DECODE_G8_STEP = round(677.2e6 + 3.25e6)
 TRAFFIC_PREFILL_D256 = round(260.3e6 + 67.8e6)
-TRAFFIC_PREFILL_D512 = round(1236.7e6 + 134.2e6)
+TRAFFIC_PREFILL_D512 = round(1585.6e6 + 134.2e6)
 
 
 def cpu_threads():
