@@ -223,6 +223,21 @@ int deep_workspace(nne::DeepParams& p, int max_tiles, const nne_workspace_t* wsp
     return NNE_OK;
 }
 
+// Head dims 129-256 with more query rows per KV head than the split-K kernel
+// takes: the wave-pair kernel at d = 256 when its work items (4 units of 32
+// rows each) fill the device, else the deep kernel's 2-wave form, which pads
+// no dims to 256 and spreads (or key-splits) small problems over the CUs.
+// (Measured: d = 192 B = 8, H = 20, T = 1500 3.32 -> 2.56 ms; d = 256 causal
+// B = 1, H = 8, T = 1024 0.28 -> 0.17 ms; at d = 256 with the device full the
+// wave-pair kernel is level or up to 2 % faster.)
+bool wide_on_deep(int64_t B, int64_t Hkv, int64_t G, int64_t Tq, int d) {
+    if (nne::prefill_padded_dim(d) != 0 || nne::splitk_padded_dim(d) == 0) return false;
+    if (G * Tq <= nne::splitk_max_rows()) return false;
+    if (d != 256) return true;
+    const int64_t items = B * Hkv * ((G * ((Tq + 31) / 32) + 3) / 4);
+    return items < device_cus();
+}
+
 // Records of the largest key split a deep-kernel problem of these shapes
 // takes (max_tiles: tiles of its longest unit; 0 when unknown).  A decode
 // step (Tq = 1) may take the ragged split instead: at most one record of its
@@ -249,11 +264,11 @@ int run_attention(const float* q, const int64_t* qs_, const int64_t* qst, const 
     const int B = (int)qs_[0], Hq = (int)qs_[1], Tq = (int)qs_[2], d = (int)qs_[3];
     const int Hkv = (int)ks_[1], Tk = (int)ks_[2];
     if ((int64_t)B * Hq * Tq == 0 || d == 0) return NNE_OK;
-    // Head dims above 128 (d <= 256) run on the wave-pair MFMA kernel, or on
-    // the split-K kernel when a KV head has few query rows; above 256 on the
-    // deep kernel.
+    // Head dims above 128 (d <= 256) run on the wave-pair MFMA kernel or the
+    // deep kernel's 2-wave form (wide_on_deep), or on the split-K kernel when a
+    // KV head has few query rows; above 256 on the deep kernel.
     const bool wide = nne::prefill_padded_dim(d) == 0;
-    const bool deep = wide && nne::splitk_padded_dim(d) == 0;
+    const bool deep = wide && (nne::splitk_padded_dim(d) == 0 || wide_on_deep(B, Hkv, Hq / Hkv, Tq, d));
     // Offsets beyond +-2^30 cannot change visibility for int32 lengths.
     const int qoff = (int)std::max<int64_t>(-(1 << 30), std::min<int64_t>(q_offset, 1 << 30));
     const bool vec = d % 4 == 0 && vec_view(q, qst) && vec_view(k, kst) && vec_view(v, vst) &&
@@ -399,7 +414,9 @@ nne_workspace_size_t attention_workspace(const int64_t* qs_, const int64_t* ks_,
     const int Hkv = (int)ks_[1], Tk = (int)ks_[2];
     if ((int64_t)B * Hq * Tq == 0 || d == 0 || Hkv == 0) return r;
     const int qoff = (int)std::max<int64_t>(-(1 << 30), std::min<int64_t>(q_offset, 1 << 30));
-    if (nne::splitk_padded_dim(d) == 0) {   // above 256 dims: the deep kernel's key split
+    // The deep kernel's key split: above 256 dims, and head dims 129-256 on its
+    // 2-wave form.
+    if (nne::splitk_padded_dim(d) == 0 || (Hq % Hkv == 0 && wide_on_deep(B, Hkv, Hq / Hkv, Tq, d))) {
         if (d % 4 == 0 && Hq % Hkv == 0)
             r.records_bytes = deep_workspace_bytes(B, Hq, Hkv, Tq, d, deep_max_tiles(Tk, causal, qoff, Tq));
         return r;

@@ -72,23 +72,26 @@ __device__ __forceinline__ int clamp_keys(int64_t x, int tk) {
 // DW waves per workgroup.  Per wave: QC chunks of S (STREAMQ: further chunks
 // read again each tile) and OB output blocks (the workgroup's output chunk is
 // 32 * DW * OB dims).  Q^T of the chunks stays in registers, except that the
-// 4-wave form keeps its last 8 chunks in LDS.  KP chunks of the next tile's K
-// are loaded during the current tile, and VP key steps of a tile's V at its
-// start; the rest is loaded in groups of 4 inside its phase.  8 waves: one
-// workgroup per CU; 4 waves: two per CU, whose exchanges and softmaxes
-// interleave with each other's MFMAs.
+// 4- and 2-wave forms keep their last 8 chunks in LDS.  KP chunks of the next
+// tile's K are loaded during the current tile, and VP key steps of a tile's V
+// at its start; the rest is loaded in groups of 4 inside its phase.  8 waves:
+// one workgroup per CU; 4 waves: two per CU, 2 waves (head dims up to 256):
+// four per CU, whose exchanges and softmaxes interleave with each other's
+// MFMAs.
 template <bool CAUSAL, int DW, int QC, int OB, bool STREAMQ, bool SPLIT>
-__global__ __launch_bounds__(64 * DW, 8 / DW) void deep_attention_kernel(const DeepParams p) {
-    static_assert(DW == 8 || (DW == 4 && QC == 16 && !SPLIT && !STREAMQ), "the two workgroup forms");
-    constexpr int KP = DW == 4 ? 4 : (QC < 8 ? QC : 8);
+__global__ __launch_bounds__(64 * DW, DW == 8 ? 1 : 2) void deep_attention_kernel(const DeepParams p) {
+    static_assert(DW == 8 || ((DW == 4 || DW == 2) && QC == 16 && OB == 4 && !SPLIT && !STREAMQ),
+                  "the workgroup forms");
+    constexpr int KP = DW <= 4 ? 4 : (QC < 8 ? QC : 8);
     constexpr int VP = OB <= 2 ? 16 : 4;
-    constexpr int QL = DW == 4 ? 8 : 0;  // Q^T chunks in LDS (the last QL of QC)
+    constexpr int QL = DW <= 4 ? 8 : 0;  // Q^T chunks in LDS (the last QL of QC)
     constexpr int CB = 32 * DW;          // dims between a wave's output blocks
     __shared__ __attribute__((aligned(16))) float xs[2 * DW * XW];
     __shared__ __attribute__((aligned(16))) float red[2 * XW];
     __shared__ __attribute__((aligned(16))) float qs[QL > 0 ? DW * QL * 256 : 4];
 
-    static_assert(32 * DW * OB == kDeepChunk, "output chunk of one workgroup");
+    // Output chunk of one workgroup: kDeepChunk dims (256 on the 2-wave form, unsplit only).
+    static_assert(32 * DW * OB == kDeepChunk || (DW == 2 && !SPLIT), "output chunk of one workgroup");
     // Key-split launches (few units, no K/V sharing between them worth an
     // L2) deal the workgroups round-robin over the XCDs instead, so that the
     // parts of ragged sequences spread over the whole device.
@@ -364,11 +367,14 @@ __global__ __launch_bounds__(64 * DW, 8 / DW) void deep_attention_kernel(const D
                 }
                 *reinterpret_cast<float2*>(rb + e) = a;
             } else {
-                const int e = 256 * wave + 4 * lane;
-                vf4 a = load4(xb + e);
 #pragma unroll
-                for (int w = 1; w < DW; ++w) a += load4(xb + w * XW + e);
-                *reinterpret_cast<vf4*>(rb + e) = a;
+                for (int e4 = 0; e4 < XW / DW / 256; ++e4) {
+                    const int e = (XW / DW) * wave + 4 * lane + 256 * e4;
+                    vf4 a = load4(xb + e);
+#pragma unroll
+                    for (int w = 1; w < DW; ++w) a += load4(xb + w * XW + e);
+                    *reinterpret_cast<vf4*>(rb + e) = a;
+                }
             }
             __syncthreads();
             if (nob == 0) continue;
@@ -544,7 +550,7 @@ hipError_t launch_deep_v(DeepParams p, hipStream_t stream) {
     // the unsplit kernel 35 VGPRs and 7 % at d = 512 when shared.)
     const int64_t rows = (int64_t)p.G * p.Tq;
     const int64_t units = (rows + 31) / 32;
-    const int64_t n_oc = (p.d + kDeepChunk - 1) / kDeepChunk;
+    const int64_t n_oc = (p.d + 32 * DW * OB - 1) / (32 * DW * OB);
     if (p.n_split < 1 || (p.n_split > 1 && (!p.ws || p.n_split > kDeepMaxSplit || p.split_tiles < 1 ||
                                             p.rpu != (int)(rows < 32 ? rows : 32))))
         return hipErrorInvalidValue;
@@ -587,8 +593,11 @@ hipError_t launch_deep_v(DeepParams p, hipStream_t stream) {
 // long one runs alone with one wave per SIMD), and so do decode steps (a few
 // rows per unit, streaming their caches: B = 32, d = 512 634 us with 8
 // waves, 781 us with 4).
+// Head dims 129-256 (prefill the wave-pair kernel does not take) run the
+// 2-wave form unsplit, and the 8-wave form's key split.
 template <bool CAUSAL>
 hipError_t launch_deep_t(const DeepParams& p, int cus, hipStream_t stream) {
+    if (p.d <= 256 && p.n_split == 1) return launch_deep_v<CAUSAL, 2, 16, 4, false>(p, stream);
     const int64_t rows = (int64_t)p.G * p.Tq, units = (rows + 31) / 32;
     const int64_t wg = (int64_t)p.B * p.Hkv * units * ((p.d + kDeepChunk - 1) / kDeepChunk);
     if (p.d <= 512 && p.n_split == 1 && rows >= 32 && wg > (CAUSAL ? 2 : 1) * (int64_t)cus)
@@ -601,7 +610,7 @@ hipError_t launch_deep_t(const DeepParams& p, int cus, hipStream_t stream) {
 }  // namespace
 
 hipError_t launch_deep(DeepParams p, bool causal, int cus, hipStream_t stream) {
-    if (p.d <= 256 || p.d % 4 != 0 || p.Hkv <= 0 || p.G <= 0) return hipErrorInvalidValue;
+    if (p.d <= 128 || p.d % 4 != 0 || p.Hkv <= 0 || p.G <= 0) return hipErrorInvalidValue;
     return causal ? launch_deep_t<true>(p, cus, stream) : launch_deep_t<false>(p, cus, stream);
 }
 

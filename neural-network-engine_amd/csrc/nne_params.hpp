@@ -74,10 +74,12 @@ struct PrefillParams {
     uint16_t part_prefix[kMaxSplitItems + 1];
 };
 
-// Head dims above 256 (deep.hip), prefill, cross-attention and decode alike.
-// The G * Tq query rows of a KV head are flattened (row r: query head
-// kvh * G + r / Tq, position r % Tq) and cut into 32-row units; a workgroup
-// serves one unit and one kDeepChunk-dim chunk of the output dims.  Sequence
+// Head dims above 256 (deep.hip), prefill, cross-attention and decode alike,
+// and prefill at 129-256 dims the wave-pair kernel does not take.  The G * Tq
+// query rows of a KV head are flattened (row r: query head kvh * G + r / Tq,
+// position r % Tq) and cut into 32-row units; a workgroup serves one unit and
+// one kDeepChunk-dim chunk of the output dims (256 dims on the 2-wave form,
+// which runs unsplit).  Sequence
 // b has lens[b] keys when lens != null (a KV cache), else Tk; with `causal`,
 // key c is visible to position t iff c <= t + q_offset.
 constexpr int kDeepChunk = 512;
@@ -92,7 +94,7 @@ struct DeepParams {
     int q_offset;
     float qscale;    // softmax scale * log2(e), folded into Q
     int n_units;     // ceil(G * Tq / 32) per KV head
-    int n_oc;        // ceil(d / kDeepChunk) output chunks per unit
+    int n_oc;        // output chunks per unit
     int total;       // B * Hkv * n_units * n_oc * n_split workgroups
     int per_xcd;     // ceil(total / 8)
     // Causal launches over whole KV heads per XCD (B * Hkv % 8 == 0):

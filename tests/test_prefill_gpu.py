@@ -334,8 +334,11 @@ def test_stream_release_frees_and_reallocates(nne, cuda):
 def test_head_dims_above_128(nne, cuda, b, hq, hkv, tq, tk, d, causal, q_off):
     """flash_attention_forward takes any head dim (flash_attention.rs:39-48):
     d in (128, 256] runs on the wave-pair MFMA kernel (each 32-row unit on two
-    waves, one per half of the head dim), or on the split-K kernel when a KV
-    head has at most 16 query rows."""
+    waves, one per half of the head dim) when its work items fill the device
+    at d = 256, else on the deep kernel (its 2-wave form, or its key split for
+    problems of few units), or on the split-K kernel when a KV head has at
+    most 16 query rows.  (These shapes are small: all but the split-K ones
+    take the deep kernel.)"""
     print("case wide head dim", b, hq, hkv, tq, tk, d, causal, q_off, flush=True)
     s = 17 * tq + d
     q, k, v = rnd(s, b, hq, tq, d), rnd(s + 1, b, hkv, tk, d), rnd(s + 2, b, hkv, tk, d)
@@ -460,6 +463,58 @@ def test_deep_head_dim_strided_views_and_repeat(nne, cuda):
     ref = T.ref_flash(qt.transpose(0, 2, 1, 3), kt.transpose(0, 2, 1, 3),
                       vt.transpose(0, 2, 1, 3), True)
     T.assert_close(first.transpose(0, 2, 1, 3), ref, what="d=512 strided")
+
+
+@pytest.mark.parametrize("b,hq,hkv,tq,tk,d,causal,q_off,layout", [
+    (2, 16, 16, 256, 256, 192, True, 0, 0),      # 256 units, unsplit
+    (2, 16, 16, 256, 256, 192, True, 0, 1),      # the same on [B, T, H, d] views
+    (2, 16, 4, 300, 350, 160, True, 50, 0),      # GQA, units straddling query heads, offset
+    (1, 32, 8, 256, 256, 256, True, 0, 0),       # d = 256 with too few wave-pair items
+    (3, 8, 8, 130, 90, 228, False, 0, 0),        # Tk < Tq, a half-valid last 8-dim chunk
+    (1, 4, 4, 64, 1500, 192, False, 0, 0),       # 8 units: the 8-wave key split at d = 192
+])
+def test_deep_two_wave_form(nne, cuda, b, hq, hkv, tq, tk, d, causal, q_off, layout):
+    """Head dims 129-256 that the wave-pair kernel does not take (dims other
+    than 256, or too few of its 4-unit items to fill the device) run the deep
+    kernel: its 2-wave form, four workgroups per CU (a wave pair per 32-row
+    unit, Q^T half in LDS), or for few units its 8-wave key split."""
+    print("case deep two-wave", b, hq, hkv, tq, tk, d, causal, q_off, layout, flush=True)
+    s = 31 * tq + d
+    q, k, v = rnd(s, b, hq, tq, d), rnd(s + 1, b, hkv, tk, d), rnd(s + 2, b, hkv, tk, d)
+    if layout == 0:
+        qd, kd, vd = dev(q, cuda), dev(k, cuda), dev(v, cuda)
+    else:
+        qd, kd, vd = (dev(x.transpose(0, 2, 1, 3), cuda).transpose(1, 2) for x in (q, k, v))
+    got = host(nne.attention_forward(qd, kd, vd, causal, q_offset=q_off))
+    r0 = max(0, -q_off) if causal else 0
+    assert not got[:, :, :r0].any()
+    ref = T.ref_standard(q[:, :, r0:], k, v, causal, start_pos=q_off + r0)
+    T.assert_close(got[:, :, r0:], ref, what="d=%d two-wave" % d)
+
+
+@pytest.mark.parametrize("b,hq,hkv,t,causal", [
+    (2, 16, 16, 1024, False),    # 256 items of 4 units: the wave-pair kernel
+    (1, 32, 8, 1024, True),      # GQA, 256 items
+])
+def test_wave_pair_kernel_full_device(nne, cuda, b, hq, hkv, t, causal):
+    """d = 256 problems whose wave-pair items fill the device stay on the
+    wave-pair kernel: sampled rows of sampled heads against the oracle, every
+    output finite."""
+    print("case wave-pair full device", b, hq, hkv, t, causal, flush=True)
+    d = 256
+    rng = np.random.default_rng(b * hq * t + causal)
+    q, k, v = (rng.standard_normal((b, h, t, d), dtype=np.float32) for h in (hq, hkv, hkv))
+    got = host(nne.attention_forward(dev(q, cuda), dev(k, cuda), dev(v, cuda), causal))
+    assert np.isfinite(got).all()
+    g = hq // hkv
+    for bi in {0, b - 1}:
+        for h in (0, hq - 1):
+            for r0 in (0, t // 2 - 32, t - 64):
+                rows = slice(r0, r0 + 64)
+                ref = T.ref_standard(q[bi:bi + 1, h:h + 1, rows], k[bi:bi + 1, h // g:h // g + 1],
+                                     v[bi:bi + 1, h // g:h // g + 1], causal, start_pos=r0)
+                T.assert_close(got[bi:bi + 1, h:h + 1, rows], ref,
+                               what="wave pair b %d head %d rows %d" % (bi, h, r0))
 
 
 def test_wide_head_dim_strided_views_and_repeat(nne, cuda):
