@@ -38,9 +38,10 @@
 //  output blocks (S from 4 partials, Q^T of its last 8 chunks in LDS), so a
 //  tile's MFMAs per wave double against the same exchange and softmax, and
 //  one workgroup's exchange overlaps the other's MFMAs.
-//  A unit of more than 512 dims takes one workgroup per output chunk, each
-//  recomputing S (at d = 1024 that is 1.5x the algorithmic MFMA work; holding
-//  O^T of 1024 dims instead spilled registers in the loop).  Workgroup ids go
+//  Above 512 dims an unsplit unit takes one 8-wave workgroup per 1024-dim
+//  output chunk (4 output blocks and 16 S chunks per wave, half of its Q^T in
+//  LDS), each chunk recomputing S; key splits keep 512-dim chunks, whose
+//  records the combine kernel merges.  Workgroup ids go
 //  to the 8 XCDs in turn; XCD x takes the x-th eighth of the (sequence, KV
 //  head, unit, chunk) list, so the units of a KV head, which read the same
 //  K/V rows, share an L2, and causal units are taken longest first (on the
@@ -72,26 +73,29 @@ __device__ __forceinline__ int clamp_keys(int64_t x, int tk) {
 // DW waves per workgroup.  Per wave: QC chunks of S (STREAMQ: further chunks
 // read again each tile) and OB output blocks (the workgroup's output chunk is
 // 32 * DW * OB dims).  Q^T of the chunks stays in registers, except that the
-// 4- and 2-wave forms keep their last 8 chunks in LDS.  KP chunks of the next
-// tile's K are loaded during the current tile, and VP key steps of a tile's V
-// at its start; the rest is loaded in groups of 4 inside its phase.  8 waves:
-// one workgroup per CU; 4 waves: two per CU, 2 waves (head dims up to 256):
-// four per CU, whose exchanges and softmaxes interleave with each other's
-// MFMAs.
+// forms with 4 output blocks per wave keep their last 8 chunks in LDS.  KP
+// chunks of the next tile's K are loaded during the current tile, and VP key
+// steps of a tile's V at its start; the rest is loaded in groups of 4 inside
+// its phase.  8 waves: one workgroup per CU (2 output blocks per wave, or 4 on
+// a 1024-dim chunk above 512 dims); 4 waves: two per CU; 2 waves (head dims
+// up to 256): four per CU.  Co-resident workgroups' exchanges and softmaxes
+// interleave with each other's MFMAs.
 template <bool CAUSAL, int DW, int QC, int OB, bool STREAMQ, bool SPLIT>
 __global__ __launch_bounds__(64 * DW, DW == 8 ? 1 : 2) void deep_attention_kernel(const DeepParams p) {
-    static_assert(DW == 8 || ((DW == 4 || DW == 2) && QC == 16 && OB == 4 && !SPLIT && !STREAMQ),
+    static_assert((DW == 8 && OB == 2) || (QC == 16 && OB == 4 && !SPLIT && (DW == 8 || !STREAMQ)),
                   "the workgroup forms");
-    constexpr int KP = DW <= 4 ? 4 : (QC < 8 ? QC : 8);
+    constexpr bool OB4 = OB == 4;
+    constexpr int KP = OB4 ? 4 : (QC < 8 ? QC : 8);
     constexpr int VP = OB <= 2 ? 16 : 4;
-    constexpr int QL = DW <= 4 ? 8 : 0;  // Q^T chunks in LDS (the last QL of QC)
+    constexpr int QL = OB4 ? 8 : 0;  // Q^T chunks in LDS (the last QL of QC)
     constexpr int CB = 32 * DW;          // dims between a wave's output blocks
     __shared__ __attribute__((aligned(16))) float xs[2 * DW * XW];
     __shared__ __attribute__((aligned(16))) float red[2 * XW];
     __shared__ __attribute__((aligned(16))) float qs[QL > 0 ? DW * QL * 256 : 4];
 
-    // Output chunk of one workgroup: kDeepChunk dims (256 on the 2-wave form, unsplit only).
-    static_assert(32 * DW * OB == kDeepChunk || (DW == 2 && !SPLIT), "output chunk of one workgroup");
+    // Output chunk of one workgroup: kDeepChunk dims, or (unsplit forms) 256
+    // on 2 waves and 1024 on 8 waves with 4 blocks each.
+    static_assert(32 * DW * OB == kDeepChunk || !SPLIT, "output chunk of one workgroup");
     // Key-split launches (few units, no K/V sharing between them worth an
     // L2) deal the workgroups round-robin over the XCDs instead, so that the
     // parts of ragged sequences spread over the whole device.
@@ -575,7 +579,7 @@ hipError_t launch_deep_v(DeepParams p, hipStream_t stream) {
                            dim3(8 * p.per_xcd), dim3(64 * DW), 0, stream, p);
         return hipGetLastError();
     }
-    if constexpr (DW == 8) {
+    if constexpr (DW == 8 && OB == 2) {
         hipLaunchKernelGGL((deep_attention_kernel<CAUSAL, DW, QC, OB, STREAMQ, true>), dim3(8 * p.per_xcd),
                            dim3(64 * DW), 0, stream, p);
         hipError_t e = hipGetLastError();
@@ -583,7 +587,7 @@ hipError_t launch_deep_v(DeepParams p, hipStream_t stream) {
         hipLaunchKernelGGL(deep_combine_kernel, dim3((unsigned)base), dim3(256), 0, stream, p);
         return hipGetLastError();
     }
-    return hipErrorInvalidValue;   // (the 4-wave form serves unsplit launches only)
+    return hipErrorInvalidValue;   // (the forms with 4 output blocks serve unsplit launches only)
 }
 
 // Up to 512 dims, problems of full 32-row units with more workgroups than
@@ -603,6 +607,14 @@ hipError_t launch_deep_t(const DeepParams& p, int cus, hipStream_t stream) {
     if (p.d <= 512 && p.n_split == 1 && rows >= 32 && wg > (CAUSAL ? 2 : 1) * (int64_t)cus)
         return launch_deep_v<CAUSAL, 4, 16, 4, false>(p, stream);
     if (p.d <= 512) return launch_deep_v<CAUSAL, 8, 8, 2, false>(p, stream);
+    // Above 512 dims unsplit launches take 1024-dim output chunks (S computed
+    // once per 1024 dims instead of per 512: d = 1024 non-causal B = 1, H = 8,
+    // T = 2048 2.03 -> 1.17 ms, d = 2048 causal B = 1, H = 4, T = 2048 3.80 ->
+    // 2.16 ms); key splits keep 512-dim records.
+    if (p.n_split == 1) {
+        if (p.d <= 1024) return launch_deep_v<CAUSAL, 8, 16, 4, false>(p, stream);
+        return launch_deep_v<CAUSAL, 8, 16, 4, true>(p, stream);
+    }
     if (p.d <= 1024) return launch_deep_v<CAUSAL, 8, 16, 2, false>(p, stream);
     return launch_deep_v<CAUSAL, 8, 16, 2, true>(p, stream);
 }

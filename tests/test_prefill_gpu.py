@@ -358,8 +358,10 @@ def test_head_dims_above_128(nne, cuda, b, hq, hkv, tq, tk, d, causal, q_off):
     (2, 4, 2, 70, 90, 320, True, 20),       # GQA, bottom-right offset
     (1, 2, 1, 40, 64, 384, True, -10),      # rows that see no key
     (2, 8, 2, 8, 300, 512, False, 0),       # 8 queries x G = 4: one unit per KV head
-    (1, 3, 3, 33, 33, 1024, True, 0),       # Q^T of 128 dims per wave in registers
-    (1, 2, 2, 70, 70, 1028, True, 0),       # two output chunks, Q^T beyond 128 dims re-read
+    (1, 3, 3, 33, 33, 1024, True, 0),       # one 1024-dim output chunk on 8 waves
+    (1, 2, 2, 70, 70, 1028, True, 0),       # two output chunks, Q^T beyond 128 dims per wave re-read
+    (2, 8, 8, 300, 300, 768, True, 0),      # 160 units, unsplit, a partial last unit
+    (1, 16, 4, 100, 130, 1024, True, 30),   # GQA above 512 dims, units straddling heads
     (1, 1, 1, 64, 100, 2048, False, 0),
     (3, 5, 5, 100, 37, 768, False, 0),      # Tk < Tq
     (2, 4, 4, 3, 300, 640, True, 297),      # a few rows at the end of a long cache
