@@ -122,9 +122,10 @@ int nne_counters_init(uint32_t *counters, uint64_t n, void *stream);
  * Any head dim; above 128 the tensors must be 16-byte vector views
  * (d % 4 == 0, unit dim stride, other strides multiples of 4, 16-byte
  * aligned) -- NNE_EINVAL otherwise.  Above 256 dims a separate kernel runs
- * (MFMA, K/V read straight into operand layout); problems with too few
- * query rows to fill the device split their keys over several workgroups,
- * with records in the workspace. */
+ * (MFMA, K/V read straight into operand layout), and so do 129-255 dims and
+ * d = 256 problems too small to fill the device on the 256-dim kernel;
+ * problems with too few query rows to fill the device split their keys over
+ * several workgroups, with records in the workspace. */
 int nne_flash_attention_forward(const float *q, const int64_t q_shape[4], const int64_t q_strides[4],
                                 const float *k, const int64_t k_shape[4], const int64_t k_strides[4],
                                 const float *v, const int64_t v_shape[4], const int64_t v_strides[4],
