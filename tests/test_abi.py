@@ -279,6 +279,16 @@ def test_workspace_size_queries(nne):
     assert lib.nne_attention_workspace_size(i64(8, 20, 8, 64), i64(8, 20, 1500, 64), 0, 0,
                                             ctypes.byref(size)) == nne.NNE_OK
     assert size.records_bytes > 0 and size.n_counters >= 8 * 20
+    # 129-256 dims: d = 256 with the device full stays on the wave-pair kernel
+    # (no workspace); a d = 192 prefill of few units takes the deep kernel's
+    # key split: records only (4 heads x 2 units x 8 parts of 32 rows x
+    # (512 + 2) floats, 256 CUs assumed without a device)
+    assert lib.nne_attention_workspace_size(i64(1, 32, 2048, 256), i64(1, 8, 2048, 256), 1, 0,
+                                            ctypes.byref(size)) == nne.NNE_OK
+    assert (size.records_bytes, size.n_counters) == (0, 0)
+    assert lib.nne_attention_workspace_size(i64(1, 4, 64, 192), i64(1, 4, 1500, 192), 0, 0,
+                                            ctypes.byref(size)) == nne.NNE_OK
+    assert (size.records_bytes, size.n_counters) == (8 * 8 * 32 * 514 * 4, 0)
     # shapes the call would refuse
     assert lib.nne_attention_workspace_size(i64(1, 6, 8, 16), i64(1, 4, 8, 16), 1, 0,
                                             ctypes.byref(size)) == nne.NNE_ESHAPE

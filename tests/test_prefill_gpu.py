@@ -417,6 +417,7 @@ def test_deep_four_wave_form(nne, cuda, b, hq, hkv, tq, tk, d, causal, q_off, la
     (2, 4, 4, 8, 3000, 512, False, 0),      # cross-attention: 8 queries, keys split in 8
     (1, 8, 2, 4, 2500, 384, True, 2496),    # 4 new rows at the end of a long cache, G = 4
     (1, 2, 1, 3, 1200, 1028, False, 0),     # two output chunks, each split
+    (1, 4, 4, 64, 1500, 192, False, 0),     # 129-256 dims off the wave-pair kernel: 8 units split
 ])
 def test_deep_key_split(nne, cuda, b, hq, hkv, tq, tk, d, causal, q_off):
     """Problems with too few query rows to fill the device split each unit's
