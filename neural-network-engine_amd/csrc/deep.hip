@@ -1,5 +1,6 @@
 // Attention at head dims above 256: prefill, cross-attention and decode over a
-// KV cache, on v_mfma_f32_32x32x2_f32.
+// KV cache, on v_mfma_f32_32x32x2_f32; and prefill at 129-256 dims that the
+// wave-pair kernel does not take (dims other than 256, small problems).
 //
 // Algorithm: the online softmax of the reference's flash_attention_forward
 // (src/nn/flash_attention.rs:91-195) over 32-key tiles, rows that see no key
@@ -37,7 +38,9 @@
 //  instead, two workgroups per CU: each wave takes twice the chunks and
 //  output blocks (S from 4 partials, Q^T of its last 8 chunks in LDS), so a
 //  tile's MFMAs per wave double against the same exchange and softmax, and
-//  one workgroup's exchange overlaps the other's MFMAs.
+//  one workgroup's exchange overlaps the other's MFMAs.  At 129-256 dims a
+//  2-wave form does the same over a 256-dim output chunk, four workgroups
+//  per CU.
 //  Above 512 dims an unsplit unit takes one 8-wave workgroup per 1024-dim
 //  output chunk (4 output blocks and 16 S chunks per wave, half of its Q^T in
 //  LDS), each chunk recomputing S; key splits keep 512-dim chunks, whose
