@@ -525,8 +525,8 @@ class KVCache:
 
 
 def decode_kernel_fits(batch, num_heads, num_kv_heads, head_dim):
-    """True when the decode step entry point takes this geometry (the library
-    reports a workspace size for it, zero above 256 dims)."""
+    """True when the decode step entry point takes this geometry (the library's
+    decode workspace query accepts it)."""
     size = NneWorkspaceSize()
     return lib().nne_decode_workspace_size(max(int(batch), 1), int(num_heads),
                                            int(num_kv_heads), int(head_dim),
