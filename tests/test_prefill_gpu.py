@@ -398,7 +398,7 @@ def test_deep_four_wave_form(nne, cuda, b, hq, hkv, tq, tk, d, causal, q_off, la
     """Prefill problems of more workgroups than CUs (causal: more than two
     per CU; 257+ and 513+ units on the 256-CU MI355X) run the deep kernel's
     4-wave form: two workgroups per CU, S from 4 partials, half of each
-    wave's Q^T in LDS."""
+    wave's Q^T in LDS.  A second call gives the same bits."""
     print("case deep four-wave", b, hq, hkv, tq, tk, d, causal, q_off, layout, flush=True)
     s = 29 * tq + d
     q, k, v = rnd(s, b, hq, tq, d), rnd(s + 1, b, hkv, tk, d), rnd(s + 2, b, hkv, tk, d)
@@ -407,6 +407,7 @@ def test_deep_four_wave_form(nne, cuda, b, hq, hkv, tq, tk, d, causal, q_off, la
     else:
         qd, kd, vd = (dev(x.transpose(0, 2, 1, 3), cuda).transpose(1, 2) for x in (q, k, v))
     got = host(nne.attention_forward(qd, kd, vd, causal, q_offset=q_off))
+    assert np.array_equal(host(nne.attention_forward(qd, kd, vd, causal, q_offset=q_off)), got)
     r0 = max(0, -q_off) if causal else 0
     assert not got[:, :, :r0].any()
     ref = T.ref_standard(q[:, :, r0:], k, v, causal, start_pos=q_off + r0)
@@ -480,7 +481,8 @@ def test_deep_two_wave_form(nne, cuda, b, hq, hkv, tq, tk, d, causal, q_off, lay
     """Head dims 129-256 that the wave-pair kernel does not take (dims other
     than 256, or too few of its 4-unit items to fill the device) run the deep
     kernel: its 2-wave form, four workgroups per CU (a wave pair per 32-row
-    unit, Q^T half in LDS), or for few units its 8-wave key split."""
+    unit, Q^T half in LDS), or for few units its 8-wave key split.  A second
+    call gives the same bits."""
     print("case deep two-wave", b, hq, hkv, tq, tk, d, causal, q_off, layout, flush=True)
     s = 31 * tq + d
     q, k, v = rnd(s, b, hq, tq, d), rnd(s + 1, b, hkv, tk, d), rnd(s + 2, b, hkv, tk, d)
@@ -489,6 +491,7 @@ def test_deep_two_wave_form(nne, cuda, b, hq, hkv, tq, tk, d, causal, q_off, lay
     else:
         qd, kd, vd = (dev(x.transpose(0, 2, 1, 3), cuda).transpose(1, 2) for x in (q, k, v))
     got = host(nne.attention_forward(qd, kd, vd, causal, q_offset=q_off))
+    assert np.array_equal(host(nne.attention_forward(qd, kd, vd, causal, q_offset=q_off)), got)
     r0 = max(0, -q_off) if causal else 0
     assert not got[:, :, :r0].any()
     ref = T.ref_standard(q[:, :, r0:], k, v, causal, start_pos=q_off + r0)
