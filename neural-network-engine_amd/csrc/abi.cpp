@@ -268,7 +268,11 @@ int run_attention(const float* q, const int64_t* qs_, const int64_t* qst, const 
     // deep kernel's 2-wave form (wide_on_deep), or on the split-K kernel when a
     // KV head has few query rows; above 256 on the deep kernel.
     const bool wide = nne::prefill_padded_dim(d) == 0;
-    const bool deep = wide && (nne::splitk_padded_dim(d) == 0 || wide_on_deep(B, Hkv, Hq / Hkv, Tq, d));
+    // (At 129-256 dims K/V row strides outside the deep kernel's 32-bit tile
+    // offsets keep the wave-pair kernel.)
+    const bool deep_strides = kst[2] >= 0 && vst[2] >= 0 && kst[2] < (1 << 25) && vst[2] < (1 << 25);
+    const bool deep = wide && (nne::splitk_padded_dim(d) == 0 ||
+                               (deep_strides && wide_on_deep(B, Hkv, Hq / Hkv, Tq, d)));
     // Offsets beyond +-2^30 cannot change visibility for int32 lengths.
     const int qoff = (int)std::max<int64_t>(-(1 << 30), std::min<int64_t>(q_offset, 1 << 30));
     const bool vec = d % 4 == 0 && vec_view(q, qst) && vec_view(k, kst) && vec_view(v, vst) &&

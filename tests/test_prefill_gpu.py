@@ -498,6 +498,27 @@ def test_deep_two_wave_form(nne, cuda, b, hq, hkv, tq, tk, d, causal, q_off, lay
     T.assert_close(got[:, :, r0:], ref, what="d=%d two-wave" % d)
 
 
+def test_wide_dims_kv_row_stride_beyond_deep_kernel(nne, cuda):
+    """At 129-256 dims, K/V views whose row stride is beyond the deep kernel's
+    32-bit tile offsets (2^25 floats) stay on the wave-pair kernel."""
+    import torch
+    print("case wide dims huge kv row stride", flush=True)
+    d, tk, tq = 192, 3, 40
+    q, k, v = rnd(71, 1, 1, tq, d), rnd(72, 1, 1, tk, d), rnd(73, 1, 1, tk, d)
+    st = 1 << 25
+    kv_buf = torch.zeros(2, (tk - 1) * st + d, device=cuda)
+    for i in range(tk):
+        kv_buf[0, i * st:i * st + d] = torch.from_numpy(k[0, 0, i])
+        kv_buf[1, i * st:i * st + d] = torch.from_numpy(v[0, 0, i])
+    kd = kv_buf[0].as_strided((1, 1, tk, d), (tk * st, tk * st, st, 1))
+    vd = kv_buf[1].as_strided((1, 1, tk, d), (tk * st, tk * st, st, 1))
+    got = host(nne.attention_forward(dev(q, cuda), kd, vd, True, q_offset=tk - tq))
+    r0 = tq - tk
+    assert not got[:, :, :r0].any()
+    ref = T.ref_standard(q[:, :, r0:], k, v, True, start_pos=0)
+    T.assert_close(got[:, :, r0:], ref, what="d=192 huge row stride")
+
+
 @pytest.mark.parametrize("b,hq,hkv,t,causal", [
     (2, 16, 16, 1024, False),    # 256 items of 4 units: the wave-pair kernel
     (1, 32, 8, 1024, True),      # GQA, 256 items
