@@ -498,6 +498,20 @@ def test_deep_two_wave_form(nne, cuda, b, hq, hkv, tq, tk, d, causal, q_off, lay
     T.assert_close(got[:, :, r0:], ref, what="d=%d two-wave" % d)
 
 
+@pytest.mark.parametrize("d", [192, 256, 512, 1024])
+def test_wide_and_deep_dims_empty_keys(nne, cuda, d):
+    """No keys (Tk = 0) above 128 dims: every row is zero, on the deep
+    kernel's forms as on the others."""
+    import torch
+    print("case empty keys d=%d" % d, flush=True)
+    q = dev(rnd(74, 1, 2, 40, d), cuda)
+    e = torch.zeros(1, 2, 0, d, device=cuda)
+    for causal in (False, True):
+        out = torch.full((1, 2, 40, d), float("nan"), device=cuda)
+        nne.attention_forward(q, e, e, causal, out=out)
+        assert not host(out).any()
+
+
 def test_wide_dims_kv_row_stride_beyond_deep_kernel(nne, cuda):
     """At 129-256 dims, K/V views whose row stride is beyond the deep kernel's
     32-bit tile offsets (2^25 floats) stay on the wave-pair kernel."""
